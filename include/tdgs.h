@@ -1,0 +1,328 @@
+/*
+ * tdgs.h — C-ABI of libtdgs, the MI355X (gfx950) render/train core for 3D Gaussian
+ * Splatting. Every entry point takes plain pointers and sizes; device buffers are owned by
+ * the caller; every call is asynchronous on the given HIP stream unless stated otherwise.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   render!                        src/forward_core.jl:196-314
+ *   fill_keep_gaussians_kernel!    src/forward_core.jl:326-355
+ *   fill_fgidx_to_gidx_kernel!     src/forward_core.jl:371-386   (+ accumulate! at :231)
+ *   project_fgaussians_kernel!     src/forward_core.jl:411-517
+ *   fill_df2dgs_codes_..._kernel!  src/forward_core.jl:531-603   (+ accumulate! at :259)
+ *   sort_pairs / determine_sort_pairs_temp_storage
+ *                                  deps/cub_sort_pairs/cub_sort_pairs_wrapper.cu:31-61,
+ *                                  called from src/forward_core.jl:618-660
+ *   fill_tiles_end_sdfgidx_kernel! src/forward_core.jl:676-734
+ *   render_tiles_kernel!           src/forward_core.jl:756-993
+ *   render_void!                   src/forward_structs.jl:743-757
+ *   backward!                      src/backward_core.jl:37-72
+ *   update! (Adam)                 src/optimizer.jl:964-1009, 1084-1127, 1165-1248
+ *   adaptive_density_control!      src/gaussians.jl:1526-1694, src/optimizer.jl:1304-1378
+ *   maybe_densify_and_prune!       src/training.jl:313-444, 472-580
+ *
+ * Conventions (identical to the reference so results compare bit for bit):
+ *   - Arrays use the reference's Julia column-major layouts: "k x n" means k contiguous
+ *     values per element. Images are 3 x h x w (rgb) and h x w (T, depth, last); pixel
+ *     (row v, column u), 1-based, sits at offset (v-1) + h*(u-1).
+ *   - Index values stored in buffers are 1-based (fgidx_to_gidx, sorted values, tiles_end,
+ *     last contributor; 0 means "none").
+ *   - Keys are (int64(tile) << 32) | int32 bits of the float32 depth; tile = tx + (ty-1)*ntx.
+ *   - Return value: TDGS_OK or an error code; tdgs_last_error() gives the message of the
+ *     last failure on the calling host thread. No exception crosses the ABI.
+ *   - Calls that report a count back to the host (number of filtered Gaussians, number of
+ *     duplicated keys, number of Gaussians after densification) synchronise their stream.
+ */
+#ifndef TDGS_H
+#define TDGS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TDGS_ABI_VERSION 1
+
+enum {
+    TDGS_OK = 0,
+    TDGS_ERR_INVALID = 1,     /* bad argument: null pointer, size, degree, tile shape */
+    TDGS_ERR_CAPACITY = 2,    /* a caller buffer is too small; the *_out count says how big */
+    TDGS_ERR_HIP = 3,         /* a HIP runtime call failed */
+    TDGS_ERR_UNSUPPORTED = 4  /* option combination not implemented */
+};
+
+enum { TDGS_TRAINABLE = 0, TDGS_RENDER_ONLY = 1 };
+enum { TDGS_CLIP_CLAMP = 0, TDGS_CLIP_FILTER = 1 };  /* CovarianceBoundaryClamp / BoundaryFilter */
+
+/* tdgs_render_options.flags */
+#define TDGS_FLAG_EXACT_SH_JACOBIAN 0x1  /* use basis coefficient 16 where src/sh.jl:249 uses 15 */
+
+/* PinholeCamera (src/cameras.jl:50-106): P = K [R^T | -R^T t] cached as 3x4, row-major here. */
+typedef struct tdgs_camera {
+    int32_t width;
+    int32_t height;
+    float P[12];        /* row-major 3x4 projection matrix */
+    float near_z;       /* exclusive */
+    float far_z;        /* inclusive (may be +inf) */
+    float position[3];  /* camera centre (camera-to-world translation) */
+} tdgs_camera;
+
+/* RenderOptions (src/forward_structs.jl:579-665); clip bounds already in pixel units. */
+typedef struct tdgs_render_options {
+    float background[3];
+    float aa_min_factor;
+    float min_alpha;
+    float max_alpha;
+    float min_transmittance;
+    float dilation_x;
+    float dilation_y;
+    float clip_x_min, clip_x_max, clip_y_min, clip_y_max;
+    int32_t sh_degree;   /* degree used for colour; <= the Gaussians' storage degree */
+    int32_t clip_mode;   /* TDGS_CLIP_CLAMP or TDGS_CLIP_FILTER */
+    int32_t antialiasing;
+    int32_t flags;
+} tdgs_render_options;
+
+/* Tiling (src/forward_structs.jl:340-380): ntx = cld(w, tw), nty = cld(h, th). */
+typedef struct tdgs_tiling {
+    int32_t tile_width;
+    int32_t tile_height;
+    int32_t nb_tiles_x;
+    int32_t nb_tiles_y;
+} tdgs_tiling;
+
+/* TrainableGaussiansVector (src/gaussians.jl:29-98) or RenderOnlyGaussiansVector (:342-392). */
+typedef struct tdgs_gaussians {
+    int32_t kind;           /* TDGS_TRAINABLE or TDGS_RENDER_ONLY */
+    int32_t n;
+    int32_t sh_degree;      /* storage degree: (sh_degree+1)^2 coefficients per channel */
+    int32_t reserved;
+    float* means_opacity;   /* 4 x n: [x, y, z, opacity logit] or [x, y, z, opacity] */
+    float* scaling;         /* 3 x n log-scales (trainable) */
+    float* rotation;        /* 4 x n unnormalised quaternions [r, x, y, z] (trainable) */
+    float* covariances;     /* 6 x n lower [V11, V21, V31, V22, V32, V33] (render-only) */
+    float* sh;              /* h x 3 x n, coefficient fastest */
+} tdgs_gaussians;
+
+/* RenderBuffers (src/forward_structs.jl:1541-1677) + Filtered2DGaussiansVector (:762-833). */
+typedef struct tdgs_render_buffers {
+    int32_t capacity;        /* per-Gaussian arrays hold this many entries (>= n) */
+    int32_t reserved;
+    int64_t key_capacity;    /* per-key arrays hold this many entries */
+    uint8_t* keep;           /* capacity; keep flags (written when non-null) */
+    int32_t* fgidx_to_gidx;  /* capacity; 1-based */
+    float* depths;           /* capacity */
+    float* f2d;              /* 9 x capacity: [mu_x, mu_y, a, M11, M21, M22, r, g, b] */
+    int32_t* tile_ranges;    /* 4 x capacity: [tx_min, ty_min, tx_max, ty_max] */
+    int32_t* counts;         /* capacity; overlapped tiles per filtered Gaussian */
+    int64_t* keys;           /* key_capacity; emitted keys (depth order) */
+    int32_t* values;         /* key_capacity */
+    int64_t* sorted_keys;    /* key_capacity */
+    int32_t* sorted_values;  /* key_capacity; sdfgidx_to_fgidx, 1-based */
+    int32_t* tiles_end;      /* nb_tiles; tiles_end_sdfgidx */
+    void* temp;              /* scratch of tdgs_render_temp_bytes() bytes */
+    size_t temp_bytes;
+} tdgs_render_buffers;
+
+/* RenderOutputs (src/forward_structs.jl:1-129); each pointer may be null (not requested). */
+typedef struct tdgs_render_outputs {
+    float* rgb;      /* 3 x h x w */
+    float* T;        /* h x w transmittance */
+    float* depth;    /* h x w */
+    int32_t* last;   /* h x w last contributing sorted index (1-based, 0 = none) */
+} tdgs_render_outputs;
+
+/* FilteredGaussiansGradientsVector (src/backward_structs.jl:1-93). The four 2D gradient
+ * arrays (mean2d 2, opacity 1, inverse covariance lower 3, colour 3) are interleaved per
+ * filtered Gaussian as 9 x capacity; the 3D gradient arrays keep the reference layout. */
+typedef struct tdgs_gradients {
+    int32_t capacity;
+    int32_t sh_degree;          /* storage degree of sh */
+    float* grads2d;             /* 9 x capacity */
+    float* mean3d;              /* 3 x capacity */
+    float* opacity_feature;     /* capacity */
+    float* scaling_features;    /* 3 x capacity */
+    float* rotation_features;   /* 4 x capacity */
+    float* sh;                  /* h x 3 x capacity */
+} tdgs_gradients;
+
+/* GaussianAdamMomentsLearningRatesVector + AdamOptimizer (src/optimizer.jl:9-195, 761-854). */
+typedef struct tdgs_adam_state {
+    float* means_moments;       /* 2 x 3 x n (m1, m2 interleaved) */
+    float* opacity_moments;     /* 2 x n */
+    float* scaling_moments;     /* 2 x 3 x n */
+    float* rotation_moments;    /* 2 x 4 x n */
+    float* sh_moments;          /* 2 x h x 3 x n */
+    float lr_means, lr_opacity, lr_scaling, lr_rotation, lr_sh_dc, lr_sh_rest;
+    float beta1, beta2, epsilon;
+    int32_t update_count;       /* incremented by tdgs_adam_step */
+} tdgs_adam_state;
+
+/* AdaptiveDensityControlBuffers (src/training_structs.jl:265-331). */
+typedef struct tdgs_adc_buffers {
+    int32_t capacity;           /* per-Gaussian arrays (>= n) */
+    int32_t new_capacity;       /* ngidx_to_gidx capacity */
+    float* accum_grad_norms;    /* capacity; accumulated mean2d grad norms (NDC) */
+    int32_t* contribution_counts; /* capacity */
+    uint8_t* prune;             /* capacity */
+    uint8_t* densify;           /* capacity */
+    uint8_t* clone;             /* capacity */
+    int32_t* new_counts_cs;     /* capacity; inclusive scan of (!prune + densify) */
+    int32_t* ngidx_to_gidx;     /* new_capacity; 1-based */
+    void* temp;                 /* scratch of tdgs_scan_temp_bytes(capacity) bytes */
+    size_t temp_bytes;
+} tdgs_adc_buffers;
+
+typedef struct tdgs_ctx tdgs_ctx;
+
+/* ---- context, errors, device memory plumbing --------------------------------------- */
+int tdgs_abi_version(void);
+const char* tdgs_last_error(void);
+int tdgs_ctx_create(int device, tdgs_ctx** ctx_out);
+int tdgs_ctx_destroy(tdgs_ctx* ctx);
+int tdgs_malloc(void** ptr_out, size_t bytes);
+int tdgs_free(void* ptr);
+int tdgs_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int tdgs_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int tdgs_memset(void* dst, int value, size_t bytes, void* stream);
+int tdgs_stream_synchronize(void* stream);
+
+/* ---- forward building blocks (each replaces one reference kernel) ------------------- */
+
+/* fill_keep_gaussians_kernel! (forward_core.jl:326-355): keep[g] = culling test. */
+int tdgs_fill_keep(void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
+                   const tdgs_render_options* opt, uint8_t* keep);
+
+/* Scratch bytes for the device-wide scans used by the calls below (n elements). */
+size_t tdgs_scan_temp_bytes(int64_t n);
+
+/* accumulate!(+) + fill_fgidx_to_gidx_kernel! (forward_core.jl:231-244, 371-386):
+ * keep_cs = inclusive scan of keep; fgidx_to_gidx[keep_cs[g]] = g for kept g (1-based).
+ * keep_cs may be null. Synchronises to return the number of kept Gaussians. */
+int tdgs_fill_fgidx_to_gidx(tdgs_ctx* ctx, void* stream, const uint8_t* keep, int32_t n,
+                            int32_t* keep_cs, int32_t* fgidx_to_gidx, void* temp,
+                            size_t temp_bytes, int32_t* nb_fgaussians_out);
+
+/* accumulate!(+) of overlapped-tile counts (forward_core.jl:259-264): inclusive scan.
+ * Synchronises to return the total (M); fails with TDGS_ERR_CAPACITY if M >= 2^31. */
+int tdgs_scan_counts(tdgs_ctx* ctx, void* stream, const int32_t* counts, int32_t n,
+                     int32_t* counts_cs, void* temp, size_t temp_bytes, int64_t* total_out);
+
+/* fill_df2dgs_codes_and_dfgidx_to_fgidx_kernel! (forward_core.jl:531-603). */
+int tdgs_emit_keys(void* stream, int32_t nb_fgaussians, const float* depths,
+                   const int32_t* tile_ranges, const int32_t* counts_cs,
+                   const tdgs_tiling* tiling, int64_t* keys, int32_t* values);
+
+/* determine_sort_pairs_temp_storage / sort_pairs (cub_sort_pairs_wrapper.cu:31-61):
+ * stable LSD radix sort of (int64 key, int32 value) pairs on key bits [0, end_bit).
+ * Same argument order as the CUB wrapper, plus a stream. */
+size_t tdgs_sort_pairs_temp_bytes(int32_t n, int32_t end_bit);
+int tdgs_sort_pairs(void* temp, size_t temp_bytes, const int64_t* keys_in, int64_t* keys_out,
+                    const int32_t* values_in, int32_t* values_out, int32_t n, int32_t end_bit,
+                    void* stream);
+
+/* fill_tiles_end_sdfgidx_kernel! (forward_core.jl:676-734). */
+int tdgs_tile_ranges(void* stream, int64_t nb_keys, const int64_t* sorted_keys,
+                     int32_t nb_tiles, int32_t* tiles_end);
+
+/* render_tiles_kernel! (forward_core.jl:756-993) on already sorted lists; render_void!
+ * semantics are not applied here. */
+int tdgs_render_tiles(void* stream, const tdgs_camera* cam, const tdgs_tiling* tiling,
+                      const tdgs_render_options* opt, const tdgs_render_buffers* buf,
+                      const tdgs_render_outputs* out);
+
+/* ---- forward: render! --------------------------------------------------------------- */
+
+/* Scratch for tdgs_render with the given capacities. */
+size_t tdgs_render_temp_bytes(int32_t capacity, int64_t key_capacity, const tdgs_tiling* tiling);
+
+/* render! GPU (forward_core.jl:196-314): cull, compact, project, duplicate, sort, ranges,
+ * raster. Synchronises once to learn the filtered count and the key count. When the key
+ * count exceeds buf->key_capacity it returns TDGS_ERR_CAPACITY with *nb_keys_out set and
+ * leaves the outputs untouched; grow the key arrays (and temp) and call again. */
+int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
+                const tdgs_tiling* tiling, const tdgs_render_options* opt,
+                tdgs_render_buffers* buf, const tdgs_render_outputs* out,
+                int32_t* nb_fgaussians_out, int64_t* nb_keys_out);
+
+/* ---- backward: backward! -------------------------------------------------------------- */
+
+/* backward! (backward_core.jl:37-72): zero the 2D gradients, replay the tiles back to
+ * front, then the backward projection to 3D gradients. Uses the buffers of the preceding
+ * tdgs_render call with the same arguments; out must hold T and last. */
+int tdgs_backward(void* stream, tdgs_gradients* grads, const float* rgb_grad,
+                  const tdgs_render_outputs* out, const tdgs_gaussians* g,
+                  const tdgs_camera* cam, const tdgs_tiling* tiling,
+                  const tdgs_render_options* opt, const tdgs_render_buffers* buf,
+                  int32_t nb_fgaussians);
+
+/* The two halves of tdgs_backward (backward_core.jl:96-293 and :309-452). The first
+ * accumulates into grads->grads2d without zeroing it. */
+int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float* rgb_grad,
+                               const tdgs_render_outputs* out, const tdgs_camera* cam,
+                               const tdgs_tiling* tiling, const tdgs_render_options* opt,
+                               const tdgs_render_buffers* buf);
+int tdgs_backward_project(void* stream, tdgs_gradients* grads, const tdgs_gaussians* g,
+                          const tdgs_camera* cam, const tdgs_render_options* opt,
+                          const tdgs_render_buffers* buf, int32_t nb_fgaussians);
+
+/* ---- optimiser: update! -------------------------------------------------------------- */
+
+/* update!(opt, fgradients, Val(sh_degree)) (optimizer.jl:964-1009): sparse Adam over the
+ * filtered Gaussians (fgidx_to_gidx[f] <= 0 is skipped), all components in one launch;
+ * increments st->update_count. */
+int tdgs_adam_step(void* stream, tdgs_gaussians* g, tdgs_adam_state* st,
+                   const tdgs_gradients* grads, const int32_t* fgidx_to_gidx,
+                   int32_t nb_fgaussians, int32_t sh_degree);
+
+/* ---- adaptive density control -------------------------------------------------------- */
+
+/* update_adc_stats_kernel! (training.jl:472-497). */
+int tdgs_adc_stats(void* stream, tdgs_adc_buffers* adc, const tdgs_gradients* grads,
+                   const int32_t* fgidx_to_gidx, int32_t nb_fgaussians, int32_t width,
+                   int32_t height);
+
+/* Masks, counts, scan and ngidx_to_gidx (training.jl:325-397). Thresholds are in feature
+ * space: prune if logit < prune_logit or (use_max_scale and max log-scale > log_max_scale);
+ * densify if not pruned and average grad >= grad_threshold; clone if densify and max
+ * log-scale <= log_size_threshold. Synchronises to return the new Gaussian count. Fails
+ * with TDGS_ERR_CAPACITY (count in *n_new_out) if adc->new_capacity is too small. */
+int tdgs_adc_plan(tdgs_ctx* ctx, void* stream, tdgs_adc_buffers* adc, const tdgs_gaussians* g,
+                  float prune_logit, int32_t use_max_scale, float log_max_scale,
+                  float grad_threshold, float log_size_threshold, int32_t* n_new_out);
+
+/* adaptive_density_control! for parameters (gaussians.jl:1526-1694) and Adam moments
+ * (optimizer.jl:1304-1378): fills dst (n_new Gaussians; new moments must be zeroed by the
+ * caller beforehand or pass zero_moments = 1). Split means use a counter-based normal RNG
+ * keyed by (seed, old index, draw). */
+int tdgs_adc_apply(void* stream, const tdgs_adc_buffers* adc, const tdgs_gaussians* src,
+                   tdgs_gaussians* dst, const tdgs_adam_state* src_m, tdgs_adam_state* dst_m,
+                   float log_split_factor, uint64_t seed, int32_t zero_moments);
+
+/* adjust_fgidx_to_gidx_adc_kernel! (training.jl:514-541). */
+int tdgs_adc_remap_fgidx(void* stream, const tdgs_adc_buffers* adc, int32_t* fgidx_to_gidx,
+                         int32_t nb_fgaussians);
+
+/* Reset the ADC statistics (set_nb_gaussians!, training_structs.jl). */
+int tdgs_adc_reset_stats(void* stream, tdgs_adc_buffers* adc, int32_t n);
+
+/* ---- training helpers ------------------------------------------------------------------ */
+
+/* L1 part of the loss and its gradient (training.jl:206-215):
+ * grad = (rendered > gt ? w : -w) + dssim_weight * grad_in (grad_in may be null),
+ * w = l1_weight / count. Writes sum |rendered - gt| into *l1_sum_dev (device float, may be
+ * null). */
+int tdgs_l1_loss_grad(void* stream, const float* rendered, const float* gt, int64_t count,
+                      float l1_weight, float dssim_weight, const float* dssim_grad,
+                      float* grad_out, float* l1_sum_dev);
+
+/* reset_opacities! (gaussians.jl:1093-1101) + zero opacity moments (optimizer.jl:754-756). */
+int tdgs_opacity_reset(void* stream, tdgs_gaussians* g, float max_logit,
+                       float* opacity_moments);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TDGS_H */

@@ -1,0 +1,282 @@
+"""ctypes wrapper of the CPU oracle (oracle/liboracle.so). TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this module; it is
+the checker, never the measured or shipped path. Arrays are numpy arrays in the reference's
+memory layouts (see threedgaussiansplatting.jl_amd/host.py): per-Gaussian k x n Julia arrays
+are (n, k) C-order arrays here, images 3 x h x w are (w, h, 3).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+
+def _abi():
+    import importlib
+    return importlib.import_module(__package_root__() + ".abi")
+
+
+def __package_root__():
+    import sys
+    for name in ("tdgs_amd",):
+        if name in sys.modules:
+            return name
+    raise RuntimeError("load the package first (__graft_entry__.load_package())")
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            from . import build as _b  # type: ignore
+            _b.build()
+        _LIB = C.CDLL(path)
+        _LIB.oracle_fill_fgidx_to_gidx.restype = C.c_int32
+        _LIB.oracle_scan_counts.restype = C.c_int64
+        _LIB.oracle_render.restype = C.c_int64
+        _LIB.oracle_adc_plan.restype = C.c_int32
+        _LIB.oracle_l1_loss_grad.restype = C.c_double
+        for fn in ("oracle_exp", "oracle_log", "oracle_sigmoid"):
+            getattr(_LIB, fn).restype = C.c_float
+            getattr(_LIB, fn).argtypes = [C.c_float]
+        _LIB.oracle_normal_pair.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32, C.c_void_p]
+        _LIB.oracle_sort_pairs.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                           C.c_int64, C.c_int32]
+        _LIB.oracle_tile_ranges.argtypes = [C.c_int64, C.c_void_p, C.c_int32, C.c_void_p]
+    return _LIB
+
+
+def ptr(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def gaussians_struct(g):
+    abi = _abi()
+    s = abi.Gaussians()
+    s.kind = abi.TDGS_TRAINABLE
+    s.n = g.n
+    s.sh_degree = g.sh_degree
+    s.means_opacity = g.means_opacity.ctypes.data
+    s.scaling = g.scaling.ctypes.data
+    s.rotation = g.rotation.ctypes.data
+    s.covariances = None
+    s.sh = g.sh.ctypes.data
+    return s
+
+
+def render(g, cam, tiling, opts, *, rgb=True, T=True, depth=True, last=True):
+    """render! (forward_core.jl:196-314) on the CPU; returns a dict of every intermediate."""
+    abi = _abi()
+    L = lib()
+    n = g.n
+    W, H = cam.width, cam.height
+    gs = gaussians_struct(g)
+    c_cam = cam.to_c()
+    c_t = tiling.to_c()
+    c_o = opts.to_c()
+    res = {
+        "keep": np.zeros(n, np.uint8),
+        "fgidx_to_gidx": np.zeros(n, np.int32),
+        "depths": np.zeros(n, np.float32),
+        "f2d": np.zeros((n, 9), np.float32),
+        "tile_ranges": np.zeros((n, 4), np.int32),
+        "counts": np.zeros(n, np.int32),
+        "tiles_end": np.zeros(tiling.nb_tiles, np.int32),
+    }
+    out = {
+        "rgb": np.zeros((W, H, 3), np.float32) if rgb else None,
+        "T": np.zeros((W, H), np.float32) if T else None,
+        "depth": np.zeros((W, H), np.float32) if depth else None,
+        "last": np.zeros((W, H), np.int32) if last else None,
+    }
+    b = abi.RenderBuffersC()
+    b.capacity = n
+    b.key_capacity = 0
+    b.keep = res["keep"].ctypes.data
+    b.fgidx_to_gidx = res["fgidx_to_gidx"].ctypes.data
+    b.depths = res["depths"].ctypes.data
+    b.f2d = res["f2d"].ctypes.data
+    b.tile_ranges = res["tile_ranges"].ctypes.data
+    b.counts = res["counts"].ctypes.data
+    b.tiles_end = res["tiles_end"].ctypes.data
+    o = abi.RenderOutputsC(*(None if out[k] is None else out[k].ctypes.data
+                             for k in ("rgb", "T", "depth", "last")))
+    nbf = C.c_int32(0)
+    m = L.oracle_render(C.byref(gs), C.byref(c_cam), C.byref(c_t), C.byref(c_o), C.byref(b),
+                        C.byref(o), C.byref(nbf))
+    if m > 0:
+        for k, dt in (("keys", np.int64), ("values", np.int32), ("sorted_keys", np.int64),
+                      ("sorted_values", np.int32)):
+            res[k] = np.zeros(m, dt)
+        b.key_capacity = m
+        b.keys = res["keys"].ctypes.data
+        b.values = res["values"].ctypes.data
+        b.sorted_keys = res["sorted_keys"].ctypes.data
+        b.sorted_values = res["sorted_values"].ctypes.data
+        m2 = L.oracle_render(C.byref(gs), C.byref(c_cam), C.byref(c_t), C.byref(c_o), C.byref(b),
+                             C.byref(o), C.byref(nbf))
+        assert m2 == m
+    res["nb_fgaussians"] = int(nbf.value)
+    res["nb_keys"] = int(m)
+    res.update(out)
+    return res
+
+
+def fill_fgidx_to_gidx(keep):
+    keep = np.ascontiguousarray(keep, dtype=np.uint8)
+    n = keep.size
+    cs = np.zeros(n, np.int32)
+    f2g = np.zeros(n, np.int32)
+    nf = lib().oracle_fill_fgidx_to_gidx(ptr(keep), C.c_int32(n), ptr(cs), ptr(f2g))
+    return cs, f2g[:nf], nf
+
+
+def emit_keys(depths, tile_ranges, counts, tiling):
+    counts = np.ascontiguousarray(counts, dtype=np.int32)
+    nf = counts.size
+    cs = np.zeros(nf, np.int32)
+    m = lib().oracle_scan_counts(ptr(counts), C.c_int32(nf), ptr(cs))
+    keys = np.zeros(m, np.int64)
+    vals = np.zeros(m, np.int32)
+    c_t = tiling.to_c()
+    lib().oracle_emit_keys(C.c_int32(nf), ptr(np.ascontiguousarray(depths, np.float32)),
+                           ptr(np.ascontiguousarray(tile_ranges, np.int32)), ptr(cs),
+                           C.byref(c_t), ptr(keys), ptr(vals))
+    return cs, keys, vals
+
+
+def sort_pairs(keys, values, end_bit):
+    keys = np.ascontiguousarray(keys, np.int64)
+    values = np.ascontiguousarray(values, np.int32)
+    ko = np.zeros_like(keys)
+    vo = np.zeros_like(values)
+    lib().oracle_sort_pairs(ptr(keys), ptr(ko), ptr(values), ptr(vo), keys.size, end_bit)
+    return ko, vo
+
+
+def tile_ranges(sorted_keys, nb_tiles):
+    te = np.zeros(nb_tiles, np.int32)
+    sk = np.ascontiguousarray(sorted_keys, np.int64)
+    lib().oracle_tile_ranges(sk.size, ptr(sk), nb_tiles, ptr(te))
+    return te
+
+
+def backward(g, cam, tiling, opts, fwd, rgb_grad):
+    """backward! (backward_core.jl:37-72) on the CPU from the intermediates of render()."""
+    abi = _abi()
+    L = lib()
+    nf = fwd["nb_fgaussians"]
+    hg = (g.sh_degree + 1) ** 2
+    acc = np.zeros((max(nf, 1), 9), np.float64)
+    c_cam, c_t, c_o = cam.to_c(), tiling.to_c(), opts.to_c()
+    if fwd["nb_keys"] > 0:
+        L.oracle_backward_render_tiles(C.byref(c_cam), C.byref(c_t), C.byref(c_o), ptr(fwd["f2d"]),
+                                       ptr(fwd["sorted_values"]), ptr(fwd["tiles_end"]),
+                                       ptr(np.ascontiguousarray(rgb_grad, np.float32)),
+                                       ptr(fwd["T"]), ptr(fwd["last"]), ptr(acc))
+    grads2d = acc.astype(np.float32)
+    out = {
+        "grads2d": grads2d[:nf],
+        "mean3d": np.zeros((nf, 3), np.float32),
+        "opacity_feature": np.zeros(nf, np.float32),
+        "scaling_features": np.zeros((nf, 3), np.float32),
+        "rotation_features": np.zeros((nf, 4), np.float32),
+        "sh": np.zeros((nf, 3, hg), np.float32),
+    }
+    gr = abi.GradientsC()
+    gr.capacity = nf
+    gr.sh_degree = g.sh_degree
+    for k in ("mean3d", "opacity_feature", "scaling_features", "rotation_features", "sh"):
+        setattr(gr, k, out[k].ctypes.data if nf > 0 else None)
+    if nf > 0:
+        L.oracle_backward_project(C.byref(gaussians_struct(g)), C.byref(c_cam), C.byref(c_o),
+                                  C.c_int32(nf), ptr(fwd["fgidx_to_gidx"]), ptr(fwd["f2d"]),
+                                  ptr(fwd["counts"]), ptr(grads2d), C.byref(gr))
+    return out
+
+
+class AdamHost:
+    """Adam moments + learning rates (optimizer.jl:9-195) as host arrays."""
+
+    def __init__(self, n, sh_degree, lrs, beta1=0.9, beta2=0.999, epsilon=1e-15, update_count=0):
+        h = (sh_degree + 1) ** 2
+        self.means = np.zeros((n, 3, 2), np.float32)
+        self.opacity = np.zeros((n, 2), np.float32)
+        self.scaling = np.zeros((n, 3, 2), np.float32)
+        self.rotation = np.zeros((n, 4, 2), np.float32)
+        self.sh = np.zeros((n, 3, h, 2), np.float32)
+        self.lrs = list(lrs)
+        self.beta1, self.beta2, self.epsilon = beta1, beta2, epsilon
+        self.update_count = update_count
+
+    def struct(self):
+        abi = _abi()
+        s = abi.AdamStateC()
+        s.means_moments = self.means.ctypes.data
+        s.opacity_moments = self.opacity.ctypes.data
+        s.scaling_moments = self.scaling.ctypes.data
+        s.rotation_moments = self.rotation.ctypes.data
+        s.sh_moments = self.sh.ctypes.data
+        (s.lr_means, s.lr_opacity, s.lr_scaling, s.lr_rotation, s.lr_sh_dc,
+         s.lr_sh_rest) = [float(v) for v in self.lrs]
+        s.beta1, s.beta2, s.epsilon = float(self.beta1), float(self.beta2), float(self.epsilon)
+        s.update_count = int(self.update_count)
+        return s
+
+
+def adam_step(g, adam: AdamHost, grads, fgidx_to_gidx, sh_degree):
+    abi = _abi()
+    nf = len(fgidx_to_gidx)
+    gr = abi.GradientsC()
+    gr.capacity = nf
+    gr.sh_degree = (grads["sh"].shape[2] ** 0.5) - 1 if False else int(round(grads["sh"].shape[2] ** 0.5)) - 1
+    for k in ("mean3d", "opacity_feature", "scaling_features", "rotation_features", "sh"):
+        grads[k] = np.ascontiguousarray(grads[k], np.float32)
+        setattr(gr, k, grads[k].ctypes.data)
+    st = adam.struct()
+    f2g = np.ascontiguousarray(fgidx_to_gidx, np.int32)
+    lib().oracle_adam_step(C.byref(gaussians_struct(g)), C.byref(st), C.byref(gr), ptr(f2g),
+                           C.c_int32(nf), C.c_int32(sh_degree))
+    adam.update_count = st.update_count
+
+
+def cpu_render_reference(g, cam, opts, threads=1):
+    """render! for CPU arrays (forward_core.jl:25-177): the reference's own CPU renderer."""
+    W, H = cam.width, cam.height
+    rgb = np.zeros((W, H, 3), np.float32)
+    T = np.zeros((W, H), np.float32)
+    c_cam, c_o = cam.to_c(), opts.to_c()
+    lib().cpu_render_reference(C.byref(gaussians_struct(g)), C.byref(c_cam), C.byref(c_o),
+                               C.c_int32(threads), ptr(rgb), ptr(T))
+    return rgb, T
+
+
+def exp(x):
+    return lib().oracle_exp(float(x))
+
+
+def log(x):
+    return lib().oracle_log(float(x))
+
+
+def sigmoid(x):
+    return lib().oracle_sigmoid(float(x))
+
+
+def quat_to_rot(q):
+    q = np.ascontiguousarray(q, np.float32)
+    R = np.zeros(9, np.float32)
+    lib().oracle_quat_to_rot(ptr(q), ptr(R))
+    return R.reshape(3, 3)
+
+
+def normal_pair(seed, stream, pair):
+    out = np.zeros(2, np.float32)
+    lib().oracle_normal_pair(seed, stream, pair, ptr(out))
+    return out

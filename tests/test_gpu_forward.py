@@ -1,0 +1,129 @@
+"""GPU parity of the forward path (render!) against the CPU oracle, through the C-ABI.
+
+Integer outputs (compaction, tile rectangles, counts, sorted keys and lists, tile ranges,
+last contributors) and, because the kernels run the oracle's exact single-precision
+operation sequence, the images themselves must match bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from tdgs_amd import host, synthetic
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu_render(core, g_host, cam, t, opts, depth=True):
+    g = core.TrainableGaussiansVector.from_host(g_host, 0)
+    out = core.RenderOutputs.for_camera(cam, 0, include_depth=depth)
+    buf = core.RenderBuffers(len(g), t, 0, keep_flags=True)
+    core.render_(out, g, cam, t, opts, buf)
+    torch.cuda.synchronize()
+    return out, buf
+
+
+def _assert_forward_equal(orc_r, out, buf):
+    nf, m = orc_r["nb_fgaussians"], orc_r["nb_keys"]
+    assert buf.nb_fgaussians == nf
+    assert buf.nb_keys == m
+    np.testing.assert_array_equal(buf.keep.cpu().numpy()[: len(orc_r["keep"])], orc_r["keep"])
+    np.testing.assert_array_equal(buf.fgidx_to_gidx[:nf].cpu().numpy(), orc_r["fgidx_to_gidx"][:nf])
+    counts = buf.counts[:nf].cpu().numpy()
+    np.testing.assert_array_equal(counts, orc_r["counts"][:nf])
+    ne = counts > 0
+    np.testing.assert_array_equal(buf.tile_ranges[:nf].cpu().numpy()[ne], orc_r["tile_ranges"][:nf][ne])
+    np.testing.assert_array_equal(buf.depths[:nf].cpu().numpy()[ne], orc_r["depths"][:nf][ne])
+    np.testing.assert_array_equal(buf.f2d[:nf].cpu().numpy()[ne], orc_r["f2d"][:nf][ne])
+    if m > 0:
+        np.testing.assert_array_equal(buf.sorted_keys[:m].cpu().numpy(), orc_r["sorted_keys"])
+        np.testing.assert_array_equal(buf.sorted_values[:m].cpu().numpy(), orc_r["sorted_values"])
+        np.testing.assert_array_equal(buf.tiles_end.cpu().numpy(), orc_r["tiles_end"])
+    np.testing.assert_array_equal(out.last.cpu().numpy(), orc_r["last"])
+    np.testing.assert_array_equal(out.T.cpu().numpy(), orc_r["T"])
+    np.testing.assert_array_equal(out.rgb.cpu().numpy(), orc_r["rgb"])
+    if out.depth is not None:
+        np.testing.assert_array_equal(out.depth.cpu().numpy(), orc_r["depth"])
+
+
+def test_render_helpers_known_answers(gpu):
+    gold = golden("render_helpers.json")
+    dev = torch.device("cuda", 0)
+    cs, f2g, nf = gpu.fill_fgidx_to_gidx(torch.tensor(gold["keep"], dtype=torch.uint8, device=dev))
+    assert nf == 3 and f2g.cpu().tolist() == gold["fgidx_to_gidx"]
+    t = host.Tiling.for_screen(2, 2, 1, 1)
+    counts = torch.tensor(gold["counts"], dtype=torch.int32, device=dev)
+    ccs, m = gpu.scan_counts(counts)
+    assert m == 6
+    keys, vals = gpu.emit_keys(torch.tensor(gold["depths"], dtype=torch.float32, device=dev),
+                               torch.tensor(gold["tile_ranges"], dtype=torch.int32, device=dev), ccs, m, t)
+    assert vals.cpu().tolist() == gold["dfgidx_to_fgidx"]
+    sk, sv = gpu.sort_pairs(keys, vals, t.end_bit())
+    assert sv.cpu().tolist() == gold["sdfgidx_to_fgidx"]
+    te = gpu.tile_ranges(sk, t.nb_tiles)
+    assert te.cpu().tolist() == gold["tiles_end"]
+
+
+@pytest.mark.parametrize("n,end_bit,spread", [(1, 41, 4), (1000, 41, 8), (4097, 45, 16), (100_000, 45, 64),
+                                              (300_000, 64, 1 << 40), (70_000, 20, 1000)])
+def test_sort_pairs_matches_stable_sort(gpu, oracle, n, end_bit, spread):
+    rng = np.random.default_rng(n + end_bit)
+    hi = rng.integers(0, spread, size=n).astype(np.int64)
+    lo = rng.integers(0, 1 << 31, size=n).astype(np.int64) & ~np.int64(0xFF)  # many ties
+    keys = (hi << 32) | lo if end_bit > 32 else hi
+    vals = np.arange(1, n + 1, dtype=np.int32)
+    ko, vo = oracle.sort_pairs(keys, vals, end_bit)
+    dev = torch.device("cuda", 0)
+    gk, gv = gpu.sort_pairs(torch.from_numpy(keys).to(dev), torch.from_numpy(vals).to(dev), end_bit)
+    np.testing.assert_array_equal(gk.cpu().numpy(), ko)
+    np.testing.assert_array_equal(gv.cpu().numpy(), vo)
+
+
+@pytest.mark.parametrize("deg", [0, 1, 2, 3])
+def test_render_test_scene_bit_exact(gpu, oracle, deg):
+    g, cams = host.create_test_scene(sh_degree=deg)
+    cam = cams[0]
+    opts = host.RenderOptions.for_camera(cam, deg)
+    t = host.Tiling.for_camera(cam, 16, 16)
+    r = oracle.render(g, cam, t, opts)
+    out, buf = _gpu_render(gpu, g, cam, t, opts)
+    _assert_forward_equal(r, out, buf)
+
+
+@pytest.mark.parametrize("cfg,n,tile", [(0, None, (16, 16)), (1, 20_000, (16, 16)), (2, 60_000, (16, 16)),
+                                        (2, 60_000, (16, 32))])
+def test_render_synthetic_bit_exact(gpu, oracle, cfg, n, tile):
+    w = synthetic.config(cfg, n=n, cameras=3)
+    cam = w.cameras[min(1, len(w.cameras) - 1)]
+    t = host.Tiling.for_camera(cam, *tile)
+    opts = host.RenderOptions.for_camera(cam, w.gaussians.sh_degree, background_color=(0.1, 0.2, 0.3))
+    r = oracle.render(w.gaussians, cam, t, opts)
+    out, buf = _gpu_render(gpu, w.gaussians, cam, t, opts)
+    assert r["nb_keys"] > 1000
+    _assert_forward_equal(r, out, buf)
+
+
+def test_render_filter_mode_and_antialiasing(gpu, oracle):
+    w = synthetic.config(0, n=5000)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    from tdgs_amd import abi
+    opts = host.RenderOptions.for_camera(cam, 0, clip_mode=abi.TDGS_CLIP_FILTER, use_antialiasing=True)
+    r = oracle.render(w.gaussians, cam, t, opts)
+    out, buf = _gpu_render(gpu, w.gaussians, cam, t, opts)
+    _assert_forward_equal(r, out, buf)
+
+
+def test_render_void_when_nothing_visible(gpu, oracle):
+    g, cams = host.create_test_scene(sh_degree=0)
+    g.means_opacity[:, 2] = -5.0  # everything behind the camera
+    cam = cams[0]
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.25, 0.5, 0.75))
+    t = host.Tiling.for_camera(cam, 16, 16)
+    out, buf = _gpu_render(gpu, g, cam, t, opts)
+    assert buf.nb_fgaussians == 0
+    rgb = out.rgb.cpu().numpy()
+    np.testing.assert_array_equal(rgb[..., 0], 0.25)
+    np.testing.assert_array_equal(rgb[..., 2], 0.75)
+    assert np.all(out.T.cpu().numpy() == 1) and np.all(out.last.cpu().numpy() == 0)
+    assert np.all(np.isinf(out.depth.cpu().numpy()))

@@ -1,0 +1,346 @@
+"""Host-side mirror of the reference's render/train entry points over libtdgs.so.
+
+Device memory is torch tensors (plumbing only); every computation runs in the HIP kernels
+of libtdgs.so through its C-ABI (include/tdgs.h). There is no CPU or torch fallback: if the
+library is missing or fails to load, the calls raise.
+
+Layouts follow the reference (Julia column-major): a k x n reference array is a (n, k)
+contiguous tensor here, sh (h, 3, n) is (n, 3, h), rgb images 3 x h x w are (w, h, 3) and
+h x w images are (w, h).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import abi
+from .host import HostGaussians, PinholeCamera, RenderOptions, Tiling
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtdgs.so")
+
+
+class TdgsError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"libtdgs error {code}: {msg}")
+        self.code = code
+
+
+class CapacityError(TdgsError):
+    pass
+
+
+_LIB = None
+
+
+def lib():
+    """Load libtdgs.so; raises if it is not built (build with __graft_entry__.build())."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        L = C.CDLL(LIB_PATH)
+        L.tdgs_last_error.restype = C.c_char_p
+        for name in ("tdgs_scan_temp_bytes", "tdgs_sort_pairs_temp_bytes", "tdgs_render_temp_bytes"):
+            getattr(L, name).restype = C.c_size_t
+        L.tdgs_scan_temp_bytes.argtypes = [C.c_int64]
+        L.tdgs_sort_pairs_temp_bytes.argtypes = [C.c_int32, C.c_int32]
+        L.tdgs_render_temp_bytes.argtypes = [C.c_int32, C.c_int64, C.c_void_p]
+        L.tdgs_sort_pairs.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]
+        L.tdgs_tile_ranges.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_int32, C.c_void_p]
+        L.tdgs_fill_fgidx_to_gidx.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                              C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.tdgs_scan_counts.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                       C.c_void_p, C.c_size_t, C.c_void_p]
+        L.tdgs_emit_keys.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_void_p, C.c_void_p, C.c_void_p]
+        _LIB = L
+    return _LIB
+
+
+def check(rc):
+    if rc != abi.TDGS_OK:
+        msg = lib().tdgs_last_error().decode(errors="replace")
+        cls = CapacityError if rc == abi.TDGS_ERR_CAPACITY else TdgsError
+        raise cls(rc, msg)
+
+
+def stream_ptr(device=None):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dptr(t):
+    return None if t is None else t.data_ptr()
+
+
+_CTX = {}
+
+
+def context(device=0):
+    """Per-device library context (pinned readback buffer + device counters)."""
+    device = int(device)
+    if device not in _CTX:
+        h = C.c_void_p()
+        check(lib().tdgs_ctx_create(device, C.byref(h)))
+        _CTX[device] = h
+    return _CTX[device]
+
+
+def _dev(device):
+    return torch.device("cuda", int(device))
+
+
+# ------------------------------------------------------------------------------------
+# Containers
+# ------------------------------------------------------------------------------------
+
+class TrainableGaussiansVector:
+    """MutableTrainableGaussiansVector (src/gaussians.jl:29-98) in device memory."""
+
+    def __init__(self, means_opacity, scaling, rotation, sh):
+        self.means_opacity = means_opacity.contiguous()
+        self.scaling = scaling.contiguous()
+        self.rotation = rotation.contiguous()
+        self.sh = sh.contiguous()
+        assert self.means_opacity.dtype == torch.float32 and self.means_opacity.shape[1] == 4
+
+    kind = abi.TDGS_TRAINABLE
+
+    @classmethod
+    def from_host(cls, g: HostGaussians, device=0):
+        d = _dev(device)
+        return cls(*(torch.from_numpy(np.ascontiguousarray(a)).to(d)
+                     for a in (g.means_opacity, g.scaling, g.rotation, g.sh)))
+
+    def to_host(self) -> HostGaussians:
+        return HostGaussians(*(t.cpu().numpy() for t in (self.means_opacity, self.scaling,
+                                                         self.rotation, self.sh)))
+
+    def __len__(self):
+        return self.means_opacity.shape[0]
+
+    @property
+    def device(self):
+        return self.means_opacity.device
+
+    @property
+    def sh_degree(self):
+        return int(round(math.sqrt(self.sh.shape[2]))) - 1
+
+    def struct(self):
+        s = abi.Gaussians()
+        s.kind = abi.TDGS_TRAINABLE
+        s.n = len(self)
+        s.sh_degree = self.sh_degree
+        s.means_opacity = dptr(self.means_opacity)
+        s.scaling = dptr(self.scaling)
+        s.rotation = dptr(self.rotation)
+        s.covariances = None
+        s.sh = dptr(self.sh)
+        return s
+
+
+class RenderOnlyGaussiansVector:
+    """RenderOnlyGaussiansVector (src/gaussians.jl:342-392): opacities already activated and
+    3D covariances as lower halves."""
+
+    kind = abi.TDGS_RENDER_ONLY
+
+    def __init__(self, means_opacities, covariances, sh):
+        self.means_opacity = means_opacities.contiguous()
+        self.covariances = covariances.contiguous()
+        self.sh = sh.contiguous()
+
+    def __len__(self):
+        return self.means_opacity.shape[0]
+
+    @property
+    def device(self):
+        return self.means_opacity.device
+
+    @property
+    def sh_degree(self):
+        return int(round(math.sqrt(self.sh.shape[2]))) - 1
+
+    def struct(self):
+        s = abi.Gaussians()
+        s.kind = abi.TDGS_RENDER_ONLY
+        s.n = len(self)
+        s.sh_degree = self.sh_degree
+        s.means_opacity = dptr(self.means_opacity)
+        s.scaling = None
+        s.rotation = None
+        s.covariances = dptr(self.covariances)
+        s.sh = dptr(self.sh)
+        return s
+
+
+class RenderOutputs:
+    """RenderOutputs (src/forward_structs.jl:1-129)."""
+
+    def __init__(self, width, height, device=0, include_rgb=True, include_transmittance=True,
+                 include_depth=False, include_last_contributing_indices=True):
+        d = _dev(device)
+        self.width, self.height = int(width), int(height)
+        self.rgb = torch.empty((width, height, 3), dtype=torch.float32, device=d) if include_rgb else None
+        self.T = torch.empty((width, height), dtype=torch.float32, device=d) if include_transmittance else None
+        self.depth = torch.empty((width, height), dtype=torch.float32, device=d) if include_depth else None
+        self.last = (torch.empty((width, height), dtype=torch.int32, device=d)
+                     if include_last_contributing_indices else None)
+
+    @classmethod
+    def for_camera(cls, cam: PinholeCamera, device=0, **kw):
+        return cls(cam.width, cam.height, device, **kw)
+
+    def struct(self):
+        return abi.RenderOutputsC(dptr(self.rgb), dptr(self.T), dptr(self.depth), dptr(self.last))
+
+
+class RenderBuffers:
+    """RenderBuffers + Filtered2DGaussiansVector (src/forward_structs.jl:762-833, 1541-1677).
+    Per-Gaussian arrays hold `capacity` entries; key arrays grow on demand."""
+
+    def __init__(self, capacity, tiling: Tiling, device=0, key_capacity=None, keep_flags=False):
+        d = _dev(device)
+        self.device = d
+        self.capacity = int(capacity)
+        self.tiling = tiling
+        cap = max(self.capacity, 1)
+        self.keep = torch.empty(cap, dtype=torch.uint8, device=d) if keep_flags else None
+        self.fgidx_to_gidx = torch.empty(cap, dtype=torch.int32, device=d)
+        self.depths = torch.empty(cap, dtype=torch.float32, device=d)
+        self.f2d = torch.empty((cap, 9), dtype=torch.float32, device=d)
+        self.tile_ranges = torch.empty((cap, 4), dtype=torch.int32, device=d)
+        self.counts = torch.empty(cap, dtype=torch.int32, device=d)
+        self.tiles_end = torch.empty(tiling.nb_tiles, dtype=torch.int32, device=d)
+        self.nb_fgaussians = 0
+        self.nb_keys = 0
+        self.key_capacity = 0
+        self.keys = self.values = self.sorted_keys = self.sorted_values = None
+        self._alloc_keys(key_capacity if key_capacity is not None else 8 * cap)
+
+    def _alloc_keys(self, key_capacity):
+        d = self.device
+        kc = max(int(key_capacity), 1)
+        self.key_capacity = kc
+        self.keys = torch.empty(kc, dtype=torch.int64, device=d)
+        self.values = torch.empty(kc, dtype=torch.int32, device=d)
+        self.sorted_keys = torch.empty(kc, dtype=torch.int64, device=d)
+        self.sorted_values = torch.empty(kc, dtype=torch.int32, device=d)
+        tb = lib().tdgs_render_temp_bytes(self.capacity, kc, C.byref(self.tiling.to_c()))
+        self.temp = torch.empty(int(tb), dtype=torch.uint8, device=d)
+
+    def ensure_capacity(self, n):
+        if n > self.capacity:
+            self.__init__(n, self.tiling, self.device.index, self.key_capacity, self.keep is not None)
+
+    def struct(self):
+        b = abi.RenderBuffersC()
+        b.capacity = self.capacity
+        b.key_capacity = self.key_capacity
+        b.keep = dptr(self.keep)
+        b.fgidx_to_gidx = dptr(self.fgidx_to_gidx)
+        b.depths = dptr(self.depths)
+        b.f2d = dptr(self.f2d)
+        b.tile_ranges = dptr(self.tile_ranges)
+        b.counts = dptr(self.counts)
+        b.keys = dptr(self.keys)
+        b.values = dptr(self.values)
+        b.sorted_keys = dptr(self.sorted_keys)
+        b.sorted_values = dptr(self.sorted_values)
+        b.tiles_end = dptr(self.tiles_end)
+        b.temp = dptr(self.temp)
+        b.temp_bytes = self.temp.numel()
+        return b
+
+
+# ------------------------------------------------------------------------------------
+# render!
+# ------------------------------------------------------------------------------------
+
+def render_(outputs: RenderOutputs, gaussians, camera: PinholeCamera, tiling: Tiling,
+            options: RenderOptions, buffers: RenderBuffers):
+    """render! (src/forward_core.jl:196-314). Grows the key buffers when needed."""
+    dev = gaussians.device.index
+    buffers.ensure_capacity(len(gaussians))
+    g = gaussians.struct()
+    cam, t, o = camera.to_c(), tiling.to_c(), options.to_c()
+    out = outputs.struct()
+    nbf = C.c_int32(0)
+    m = C.c_int64(0)
+    for _ in range(2):
+        b = buffers.struct()
+        rc = lib().tdgs_render(context(dev), stream_ptr(dev), C.byref(g), C.byref(cam), C.byref(t),
+                               C.byref(o), C.byref(b), C.byref(out), C.byref(nbf), C.byref(m))
+        if rc == abi.TDGS_ERR_CAPACITY and m.value > buffers.key_capacity and m.value < 2**31 - 1:
+            buffers._alloc_keys(int(m.value * 1.25) + 1024)
+            continue
+        check(rc)
+        break
+    buffers.nb_fgaussians = int(nbf.value)
+    buffers.nb_keys = int(m.value)
+    return outputs
+
+
+# ------------------------------------------------------------------------------------
+# Building blocks (one reference kernel each)
+# ------------------------------------------------------------------------------------
+
+def fill_fgidx_to_gidx(keep: torch.Tensor):
+    """accumulate!(+) + fill_fgidx_to_gidx_kernel! (forward_core.jl:231-244, 371-386)."""
+    dev = keep.device.index
+    n = keep.numel()
+    cs = torch.empty(n, dtype=torch.int32, device=keep.device)
+    f2g = torch.empty(n, dtype=torch.int32, device=keep.device)
+    temp = torch.empty(int(lib().tdgs_scan_temp_bytes(n)), dtype=torch.uint8, device=keep.device)
+    nf = C.c_int32(0)
+    check(lib().tdgs_fill_fgidx_to_gidx(context(dev), stream_ptr(dev), dptr(keep.to(torch.uint8)), n,
+                                        dptr(cs), dptr(f2g), dptr(temp), temp.numel(), C.byref(nf)))
+    return cs, f2g[: nf.value], nf.value
+
+
+def scan_counts(counts: torch.Tensor):
+    dev = counts.device.index
+    n = counts.numel()
+    cs = torch.empty(n, dtype=torch.int32, device=counts.device)
+    temp = torch.empty(int(lib().tdgs_scan_temp_bytes(n)), dtype=torch.uint8, device=counts.device)
+    tot = C.c_int64(0)
+    check(lib().tdgs_scan_counts(context(dev), stream_ptr(dev), dptr(counts), n, dptr(cs), dptr(temp),
+                                 temp.numel(), C.byref(tot)))
+    return cs, tot.value
+
+
+def emit_keys(depths, tile_ranges, counts_cs, total, tiling: Tiling):
+    dev = depths.device.index
+    nf = depths.numel()
+    keys = torch.empty(max(total, 1), dtype=torch.int64, device=depths.device)
+    vals = torch.empty(max(total, 1), dtype=torch.int32, device=depths.device)
+    check(lib().tdgs_emit_keys(stream_ptr(dev), nf, dptr(depths), dptr(tile_ranges), dptr(counts_cs),
+                               C.byref(tiling.to_c()), dptr(keys), dptr(vals)))
+    return keys[:total], vals[:total]
+
+
+def sort_pairs(keys: torch.Tensor, values: torch.Tensor, end_bit: int):
+    """sort_pairs (cub_sort_pairs_wrapper.cu:31-43): stable radix sort on bits [0, end_bit)."""
+    dev = keys.device.index
+    n = keys.numel()
+    tb = int(lib().tdgs_sort_pairs_temp_bytes(n, end_bit))
+    temp = torch.empty(tb, dtype=torch.uint8, device=keys.device)
+    ko = torch.empty_like(keys)
+    vo = torch.empty_like(values)
+    check(lib().tdgs_sort_pairs(dptr(temp), tb, dptr(keys), dptr(ko), dptr(values), dptr(vo), n, end_bit,
+                                stream_ptr(dev)))
+    return ko, vo
+
+
+def tile_ranges(sorted_keys: torch.Tensor, nb_tiles: int):
+    dev = sorted_keys.device.index
+    te = torch.empty(nb_tiles, dtype=torch.int32, device=sorted_keys.device)
+    check(lib().tdgs_tile_ranges(stream_ptr(dev), sorted_keys.numel(), dptr(sorted_keys), nb_tiles, dptr(te)))
+    return te

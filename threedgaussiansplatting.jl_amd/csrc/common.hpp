@@ -1,0 +1,76 @@
+// common.hpp — error reporting, launch helpers and wave-level primitives shared by the
+// gfx950 kernels of libtdgs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "tdgs_math.hpp"
+
+namespace tdgs {
+
+// Last error message of the calling host thread (tdgs_last_error()).
+void set_error(const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what, const char* file, int line);
+
+#define TDGS_HIP(call)                                                              \
+    do {                                                                            \
+        hipError_t e_ = (call);                                                     \
+        if (e_ != hipSuccess) return ::tdgs::hip_fail(e_, #call, __FILE__, __LINE__); \
+    } while (0)
+
+#define TDGS_LAUNCHED() TDGS_HIP(hipGetLastError())
+
+#define TDGS_REQUIRE(cond, ...)               \
+    do {                                      \
+        if (!(cond)) {                        \
+            ::tdgs::set_error(__VA_ARGS__);   \
+            return TDGS_ERR_INVALID;          \
+        }                                     \
+    } while (0)
+
+#define TDGS_TRY(expr)              \
+    do {                            \
+        int r_ = (expr);            \
+        if (r_ != TDGS_OK) return r_; \
+    } while (0)
+
+constexpr int kWave = 64;
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
+
+// Bump allocator over a caller-provided scratch buffer.
+struct Arena {
+    char* base;
+    size_t size;
+    size_t used;
+    Arena(void* p, size_t n) : base((char*)p), size(n), used(0) {}
+    template <class T>
+    T* take(int64_t count) {
+        const size_t bytes = align_up((size_t)(count > 0 ? count : 1) * sizeof(T));
+        if (used + bytes > size) return nullptr;
+        T* p = (T*)(base + used);
+        used += bytes;
+        return p;
+    }
+};
+
+// Counting-only twin of Arena: how many bytes a sequence of take() calls needs.
+struct ArenaSize {
+    size_t used = 0;
+    template <class T>
+    void take(int64_t count) { used += align_up((size_t)(count > 0 ? count : 1) * sizeof(T)); }
+};
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    return (1ull << __lane_id()) - 1ull;
+}
+
+// Device-wide scan over n int32 items produced by a functor, with int64 running sums
+// (scan.hip). In(i) returns item i; Out(i, inclusive, item) consumes the result.
+size_t scan_temp_bytes_internal(int64_t n);
+
+}  // namespace tdgs

@@ -1,0 +1,602 @@
+// forward.hip — render! on gfx950: cull + compact, projection, key duplication, sort,
+// tile ranges and per-tile front-to-back blending.
+//
+// Reference: src/forward_core.jl:196-993, src/forward_structs.jl:743-757.
+//
+// Pipeline of tdgs_render (one host synchronisation, to learn N_f and M):
+//   1. keep flags + per-tile sums                 scan pass 1 (KeepEval)
+//   2. fgidx_to_gidx compaction                   scan pass 3 (CompactOut)
+//   3. projection of the N_f kept Gaussians       k_project (grid over capacity; N_f read on
+//                                                 the device), also writes a 32-bit depth key
+//   4. stable sort of (depth bits, fgidx)         radix, bits [0, 32)
+//   5. scan of tile counts in depth order -> M    scan (SortedCounts)
+//   6. key emission in depth order                k_emit_depth_order
+//   7. stable sort by tile                        radix, key bits [32, end_bit)
+//   8. tile ranges                                k_tile_ranges
+//   9. blending                                   k_render_tiles
+// Steps 4-7 give exactly CUB's result on the reference's emission order: a Gaussian emits at
+// most one key per tile, so the reference's stable sort by (tile, depth bits) breaks ties by
+// ascending fgidx, i.e. it orders keys by (tile, depth bits, fgidx). Sorting the Gaussians by
+// (depth bits, fgidx) first and then stably by tile yields that same total order while
+// sorting only the tile bits of the M duplicated keys (2 passes instead of 6).
+#include "internal.hpp"
+#include "scan.hpp"
+#include "sort.hpp"
+
+namespace tdgs {
+
+// ------------------------------------------------------------------------------------
+// Culling + compaction
+// ------------------------------------------------------------------------------------
+
+struct KeepEval {
+    const float* mo;
+    int kind;
+    tdgs_camera cam;
+    tdgs_render_options opt;
+    uint8_t* keep;
+    __device__ int32_t operator()(int64_t i) const {
+        const float4 m = reinterpret_cast<const float4*>(mo)[i];
+        const bool k = keep_gaussian(cam, opt, m.x, m.y, m.z, opacity_of(kind, m.w));
+        keep[i] = k ? 1 : 0;
+        return k ? 1 : 0;
+    }
+};
+
+struct CompactOut {
+    int32_t* fgidx_to_gidx;
+    int32_t* keep_cs;
+    __device__ void operator()(int64_t i, int64_t incl, int32_t item) const {
+        if (keep_cs) keep_cs[i] = (int32_t)incl;
+        if (item) fgidx_to_gidx[incl - 1] = (int32_t)(i + 1);
+    }
+};
+
+__global__ void k_fill_keep(KeepEval ev, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) ev(i);
+}
+
+// ------------------------------------------------------------------------------------
+// Projection (project_fgaussians_kernel!, forward_core.jl:411-517)
+// ------------------------------------------------------------------------------------
+
+struct ProjectArgs {
+    tdgs_gaussians g;
+    tdgs_camera cam;
+    tdgs_tiling tiling;
+    tdgs_render_options opt;
+    int64_t cap;
+    const int64_t* d_nbf;     // device count of filtered Gaussians (or null: use nbf)
+    int64_t nbf;
+    const int32_t* fgidx_to_gidx;
+    float* depths;
+    float* f2d;
+    int32_t* ranges;
+    int32_t* counts;
+    uint32_t* depth_keys;     // optional: depth bits (0xffffffff when empty or unused)
+    int32_t* depth_vals;      // optional: fgidx (1-based), 0 for unused slots
+};
+
+__global__ __launch_bounds__(256) void k_project(ProjectArgs a) {
+    const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= a.cap) return;
+    const int64_t nbf = a.d_nbf ? *a.d_nbf : a.nbf;
+    if (f >= nbf) {
+        if (a.depth_keys) {
+            a.depth_keys[f] = 0xffffffffu;
+            a.depth_vals[f] = 0;
+        }
+        return;
+    }
+    const int64_t gi = (int64_t)a.fgidx_to_gidx[f] - 1;
+    const float4 m = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
+    const float op = opacity_of(a.g.kind, m.w);
+    float params[7];
+    if (a.g.kind == TDGS_TRAINABLE) {
+        params[0] = a.g.scaling[3 * gi];
+        params[1] = a.g.scaling[3 * gi + 1];
+        params[2] = a.g.scaling[3 * gi + 2];
+        const float4 q = reinterpret_cast<const float4*>(a.g.rotation)[gi];
+        params[3] = q.x; params[4] = q.y; params[5] = q.z; params[6] = q.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) params[k] = a.g.covariances[6 * gi + k];
+    }
+    const Projected pr = project_geometry(a.cam, a.opt, a.tiling, a.g.kind, m.x, m.y, m.z, op, params);
+    a.counts[f] = pr.count;
+    uint32_t dk = 0xffffffffu;
+    if (pr.count > 0) {
+        const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
+        float rgb[3];
+        project_color(a.cam, a.opt.sh_degree, a.g.sh + (int64_t)3 * hs * gi, hs, m.x, m.y, m.z, rgb);
+        a.depths[f] = pr.depth;
+        reinterpret_cast<int4*>(a.ranges)[f] = make_int4(pr.rect[0], pr.rect[1], pr.rect[2], pr.rect[3]);
+        float* r = a.f2d + 9 * f;
+        r[0] = pr.mux; r[1] = pr.muy; r[2] = pr.a;
+        r[3] = pr.m11; r[4] = pr.m21; r[5] = pr.m22;
+        r[6] = rgb[0]; r[7] = rgb[1]; r[8] = rgb[2];
+        dk = float_bits(pr.depth);
+    }
+    if (a.depth_keys) {
+        a.depth_keys[f] = dk;
+        a.depth_vals[f] = (int32_t)(f + 1);
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// Key duplication
+// ------------------------------------------------------------------------------------
+
+// Overlap counts of the Gaussians in depth order (entries past N_f count 0).
+struct SortedCounts {
+    const int32_t* sorted_f;
+    const int32_t* counts;
+    const int64_t* d_nbf;
+    __device__ int32_t operator()(int64_t j) const {
+        return j < *d_nbf ? counts[sorted_f[j] - 1] : 0;
+    }
+};
+
+// One thread per Gaussian in depth order writes its keys, tiles row-major (x fastest).
+__global__ __launch_bounds__(256) void k_emit_depth_order(int64_t nbf, const int32_t* __restrict__ sorted_f,
+                                                          const int32_t* __restrict__ cs,
+                                                          const float* __restrict__ depths,
+                                                          const int32_t* __restrict__ ranges, int32_t ntx,
+                                                          int64_t* __restrict__ keys,
+                                                          int32_t* __restrict__ vals) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= nbf) return;
+    const int64_t end = cs[j];
+    int64_t d = j == 0 ? 0 : cs[j - 1];
+    if (d >= end) return;
+    const int32_t f = sorted_f[j];
+    const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
+    const int64_t low = (int64_t)float_bits(depths[f - 1]);
+    for (int32_t ty = r.y; ty <= r.w; ++ty) {
+        for (int32_t tx = r.x; tx <= r.z; ++tx) {
+            if (d >= end) return;
+            keys[d] = ((int64_t)(tx + (ty - 1) * ntx) << 32) | low;
+            vals[d] = f;
+            ++d;
+        }
+    }
+}
+
+// fill_df2dgs_codes_and_dfgidx_to_fgidx_kernel! (forward_core.jl:531-603): reference
+// emission order (ascending fgidx).
+__global__ __launch_bounds__(256) void k_emit_keys(int64_t nbf, const float* __restrict__ depths,
+                                                   const int32_t* __restrict__ ranges,
+                                                   const int32_t* __restrict__ cs, int32_t ntx,
+                                                   int64_t* __restrict__ keys,
+                                                   int32_t* __restrict__ vals) {
+    const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= nbf) return;
+    const int64_t end = cs[f];
+    int64_t d = f == 0 ? 0 : cs[f - 1];
+    if (d >= end) return;
+    const int4 r = reinterpret_cast<const int4*>(ranges)[f];
+    const float depth = depths[f];
+    for (int32_t ty = r.y; ty <= r.w; ++ty) {
+        for (int32_t tx = r.x; tx <= r.z; ++tx) {
+            if (d >= end) return;
+            keys[d] = make_key(tx + (ty - 1) * ntx, depth);
+            vals[d] = (int32_t)(f + 1);
+            ++d;
+        }
+    }
+}
+
+// fill_tiles_end_sdfgidx_kernel! (forward_core.jl:676-734). Tile ids are clamped to
+// [1, nb_tiles] so that a malformed key cannot write out of bounds.
+__global__ __launch_bounds__(256) void k_tile_ranges(int64_t m, const int64_t* __restrict__ sk,
+                                                     int32_t nb_tiles, int32_t* __restrict__ te) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    const int32_t cur = (int32_t)(sk[i] >> 32);
+    if (i == 0) {
+        const int32_t stop = cur < nb_tiles + 1 ? cur : nb_tiles + 1;
+        for (int32_t t = 1; t < stop; ++t) te[t - 1] = 0;
+    }
+    int32_t lo = cur < 1 ? 1 : cur;
+    if (i + 1 < m) {
+        int32_t nxt = (int32_t)(sk[i + 1] >> 32);
+        if (nxt > nb_tiles + 1) nxt = nb_tiles + 1;
+        for (int32_t t = lo; t < nxt; ++t) te[t - 1] = (int32_t)(i + 1);
+    } else {
+        for (int32_t t = lo; t <= nb_tiles; ++t) te[t - 1] = (int32_t)m;
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// Blending (render_tiles_kernel!, forward_core.jl:756-993)
+// ------------------------------------------------------------------------------------
+
+struct __align__(16) BlendRec {
+    float4 a;  // p0 p1 p2 p3
+    float4 b;  // p4 p5 r g
+    float4 c;  // b depth - -
+};
+
+struct BlendArgs {
+    int32_t W, H, TW, TH, ntx;
+    float bg0, bg1, bg2, min_alpha, max_alpha, min_T;
+    int64_t m;
+    const int32_t* tiles_end;
+    const int32_t* sorted_f;
+    const float* f2d;
+    const float* depths;
+    float* rgb;
+    float* T;
+    float* depth;
+    int32_t* last;
+};
+
+// One workgroup per tile, one thread per pixel. Thread t covers pixel row t % TH and column
+// t / TH of the tile, so a wavefront writes whole column segments of the column-major
+// images. Each batch of TW*TH sorted entries is converted to blending parameters once per
+// tile and staged in LDS, where every lane reads the same record (broadcast). The tile stops
+// loading batches once every pixel is done (block-wide count of live pixels).
+template <bool RGB, bool DEPTH>
+__global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
+    extern __shared__ BlendRec s_rec[];
+    const int NT = a.TW * a.TH;
+    const int t = threadIdx.x;
+    const int tx = blockIdx.x + 1, ty = blockIdx.y + 1;
+    const int tile = tx + (ty - 1) * a.ntx;
+    const int v_in = t % a.TH + 1, u_in = t / a.TH + 1;
+    const int U = u_in + (tx - 1) * a.TW, V = v_in + (ty - 1) * a.TH;
+    const bool on = U <= a.W && V <= a.H;
+    const float cu = (float)u_in - 0.5f, cv = (float)v_in - 0.5f;
+    const float uu = cu * cu, uv = cu * cv, vv = cv * cv;
+    const float u0 = (float)((tx - 1) * a.TW), v0 = (float)((ty - 1) * a.TH);
+    int64_t end = a.tiles_end[tile - 1];
+    int64_t beg = tile == 1 ? 0 : a.tiles_end[tile - 2];
+    if (end > a.m) end = a.m;
+    if (beg < 0) beg = 0;
+    if (beg > end) beg = end;
+
+    float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f, D = 0.0f;
+    int32_t last = 0;
+    bool done = !on;
+    for (int64_t base = beg; base < end; base += NT) {
+        if (__syncthreads_count(done ? 0 : 1) == 0) break;
+        const int64_t s = base + t;
+        if (s < end) {
+            const int64_t f = (int64_t)a.sorted_f[s] - 1;
+            const float* r = a.f2d + 9 * f;
+            float p[6];
+            blend_params(r[0], r[1], r[2], r[3], r[4], r[5], u0, v0, p);
+            BlendRec rec;
+            rec.a = make_float4(p[0], p[1], p[2], p[3]);
+            rec.b = make_float4(p[4], p[5], RGB ? r[6] : 0.0f, RGB ? r[7] : 0.0f);
+            rec.c = make_float4(RGB ? r[8] : 0.0f, DEPTH ? a.depths[f] : 0.0f, 0.0f, 0.0f);
+            s_rec[t] = rec;
+        }
+        __syncthreads();
+        const int nb = (int)((end - base) < NT ? (end - base) : NT);
+        if (!done) {
+            for (int j = 0; j < nb; ++j) {
+                const float4 ra = s_rec[j].a;
+                const float4 rb = s_rec[j].b;
+                const float e = fmaf(ra.x, uu, fmaf(ra.y, vv, fmaf(ra.z, uv, fmaf(ra.w, cu, fmaf(rb.x, cv, rb.y)))));
+                const float alpha = fminf(a.max_alpha, exp_f(e));
+                if (alpha < a.min_alpha) continue;
+                const float Tn = T * (1.0f - alpha);
+                if (Tn < a.min_T) {
+                    done = true;
+                    break;
+                }
+                const float w = T * alpha;
+                if (RGB || DEPTH) {
+                    const float4 rc = s_rec[j].c;
+                    if (RGB) {
+                        C0 = fmaf(w, rb.z, C0);
+                        C1 = fmaf(w, rb.w, C1);
+                        C2 = fmaf(w, rc.x, C2);
+                    }
+                    if (DEPTH) D = fmaf(w, rc.y, D);
+                }
+                T = Tn;
+                last = (int32_t)(base + j + 1);
+            }
+        }
+    }
+    if (!on) return;
+    const int64_t px = (int64_t)(V - 1) + (int64_t)a.H * (U - 1);
+    if (RGB && a.rgb) {
+        a.rgb[3 * px] = fmaf(T, a.bg0, C0);
+        a.rgb[3 * px + 1] = fmaf(T, a.bg1, C1);
+        a.rgb[3 * px + 2] = fmaf(T, a.bg2, C2);
+    }
+    if (a.T) a.T[px] = T;
+    if (DEPTH && a.depth) a.depth[px] = D;
+    if (a.last) a.last[px] = last;
+}
+
+// render_void! (forward_structs.jl:743-757).
+__global__ void k_render_void(int64_t npx, float bg0, float bg1, float bg2, float* rgb, float* T,
+                              float* depth, int32_t* last) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= npx) return;
+    if (rgb) {
+        rgb[3 * i] = bg0;
+        rgb[3 * i + 1] = bg1;
+        rgb[3 * i + 2] = bg2;
+    }
+    if (T) T[i] = 1.0f;
+    if (depth) depth[i] = kInf;
+    if (last) last[i] = 0;
+}
+
+static int launch_render_void(hipStream_t s, const tdgs_camera* cam, const tdgs_render_options* o,
+                              const tdgs_render_outputs* out) {
+    const int64_t npx = (int64_t)cam->width * cam->height;
+    k_render_void<<<(unsigned)ceil_div(npx, 256), 256, 0, s>>>(npx, o->background[0], o->background[1],
+                                                               o->background[2], out->rgb, out->T,
+                                                               out->depth, out->last);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs_tiling* t,
+                               const tdgs_render_options* o, int64_t m, const int32_t* tiles_end,
+                               const int32_t* sorted_f, const float* f2d, const float* depths,
+                               const tdgs_render_outputs* out) {
+    BlendArgs a;
+    a.W = cam->width; a.H = cam->height; a.TW = t->tile_width; a.TH = t->tile_height;
+    a.ntx = t->nb_tiles_x;
+    a.bg0 = o->background[0]; a.bg1 = o->background[1]; a.bg2 = o->background[2];
+    a.min_alpha = o->min_alpha; a.max_alpha = o->max_alpha; a.min_T = o->min_transmittance;
+    a.m = m; a.tiles_end = tiles_end; a.sorted_f = sorted_f; a.f2d = f2d; a.depths = depths;
+    a.rgb = out->rgb; a.T = out->T; a.depth = out->depth; a.last = out->last;
+    const int nt = t->tile_width * t->tile_height;
+    const dim3 grid(t->nb_tiles_x, t->nb_tiles_y);
+    const size_t lds = (size_t)nt * sizeof(BlendRec);
+    const bool rgb = out->rgb != nullptr, dep = out->depth != nullptr;
+    if (rgb && dep) k_render_tiles<true, true><<<grid, nt, lds, s>>>(a);
+    else if (rgb) k_render_tiles<true, false><<<grid, nt, lds, s>>>(a);
+    else if (dep) k_render_tiles<false, true><<<grid, nt, lds, s>>>(a);
+    else k_render_tiles<false, false><<<grid, nt, lds, s>>>(a);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+static int end_bit_of(const tdgs_tiling* t) {
+    const int64_t nt = (int64_t)t->nb_tiles_x * t->nb_tiles_y;
+    int fl = 0;
+    while ((2ll << fl) <= nt) ++fl;  // floor(log2(nt))
+    return 33 + fl;
+}
+
+// Scratch layout of tdgs_render.
+template <class A>
+static void render_layout(A& ar, int64_t cap, int64_t key_cap) {
+    ar.template take<int64_t>(kCounters);                 // unused slot (alignment)
+    ar.template take<uint8_t>(cap);                       // keep flags when buf->keep is null
+    ar.template take<uint32_t>(cap);                      // depth keys
+    ar.template take<uint32_t>(cap);                      // depth keys, ping-pong
+    ar.template take<uint32_t>(cap);                      // depth keys, sorted
+    ar.template take<int32_t>(cap);                       // depth values
+    ar.template take<int32_t>(cap);                       // depth values, ping-pong
+    ar.template take<int32_t>(cap);                       // depth values, sorted (fgidx)
+    ar.template take<int32_t>(cap);                       // counts scan in depth order
+    ar.template take<char>((int64_t)scan_temp_bytes_for(cap));
+    const int64_t big = cap > key_cap ? cap : key_cap;
+    ar.template take<char>((int64_t)radix_temp_bytes(big));
+}
+
+}  // namespace tdgs
+
+using namespace tdgs;
+
+extern "C" {
+
+int tdgs_fill_keep(void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
+                   const tdgs_render_options* opt, uint8_t* keep) {
+    TDGS_TRY(check_gaussians(g, false));
+    TDGS_TRY(check_options(opt, g->sh_degree));
+    TDGS_REQUIRE(cam && (keep || g->n == 0), "null camera or keep");
+    if (g->n == 0) return TDGS_OK;
+    KeepEval ev{g->means_opacity, g->kind, *cam, *opt, keep};
+    k_fill_keep<<<(unsigned)ceil_div(g->n, 256), 256, 0, (hipStream_t)stream>>>(ev, g->n);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+size_t tdgs_scan_temp_bytes(int64_t n) { return scan_temp_bytes_for(n); }
+
+int tdgs_fill_fgidx_to_gidx(tdgs_ctx* ctx, void* stream, const uint8_t* keep, int32_t n,
+                            int32_t* keep_cs, int32_t* fgidx_to_gidx, void* temp, size_t temp_bytes,
+                            int32_t* nb_fgaussians_out) {
+    TDGS_REQUIRE(ctx && nb_fgaussians_out, "null ctx or output");
+    TDGS_REQUIRE(n >= 0, "negative n");
+    if (n == 0) { *nb_fgaussians_out = 0; return TDGS_OK; }
+    TDGS_REQUIRE(keep && fgidx_to_gidx, "null keep or fgidx_to_gidx");
+    hipStream_t s = (hipStream_t)stream;
+    TDGS_TRY(device_scan(ItemsU8{keep}, ItemsU8{keep}, CompactOut{fgidx_to_gidx, keep_cs}, n, temp,
+                         temp_bytes, ctx->d_counters, s));
+    TDGS_TRY(read_counters(ctx, s, 1));
+    *nb_fgaussians_out = (int32_t)ctx->h_counters[0];
+    return TDGS_OK;
+}
+
+int tdgs_scan_counts(tdgs_ctx* ctx, void* stream, const int32_t* counts, int32_t n, int32_t* counts_cs,
+                     void* temp, size_t temp_bytes, int64_t* total_out) {
+    TDGS_REQUIRE(ctx && total_out, "null ctx or output");
+    TDGS_REQUIRE(n >= 0, "negative n");
+    if (n == 0) { *total_out = 0; return TDGS_OK; }
+    TDGS_REQUIRE(counts && counts_cs, "null arrays");
+    hipStream_t s = (hipStream_t)stream;
+    TDGS_TRY(device_scan(ItemsI32{counts}, ItemsI32{counts}, WriteInclusiveI32{counts_cs}, n, temp,
+                         temp_bytes, ctx->d_counters, s));
+    TDGS_TRY(read_counters(ctx, s, 1));
+    *total_out = ctx->h_counters[0];
+    if (*total_out >= (int64_t)INT32_MAX) {
+        set_error("%lld duplicated keys exceed the int32 index range", (long long)*total_out);
+        return TDGS_ERR_CAPACITY;
+    }
+    return TDGS_OK;
+}
+
+int tdgs_emit_keys(void* stream, int32_t nb_fgaussians, const float* depths, const int32_t* tile_ranges,
+                   const int32_t* counts_cs, const tdgs_tiling* tiling, int64_t* keys, int32_t* values) {
+    TDGS_REQUIRE(nb_fgaussians >= 0 && tiling, "bad arguments");
+    if (nb_fgaussians == 0) return TDGS_OK;
+    TDGS_REQUIRE(depths && tile_ranges && counts_cs && keys && values, "null arrays");
+    k_emit_keys<<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, (hipStream_t)stream>>>(
+        nb_fgaussians, depths, tile_ranges, counts_cs, tiling->nb_tiles_x, keys, values);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+size_t tdgs_sort_pairs_temp_bytes(int32_t n, int32_t end_bit) {
+    (void)end_bit;
+    const int64_t nn = n > 0 ? n : 1;
+    return align_up((size_t)nn * sizeof(int64_t)) + align_up((size_t)nn * sizeof(int32_t)) +
+           radix_temp_bytes(nn);
+}
+
+int tdgs_sort_pairs(void* temp, size_t temp_bytes, const int64_t* keys_in, int64_t* keys_out,
+                    const int32_t* values_in, int32_t* values_out, int32_t n, int32_t end_bit,
+                    void* stream) {
+    TDGS_REQUIRE(n >= 0 && end_bit >= 0 && end_bit <= 64, "bad n or end_bit");
+    if (n == 0) return TDGS_OK;
+    TDGS_REQUIRE(keys_in && keys_out && values_in && values_out && temp, "null arrays");
+    TDGS_REQUIRE(keys_in != keys_out && values_in != values_out, "sort_pairs is not in place");
+    TDGS_REQUIRE(temp_bytes >= tdgs_sort_pairs_temp_bytes(n, end_bit), "sort scratch too small");
+    Arena ar(temp, temp_bytes);
+    uint64_t* alt_k = ar.take<uint64_t>(n);
+    int32_t* alt_v = ar.take<int32_t>(n);
+    const size_t rb = radix_temp_bytes(n);
+    void* rtemp = ar.take<char>((int64_t)rb);
+    return radix_sort_pairs<uint64_t>((const uint64_t*)keys_in, (uint64_t*)keys_out, values_in, values_out,
+                                      alt_k, alt_v, n, 0, end_bit, rtemp, rb, (hipStream_t)stream);
+}
+
+int tdgs_tile_ranges(void* stream, int64_t nb_keys, const int64_t* sorted_keys, int32_t nb_tiles,
+                     int32_t* tiles_end) {
+    TDGS_REQUIRE(nb_keys >= 0 && nb_tiles > 0 && tiles_end, "bad arguments");
+    if (nb_keys == 0) return TDGS_OK;
+    TDGS_REQUIRE(sorted_keys, "null keys");
+    k_tile_ranges<<<(unsigned)ceil_div(nb_keys, 256), 256, 0, (hipStream_t)stream>>>(nb_keys, sorted_keys,
+                                                                                      nb_tiles, tiles_end);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+int tdgs_render_tiles(void* stream, const tdgs_camera* cam, const tdgs_tiling* tiling,
+                      const tdgs_render_options* opt, const tdgs_render_buffers* buf,
+                      const tdgs_render_outputs* out) {
+    TDGS_TRY(check_tiling(tiling, cam));
+    TDGS_REQUIRE(opt && buf && out, "null arguments");
+    TDGS_REQUIRE(buf->tiles_end && buf->sorted_values && buf->f2d, "null buffers");
+    TDGS_REQUIRE(!out->depth || buf->depths, "depth output needs depths");
+    return launch_render_tiles((hipStream_t)stream, cam, tiling, opt, buf->key_capacity, buf->tiles_end,
+                               buf->sorted_values, buf->f2d, buf->depths, out);
+}
+
+size_t tdgs_render_temp_bytes(int32_t capacity, int64_t key_capacity, const tdgs_tiling* tiling) {
+    (void)tiling;
+    ArenaSize sz;
+    render_layout(sz, capacity, key_capacity);
+    return sz.used + 256;
+}
+
+int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
+                const tdgs_tiling* tiling, const tdgs_render_options* opt, tdgs_render_buffers* buf,
+                const tdgs_render_outputs* out, int32_t* nb_fgaussians_out, int64_t* nb_keys_out) {
+    TDGS_REQUIRE(ctx && buf && out && nb_fgaussians_out && nb_keys_out, "null arguments");
+    TDGS_TRY(check_gaussians(g, false));
+    TDGS_TRY(check_tiling(tiling, cam));
+    TDGS_TRY(check_options(opt, g->sh_degree));
+    TDGS_REQUIRE(cam->near_z >= 0.0f, "near clipping plane must be >= 0 (got %g)", (double)cam->near_z);
+    TDGS_REQUIRE(buf->capacity >= g->n, "render buffers hold %d Gaussians, need %d", buf->capacity, g->n);
+    hipStream_t s = (hipStream_t)stream;
+    *nb_fgaussians_out = 0;
+    *nb_keys_out = 0;
+    const int64_t n = g->n;
+    if (n == 0) return launch_render_void(s, cam, opt, out);
+    TDGS_REQUIRE(buf->fgidx_to_gidx && buf->depths && buf->f2d && buf->tile_ranges && buf->counts &&
+                     buf->tiles_end && buf->temp,
+                 "null render buffers");
+    const size_t need = tdgs_render_temp_bytes(buf->capacity, buf->key_capacity, tiling);
+    if (buf->temp_bytes < need) {
+        set_error("render scratch too small: need %zu bytes, have %zu", need, buf->temp_bytes);
+        return TDGS_ERR_CAPACITY;
+    }
+    const int64_t cap = buf->capacity;
+    Arena ar(buf->temp, buf->temp_bytes);
+    ar.take<int64_t>(kCounters);
+    uint8_t* keep_tmp = ar.take<uint8_t>(cap);
+    uint32_t* dkey = ar.take<uint32_t>(cap);
+    uint32_t* dkey_alt = ar.take<uint32_t>(cap);
+    uint32_t* dkey_sorted = ar.take<uint32_t>(cap);
+    int32_t* dval = ar.take<int32_t>(cap);
+    int32_t* dval_alt = ar.take<int32_t>(cap);
+    int32_t* sorted_f = ar.take<int32_t>(cap);
+    int32_t* cs = ar.take<int32_t>(cap);
+    const size_t sbytes = scan_temp_bytes_for(cap);
+    void* stemp = ar.take<char>((int64_t)sbytes);
+    const int64_t big = cap > buf->key_capacity ? cap : buf->key_capacity;
+    const size_t rbytes = radix_temp_bytes(big);
+    void* rtemp = ar.take<char>((int64_t)rbytes);
+    uint8_t* keep = buf->keep ? buf->keep : keep_tmp;
+    int64_t* d_nbf = ctx->d_counters;
+    int64_t* d_m = ctx->d_counters + 1;
+
+    // 1-2: keep flags and compaction
+    KeepEval ev{g->means_opacity, g->kind, *cam, *opt, keep};
+    TDGS_TRY(device_scan(ev, ItemsU8{keep}, CompactOut{buf->fgidx_to_gidx, nullptr}, n, stemp, sbytes,
+                         d_nbf, s));
+    // 3: projection
+    ProjectArgs pa;
+    pa.g = *g; pa.cam = *cam; pa.tiling = *tiling; pa.opt = *opt;
+    pa.cap = n; pa.d_nbf = d_nbf; pa.nbf = 0;
+    pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
+    pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
+    pa.depth_keys = dkey; pa.depth_vals = dval;
+    k_project<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(pa);
+    TDGS_LAUNCHED();
+    // 4: Gaussians by (depth bits, fgidx)
+    TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
+                                        rtemp, rbytes, s));
+    // 5: tile counts in depth order -> M
+    TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nbf}, SortedCounts{sorted_f, buf->counts, d_nbf},
+                         WriteInclusiveI32{cs}, n, stemp, sbytes, d_m, s));
+    TDGS_TRY(read_counters(ctx, s, 2));
+    const int64_t nbf = ctx->h_counters[0];
+    const int64_t m = ctx->h_counters[1];
+    *nb_fgaussians_out = (int32_t)nbf;
+    *nb_keys_out = m;
+    if (nbf == 0 || m == 0) return launch_render_void(s, cam, opt, out);
+    if (m >= (int64_t)INT32_MAX) {
+        set_error("%lld duplicated keys exceed the int32 index range", (long long)m);
+        return TDGS_ERR_CAPACITY;
+    }
+    if (m > buf->key_capacity || !buf->keys || !buf->values || !buf->sorted_keys || !buf->sorted_values) {
+        set_error("key buffers hold %lld keys, %lld needed", (long long)buf->key_capacity, (long long)m);
+        return TDGS_ERR_CAPACITY;
+    }
+    // 6-7: emit in depth order, then stable sort on the tile bits. The first radix pass
+    // writes sorted_* when the pass count is odd, keys/values when even; emit into the other.
+    const int eb = end_bit_of(tiling);
+    const int passes = radix_passes(32, eb);
+    const bool emit_into_sorted = (passes % 2) == 0;
+    int64_t* ek = emit_into_sorted ? buf->sorted_keys : buf->keys;
+    int32_t* ev2 = emit_into_sorted ? buf->sorted_values : buf->values;
+    k_emit_depth_order<<<(unsigned)ceil_div(nbf, 256), 256, 0, s>>>(nbf, sorted_f, cs, buf->depths,
+                                                                    buf->tile_ranges, tiling->nb_tiles_x, ek, ev2);
+    TDGS_LAUNCHED();
+    TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2, buf->sorted_values,
+                                        (uint64_t*)buf->keys, buf->values, m, 32, eb, rtemp, rbytes, s));
+    // 8: tile ranges
+    const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
+    k_tile_ranges<<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles, buf->tiles_end);
+    TDGS_LAUNCHED();
+    // 9: blending
+    return launch_render_tiles(s, cam, tiling, opt, m, buf->tiles_end, buf->sorted_values, buf->f2d,
+                               buf->depths, out);
+}
+
+}  // extern "C"

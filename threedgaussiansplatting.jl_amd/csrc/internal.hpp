@@ -1,0 +1,53 @@
+// internal.hpp — pieces shared between the translation units of libtdgs.
+#pragma once
+
+#include "common.hpp"
+
+struct tdgs_ctx {
+    int device;
+    int64_t* d_counters;   // device scratch for counts reported to the host
+    int64_t* h_counters;   // pinned host mirror of d_counters
+};
+
+namespace tdgs {
+
+constexpr int kCounters = 8;
+
+// Copy the first count device counters to the host and wait for the stream.
+int read_counters(tdgs_ctx* ctx, hipStream_t stream, int count);
+
+inline int check_gaussians(const tdgs_gaussians* g, bool trainable_only) {
+    TDGS_REQUIRE(g != nullptr, "gaussians is null");
+    TDGS_REQUIRE(g->n >= 0, "negative Gaussian count %d", g->n);
+    TDGS_REQUIRE(g->sh_degree >= 0 && g->sh_degree <= 3, "unsupported SH degree %d", g->sh_degree);
+    TDGS_REQUIRE(g->kind == TDGS_TRAINABLE || g->kind == TDGS_RENDER_ONLY, "unknown Gaussian kind %d", g->kind);
+    if (trainable_only) TDGS_REQUIRE(g->kind == TDGS_TRAINABLE, "operation needs trainable Gaussians");
+    if (g->n > 0) {
+        TDGS_REQUIRE(g->means_opacity && g->sh, "null Gaussian arrays");
+        if (g->kind == TDGS_TRAINABLE) TDGS_REQUIRE(g->scaling && g->rotation, "null scaling/rotation");
+        else TDGS_REQUIRE(g->covariances, "null covariances");
+    }
+    return TDGS_OK;
+}
+
+inline int check_tiling(const tdgs_tiling* t, const tdgs_camera* cam) {
+    TDGS_REQUIRE(t && cam, "null tiling or camera");
+    TDGS_REQUIRE(t->tile_width > 0 && t->tile_height > 0, "bad tile size");
+    const int nt = t->tile_width * t->tile_height;
+    TDGS_REQUIRE(nt <= 1024 && nt % 64 == 0, "tile of %d pixels: need a multiple of 64 up to 1024", nt);
+    TDGS_REQUIRE(cam->width > 0 && cam->height > 0, "bad image size");
+    TDGS_REQUIRE(t->nb_tiles_x == (cam->width + t->tile_width - 1) / t->tile_width &&
+                     t->nb_tiles_y == (cam->height + t->tile_height - 1) / t->tile_height,
+                 "tiling does not match the image size");
+    return TDGS_OK;
+}
+
+inline int check_options(const tdgs_render_options* o, int data_degree) {
+    TDGS_REQUIRE(o != nullptr, "null options");
+    TDGS_REQUIRE(o->sh_degree >= 0 && o->sh_degree <= data_degree,
+                 "render SH degree %d exceeds the data's %d", o->sh_degree, data_degree);
+    TDGS_REQUIRE(o->clip_mode == TDGS_CLIP_CLAMP || o->clip_mode == TDGS_CLIP_FILTER, "bad clip mode");
+    return TDGS_OK;
+}
+
+}  // namespace tdgs

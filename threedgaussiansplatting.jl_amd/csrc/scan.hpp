@@ -1,0 +1,152 @@
+// scan.hpp — device-wide inclusive scan of int32 items with int64 running sums
+// (replaces CUDA.jl's accumulate!(+) at src/forward_core.jl:231, 259 and
+// src/training.jl:384). Reduce-then-scan in three launches:
+//   1. each 2048-item tile reduces its items            (k_scan_reduce)
+//   2. one block scans the tile sums, writes the total   (k_scan_tiles)
+//   3. each tile rescans its items with its offset        (k_scan_apply)
+// Items come from a functor In(i) and results go to a functor Out(i, inclusive, item), so
+// compaction, gathers and scatters fuse into the scan passes instead of separate kernels.
+#pragma once
+
+#include "common.hpp"
+
+namespace tdgs {
+
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kScanThreads * kScanItems;
+
+// Block-wide exclusive scan of one int64 per thread; returns the exclusive prefix and
+// writes the block total to *total.
+__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* total) {
+    __shared__ int64_t s_wave[kScanThreads / kWave];
+    const int lane = __lane_id();
+    const int wave = threadIdx.x / kWave;
+    int64_t incl = v;
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int64_t o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    int64_t wave_off = 0, tot = 0;
+    for (int w = 0; w < kScanThreads / kWave; ++w) {
+        const int64_t s = s_wave[w];
+        if (w < wave) wave_off += s;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return wave_off + incl - v;
+}
+
+template <class In>
+__global__ __launch_bounds__(kScanThreads) void k_scan_reduce(In in, int64_t n, int64_t* tile_sums) {
+    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    int64_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        const int64_t i = base + k;
+        if (i < n) acc += in(i);
+    }
+    int64_t total;
+    block_exclusive_scan(acc, &total);
+    if (threadIdx.x == 0) tile_sums[blockIdx.x] = total;
+}
+
+// Single block: exclusive scan of the tile sums in place; grand total to *total_out.
+__global__ __launch_bounds__(kScanThreads) void k_scan_tiles(int64_t* tile_sums, int64_t ntiles,
+                                                             int64_t* total_out) {
+    int64_t carry = 0;
+    for (int64_t start = 0; start < ntiles; start += (int64_t)kScanThreads * kScanItems) {
+        const int64_t base = start + (int64_t)threadIdx.x * kScanItems;
+        int64_t v[kScanItems];
+        int64_t acc = 0;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            v[k] = base + k < ntiles ? tile_sums[base + k] : 0;
+            acc += v[k];
+        }
+        int64_t total;
+        int64_t off = block_exclusive_scan(acc, &total) + carry;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            if (base + k < ntiles) tile_sums[base + k] = off;
+            off += v[k];
+        }
+        carry += total;
+    }
+    if (threadIdx.x == 0 && total_out) *total_out = carry;
+}
+
+template <class In, class Out>
+__global__ __launch_bounds__(kScanThreads) void k_scan_apply(In in, Out out, int64_t n,
+                                                             const int64_t* tile_offsets) {
+    const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    int32_t v[kScanItems];
+    int64_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        const int64_t i = base + k;
+        v[k] = i < n ? in(i) : 0;
+        acc += v[k];
+    }
+    int64_t total;
+    int64_t run = block_exclusive_scan(acc, &total) + tile_offsets[blockIdx.x];
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        const int64_t i = base + k;
+        run += v[k];
+        if (i < n) out(i, run, v[k]);
+    }
+}
+
+inline size_t scan_temp_bytes_for(int64_t n) {
+    return align_up((size_t)(ceil_div(n > 0 ? n : 1, kScanTile)) * sizeof(int64_t));
+}
+
+// In1 is used by the reduce pass, In2 by the apply pass (they may differ when the reduce
+// pass also materialises the items, e.g. writes keep flags that the apply pass re-reads).
+template <class In1, class In2, class Out>
+int device_scan(In1 in_reduce, In2 in_apply, Out out, int64_t n, void* temp, size_t temp_bytes,
+                int64_t* d_total, hipStream_t stream) {
+    const int64_t ntiles = ceil_div(n > 0 ? n : 1, kScanTile);
+    if (temp_bytes < (size_t)ntiles * sizeof(int64_t) || temp == nullptr) {
+        set_error("scan scratch too small: need %zu bytes, have %zu", (size_t)ntiles * 8, temp_bytes);
+        return TDGS_ERR_CAPACITY;
+    }
+    int64_t* tile_sums = (int64_t*)temp;
+    k_scan_reduce<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_reduce, n, tile_sums);
+    TDGS_LAUNCHED();
+    k_scan_tiles<<<1, kScanThreads, 0, stream>>>(tile_sums, ntiles, d_total);
+    TDGS_LAUNCHED();
+    k_scan_apply<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_apply, out, n, tile_sums);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+// Common item/result functors.
+struct ItemsU8 {
+    const uint8_t* p;
+    __device__ int32_t operator()(int64_t i) const { return p[i] ? 1 : 0; }
+};
+struct ItemsI32 {
+    const int32_t* p;
+    __device__ int32_t operator()(int64_t i) const { return p[i]; }
+};
+struct ItemsU32 {
+    const uint32_t* p;
+    __device__ int32_t operator()(int64_t i) const { return (int32_t)p[i]; }
+};
+struct WriteInclusiveI32 {
+    int32_t* p;
+    __device__ void operator()(int64_t i, int64_t incl, int32_t) const { p[i] = (int32_t)incl; }
+};
+struct WriteExclusiveU32 {
+    uint32_t* p;
+    __device__ void operator()(int64_t i, int64_t incl, int32_t item) const {
+        p[i] = (uint32_t)(incl - item);
+    }
+};
+
+}  // namespace tdgs
