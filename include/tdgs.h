@@ -176,6 +176,24 @@ typedef struct tdgs_adc_buffers {
 
 typedef struct tdgs_ctx tdgs_ctx;
 
+/* Stages timed by the optional profiler (tdgs_profile_begin/end). */
+enum {
+    TDGS_STAGE_CULL_COMPACT = 0,   /* keep flags + compaction (scan) */
+    TDGS_STAGE_PROJECT = 1,        /* projection, SH colour, tile rectangles */
+    TDGS_STAGE_DEPTH_SORT = 2,     /* radix sort of the Gaussians by depth */
+    TDGS_STAGE_COUNT_SCAN = 3,     /* scan of overlapped-tile counts */
+    TDGS_STAGE_EMIT = 4,           /* key duplication */
+    TDGS_STAGE_TILE_SORT = 5,      /* radix sort of the keys by tile */
+    TDGS_STAGE_TILE_RANGES = 6,
+    TDGS_STAGE_BLEND = 7,          /* forward per-tile blending */
+    TDGS_STAGE_BACKWARD_BLEND = 8,
+    TDGS_STAGE_BACKWARD_PROJECT = 9,
+    TDGS_STAGE_ADAM = 10,
+    TDGS_STAGE_ADC = 11,
+    TDGS_STAGE_LOSS = 12,
+    TDGS_STAGE_COUNT = 13
+};
+
 /* ---- context, errors, device memory plumbing --------------------------------------- */
 int tdgs_abi_version(void);
 const char* tdgs_last_error(void);
@@ -187,6 +205,14 @@ int tdgs_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int tdgs_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int tdgs_memset(void* dst, int value, size_t bytes, void* stream);
 int tdgs_stream_synchronize(void* stream);
+
+/* Stage profiler (calling host thread): while enabled, library calls record a pair of HIP
+ * events around each stage on the stream they run on (no extra synchronisation). At most
+ * max_records stage executions are recorded. tdgs_profile_end waits for the recorded
+ * events and returns, per stage, the summed milliseconds and the number of executions
+ * (arrays of TDGS_STAGE_COUNT entries), then disables recording. */
+int tdgs_profile_begin(int32_t max_records);
+int tdgs_profile_end(double* ms_out, int64_t* executions_out);
 
 /* ---- forward building blocks (each replaces one reference kernel) ------------------- */
 

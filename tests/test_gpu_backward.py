@@ -1,0 +1,86 @@
+"""GPU parity of backward! against the CPU oracle, through the C-ABI.
+
+The forward pass is bit-exact, so both sides replay identical lists; only the order of the
+float atomics differs, hence the tolerance: relative L2 error <= 1e-3 per gradient array
+The reference goldens are also checked directly on the GPU
+result (rtol 1e-2 per component, test/backward_core.jl:149-155).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from tdgs_amd import host, synthetic
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+ARRAYS = ["mean3d", "opacity_feature", "scaling_features", "rotation_features", "sh"]
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64).reshape(-1)
+    b = np.asarray(b, np.float64).reshape(-1)
+    nb = np.linalg.norm(b)
+    return np.linalg.norm(a - b) / nb if nb > 0 else np.linalg.norm(a)
+
+
+def _run(core, orc, g_host, cam, t, opts, rgb_grad_fn):
+    ref = orc.render(g_host, cam, t, opts)
+    g = core.TrainableGaussiansVector.from_host(g_host, 0)
+    out = core.RenderOutputs.for_camera(cam, 0)
+    buf = core.RenderBuffers(len(g), t, 0)
+    core.render_(out, g, cam, t, opts, buf)
+    rgb = out.rgb
+    grad = rgb_grad_fn(rgb).float().contiguous()
+    fg = core.FilteredGaussiansGradientsVector(buf.capacity, g.sh_degree, 0)
+    core.backward_(fg, grad, out, g, cam, t, opts, buf)
+    torch.cuda.synchronize()
+    b = orc.backward(g_host, cam, t, opts, ref, grad.cpu().numpy())
+    nf = buf.nb_fgaussians
+    assert nf == ref["nb_fgaussians"]
+    got = {"grads2d": fg.grads2d[:nf], "mean3d": fg.mean3d[:nf], "opacity_feature": fg.opacity_feature[:nf],
+           "scaling_features": fg.scaling_features[:nf], "rotation_features": fg.rotation_features[:nf],
+           "sh": fg.sh[:nf]}
+    return {k: v.cpu().numpy() for k, v in got.items()}, b
+
+
+def _l1_grad(rgb):
+    return torch.where(rgb > 0.5, 1.0, -1.0) / rgb.numel()
+
+
+@pytest.mark.parametrize("deg", [0, 1, 2, 3])
+def test_backward_test_scene(gpu, oracle, deg):
+    g, cams = host.create_test_scene(sh_degree=deg)
+    cam = cams[0]
+    opts = host.RenderOptions.for_camera(cam, deg)
+    t = host.Tiling.for_camera(cam, 16, 16)
+    got, ref = _run(gpu, oracle, g, cam, t, opts, _l1_grad)
+    for k in ["grads2d"] + ARRAYS:
+        assert rel_l2(got[k], ref[k]) <= REL_L2, k
+    if deg in (0, 3):
+        gold = golden("backward_test_scene.json")["grads"][str(deg)]
+        for i in range(3):
+            for name, key, sl in (("means2d", "grads2d", slice(0, 2)), ("scaling_features", "scaling_features", None),
+                                  ("opacity_features", "opacity_feature", None)):
+                v = got[key][i] if sl is None else got[key][i, sl]
+                r = np.asarray(gold[name][i], np.float64)
+                np.testing.assert_allclose(np.atleast_1d(v), np.atleast_1d(r), rtol=1e-2)
+
+
+@pytest.mark.parametrize("cfg,n,tile,exact", [(1, 20_000, (16, 16), False), (1, 20_000, (16, 16), True),
+                                              (2, 60_000, (16, 32), False), (0, None, (16, 16), False)])
+def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact):
+    w = synthetic.config(cfg, n=n, cameras=2)
+    cam = w.cameras[-1]
+    t = host.Tiling.for_camera(cam, *tile)
+    opts = host.RenderOptions.for_camera(cam, w.gaussians.sh_degree, background_color=(0.2, 0.1, 0.3),
+                                         exact_sh_jacobian=exact)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+
+    def rand_grad(rgb):
+        return (torch.rand(rgb.shape, generator=gen, device=rgb.device) - 0.5) * 1e-3
+
+    got, ref = _run(gpu, oracle, w.gaussians, cam, t, opts, rand_grad)
+    for k in ["grads2d"] + ARRAYS:
+        assert rel_l2(got[k], ref[k]) <= REL_L2, (k, rel_l2(got[k], ref[k]))

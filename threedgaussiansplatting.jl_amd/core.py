@@ -344,3 +344,68 @@ def tile_ranges(sorted_keys: torch.Tensor, nb_tiles: int):
     te = torch.empty(nb_tiles, dtype=torch.int32, device=sorted_keys.device)
     check(lib().tdgs_tile_ranges(stream_ptr(dev), sorted_keys.numel(), dptr(sorted_keys), nb_tiles, dptr(te)))
     return te
+
+
+# ------------------------------------------------------------------------------------
+# backward!
+# ------------------------------------------------------------------------------------
+
+class FilteredGaussiansGradientsVector:
+    """FilteredGaussiansGradientsVector (src/backward_structs.jl:1-156): per filtered Gaussian
+    2D gradients (9 interleaved: mean2d 2, opacity 1, inverse covariance lower 3, colour 3)
+    and 3D gradients in the reference layouts."""
+
+    def __init__(self, capacity, sh_degree, device=0):
+        d = _dev(device)
+        cap = max(int(capacity), 1)
+        h = (int(sh_degree) + 1) ** 2
+        self.capacity = cap
+        self.sh_degree = int(sh_degree)
+        self.grads2d = torch.zeros((cap, 9), dtype=torch.float32, device=d)
+        self.mean3d = torch.zeros((cap, 3), dtype=torch.float32, device=d)
+        self.opacity_feature = torch.zeros(cap, dtype=torch.float32, device=d)
+        self.scaling_features = torch.zeros((cap, 3), dtype=torch.float32, device=d)
+        self.rotation_features = torch.zeros((cap, 4), dtype=torch.float32, device=d)
+        self.sh = torch.zeros((cap, 3, h), dtype=torch.float32, device=d)
+
+    @property
+    def mean2d(self):
+        return self.grads2d[:, 0:2]
+
+    @property
+    def opacity(self):
+        return self.grads2d[:, 2]
+
+    @property
+    def licov2d(self):
+        return self.grads2d[:, 3:6]
+
+    @property
+    def color(self):
+        return self.grads2d[:, 6:9]
+
+    def struct(self):
+        s = abi.GradientsC()
+        s.capacity = self.capacity
+        s.sh_degree = self.sh_degree
+        s.grads2d = dptr(self.grads2d)
+        s.mean3d = dptr(self.mean3d)
+        s.opacity_feature = dptr(self.opacity_feature)
+        s.scaling_features = dptr(self.scaling_features)
+        s.rotation_features = dptr(self.rotation_features)
+        s.sh = dptr(self.sh)
+        return s
+
+
+def backward_(fgradients: FilteredGaussiansGradientsVector, rgb_image_grad: torch.Tensor,
+              outputs: RenderOutputs, gaussians: TrainableGaussiansVector, camera: PinholeCamera,
+              tiling: Tiling, options: RenderOptions, buffers: RenderBuffers):
+    """backward! (src/backward_core.jl:37-72); uses the buffers of the preceding render_."""
+    dev = gaussians.device.index
+    assert rgb_image_grad.dtype == torch.float32 and rgb_image_grad.is_contiguous()
+    gr = fgradients.struct()
+    check(lib().tdgs_backward(stream_ptr(dev), C.byref(gr), C.c_void_p(dptr(rgb_image_grad)),
+                              C.byref(outputs.struct()), C.byref(gaussians.struct()),
+                              C.byref(camera.to_c()), C.byref(tiling.to_c()), C.byref(options.to_c()),
+                              C.byref(buffers.struct()), C.c_int32(buffers.nb_fgaussians)))
+    return fgradients

@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <vector>
+
 #include "internal.hpp"
 
 namespace tdgs {
@@ -25,6 +27,36 @@ int read_counters(tdgs_ctx* ctx, hipStream_t stream, int count) {
                             hipMemcpyDeviceToHost, stream));
     TDGS_HIP(hipStreamSynchronize(stream));
     return TDGS_OK;
+}
+
+// ---- stage profiler -------------------------------------------------------------------
+
+namespace {
+struct Profiler {
+    bool on = false;
+    int32_t max_records = 0;
+    std::vector<hipEvent_t> events;   // pool, two per record
+    std::vector<int> stages;          // stage of each started record
+    int open[TDGS_STAGE_COUNT];       // index of the open record per stage, -1 if none
+};
+thread_local Profiler g_prof;
+}  // namespace
+
+void profile_mark(int stage, bool start, hipStream_t stream) {
+    Profiler& p = g_prof;
+    if (!p.on || stage < 0 || stage >= TDGS_STAGE_COUNT) return;
+    if (start) {
+        const size_t rec = p.stages.size();
+        if ((int32_t)rec >= p.max_records) return;
+        p.stages.push_back(stage);
+        p.open[stage] = (int)rec;
+        (void)hipEventRecord(p.events[2 * rec], stream);
+    } else {
+        const int rec = p.open[stage];
+        if (rec < 0) return;
+        p.open[stage] = -1;
+        (void)hipEventRecord(p.events[2 * rec + 1], stream);
+    }
 }
 
 }  // namespace tdgs
@@ -91,6 +123,40 @@ int tdgs_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
 
 int tdgs_memset(void* dst, int value, size_t bytes, void* stream) {
     TDGS_HIP(hipMemsetAsync(dst, value, bytes, (hipStream_t)stream));
+    return TDGS_OK;
+}
+
+int tdgs_profile_begin(int32_t max_records) {
+    TDGS_REQUIRE(max_records > 0, "max_records must be positive");
+    Profiler& p = g_prof;
+    while ((int32_t)p.events.size() < 2 * max_records) {
+        hipEvent_t e;
+        TDGS_HIP(hipEventCreate(&e));
+        p.events.push_back(e);
+    }
+    p.max_records = max_records;
+    p.stages.clear();
+    for (int i = 0; i < TDGS_STAGE_COUNT; ++i) p.open[i] = -1;
+    p.on = true;
+    return TDGS_OK;
+}
+
+int tdgs_profile_end(double* ms_out, int64_t* executions_out) {
+    Profiler& p = g_prof;
+    TDGS_REQUIRE(p.on, "profiler not enabled");
+    p.on = false;
+    for (int i = 0; i < TDGS_STAGE_COUNT; ++i) {
+        if (ms_out) ms_out[i] = 0.0;
+        if (executions_out) executions_out[i] = 0;
+    }
+    for (size_t r = 0; r < p.stages.size(); ++r) {
+        TDGS_HIP(hipEventSynchronize(p.events[2 * r + 1]));
+        float ms = 0.0f;
+        TDGS_HIP(hipEventElapsedTime(&ms, p.events[2 * r], p.events[2 * r + 1]));
+        if (ms_out) ms_out[p.stages[r]] += ms;
+        if (executions_out) executions_out[p.stages[r]] += 1;
+    }
+    p.stages.clear();
     return TDGS_OK;
 }
 

@@ -138,28 +138,71 @@ struct SortedCounts {
     }
 };
 
-// One thread per Gaussian in depth order writes its keys, tiles row-major (x fastest).
-__global__ __launch_bounds__(256) void k_emit_depth_order(int64_t nbf, const int32_t* __restrict__ sorted_f,
-                                                          const int32_t* __restrict__ cs,
-                                                          const float* __restrict__ depths,
-                                                          const int32_t* __restrict__ ranges, int32_t ntx,
-                                                          int64_t* __restrict__ keys,
-                                                          int32_t* __restrict__ vals) {
-    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= nbf) return;
-    const int64_t end = cs[j];
-    int64_t d = j == 0 ? 0 : cs[j - 1];
-    if (d >= end) return;
-    const int32_t f = sorted_f[j];
-    const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
-    const int64_t low = (int64_t)float_bits(depths[f - 1]);
-    for (int32_t ty = r.y; ty <= r.w; ++ty) {
-        for (int32_t tx = r.x; tx <= r.z; ++tx) {
-            if (d >= end) return;
-            keys[d] = ((int64_t)(tx + (ty - 1) * ntx) << 32) | low;
-            vals[d] = f;
-            ++d;
+// Load-balanced key emission in depth order: one thread per output key. Each workgroup owns
+// kEmitTile consecutive keys; it finds the Gaussians (depth order) that produce them by two
+// binary searches on the inclusive count scan, stages their scan values in LDS, and every
+// key then finds its Gaussian by a binary search in LDS. Writes are fully coalesced. Within
+// a Gaussian, key number `local` is tile (x0 + local % wx, y0 + local / wx): tiles row-major,
+// x fastest, as the reference emits them (forward_core.jl:577-597).
+constexpr int kEmitThreads = 256;
+constexpr int kEmitItems = 8;
+constexpr int kEmitTile = kEmitThreads * kEmitItems;
+
+__device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, int64_t x) {
+    int64_t lo = 0, hi = n;  // first index with a[i] > x
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)a[mid] > x) hi = mid; else lo = mid + 1;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
+    int64_t nbf, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
+    const float* __restrict__ depths, const int32_t* __restrict__ ranges, int32_t ntx,
+    int64_t* __restrict__ keys, int32_t* __restrict__ vals) {
+    __shared__ int32_t s_cs[kEmitTile + 1];
+    __shared__ int64_t s_range[2];
+    const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
+    const int64_t d1 = (d0 + kEmitTile < m ? d0 + kEmitTile : m) - 1;  // last key of the block
+    if (threadIdx.x < 2) s_range[threadIdx.x] = upper_bound_i32(cs, nbf, threadIdx.x == 0 ? d0 : d1);
+    __syncthreads();
+    const int64_t j_lo = s_range[0];
+    const int64_t j_hi = s_range[1] < nbf ? s_range[1] : nbf - 1;
+    const int64_t cnt = j_hi - j_lo + 1;  // Gaussians spanned (each owns >= 1 key here)
+    const bool staged = cnt <= kEmitTile;
+    if (staged) {
+        for (int64_t k = threadIdx.x; k <= cnt; k += kEmitThreads) {
+            const int64_t j = j_lo + k - 1;
+            s_cs[k] = j < 0 ? 0 : cs[j];
         }
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (int it = 0; it < kEmitItems; ++it) {
+        const int64_t d = d0 + (int64_t)it * kEmitThreads + threadIdx.x;
+        if (d >= m) break;
+        int64_t j, start;
+        if (staged) {
+            int lo = 0, hi = (int)cnt;  // largest jj in [0, cnt) with s_cs[jj] <= d
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if ((int64_t)s_cs[mid] <= d) lo = mid; else hi = mid;
+            }
+            j = j_lo + lo;
+            start = s_cs[lo];
+        } else {
+            j = upper_bound_i32(cs, nbf, d);
+            start = j == 0 ? 0 : cs[j - 1];
+        }
+        const int32_t f = sorted_f[j];
+        const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
+        const int32_t wx = r.z - r.x + 1;
+        const int32_t local = (int32_t)(d - start);
+        const int32_t ty = r.y + local / wx;
+        const int32_t tx = r.x + local % wx;
+        keys[d] = ((int64_t)(tx + (ty - 1) * ntx) << 32) | (int64_t)float_bits(depths[f - 1]);
+        vals[d] = f;
     }
 }
 
@@ -546,9 +589,12 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     int64_t* d_m = ctx->d_counters + 1;
 
     // 1-2: keep flags and compaction
-    KeepEval ev{g->means_opacity, g->kind, *cam, *opt, keep};
-    TDGS_TRY(device_scan(ev, ItemsU8{keep}, CompactOut{buf->fgidx_to_gidx, nullptr}, n, stemp, sbytes,
-                         d_nbf, s));
+    {
+        StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
+        KeepEval ev{g->means_opacity, g->kind, *cam, *opt, keep};
+        TDGS_TRY(device_scan(ev, ItemsU8{keep}, CompactOut{buf->fgidx_to_gidx, nullptr}, n, stemp, sbytes,
+                             d_nbf, s));
+    }
     // 3: projection
     ProjectArgs pa;
     pa.g = *g; pa.cam = *cam; pa.tiling = *tiling; pa.opt = *opt;
@@ -556,14 +602,24 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
     pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
     pa.depth_keys = dkey; pa.depth_vals = dval;
-    k_project<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(pa);
-    TDGS_LAUNCHED();
+    {
+        StageScope sc(TDGS_STAGE_PROJECT, s);
+        k_project<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(pa);
+        TDGS_LAUNCHED();
+    }
     // 4: Gaussians by (depth bits, fgidx)
-    TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
-                                        rtemp, rbytes, s));
+    {
+        StageScope sc(TDGS_STAGE_DEPTH_SORT, s);
+        TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
+                                            rtemp, rbytes, s));
+    }
     // 5: tile counts in depth order -> M
-    TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nbf}, SortedCounts{sorted_f, buf->counts, d_nbf},
-                         WriteInclusiveI32{cs}, n, stemp, sbytes, d_m, s));
+    {
+        StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
+        TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nbf},
+                             SortedCounts{sorted_f, buf->counts, d_nbf}, WriteInclusiveI32{cs}, n, stemp, sbytes,
+                             d_m, s));
+    }
     TDGS_TRY(read_counters(ctx, s, 2));
     const int64_t nbf = ctx->h_counters[0];
     const int64_t m = ctx->h_counters[1];
@@ -585,16 +641,27 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     const bool emit_into_sorted = (passes % 2) == 0;
     int64_t* ek = emit_into_sorted ? buf->sorted_keys : buf->keys;
     int32_t* ev2 = emit_into_sorted ? buf->sorted_values : buf->values;
-    k_emit_depth_order<<<(unsigned)ceil_div(nbf, 256), 256, 0, s>>>(nbf, sorted_f, cs, buf->depths,
-                                                                    buf->tile_ranges, tiling->nb_tiles_x, ek, ev2);
-    TDGS_LAUNCHED();
-    TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2, buf->sorted_values,
-                                        (uint64_t*)buf->keys, buf->values, m, 32, eb, rtemp, rbytes, s));
+    {
+        StageScope sc(TDGS_STAGE_EMIT, s);
+        k_emit_depth_order<<<(unsigned)ceil_div(m, kEmitTile), kEmitThreads, 0, s>>>(
+            nbf, m, sorted_f, cs, buf->depths, buf->tile_ranges, tiling->nb_tiles_x, ek, ev2);
+        TDGS_LAUNCHED();
+    }
+    {
+        StageScope sc(TDGS_STAGE_TILE_SORT, s);
+        TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
+                                            buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, 32, eb,
+                                            rtemp, rbytes, s));
+    }
     // 8: tile ranges
     const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
-    k_tile_ranges<<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles, buf->tiles_end);
-    TDGS_LAUNCHED();
+    {
+        StageScope sc(TDGS_STAGE_TILE_RANGES, s);
+        k_tile_ranges<<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles, buf->tiles_end);
+        TDGS_LAUNCHED();
+    }
     // 9: blending
+    StageScope sc(TDGS_STAGE_BLEND, s);
     return launch_render_tiles(s, cam, tiling, opt, m, buf->tiles_end, buf->sorted_values, buf->f2d,
                                buf->depths, out);
 }

@@ -16,6 +16,16 @@ constexpr int kCounters = 8;
 // Copy the first count device counters to the host and wait for the stream.
 int read_counters(tdgs_ctx* ctx, hipStream_t stream, int count);
 
+// Stage profiler: records a start/stop HIP event pair around a stage when enabled.
+void profile_mark(int stage, bool start, hipStream_t stream);
+
+struct StageScope {
+    int stage;
+    hipStream_t stream;
+    StageScope(int st, hipStream_t s) : stage(st), stream(s) { profile_mark(stage, true, stream); }
+    ~StageScope() { profile_mark(stage, false, stream); }
+};
+
 inline int check_gaussians(const tdgs_gaussians* g, bool trainable_only) {
     TDGS_REQUIRE(g != nullptr, "gaussians is null");
     TDGS_REQUIRE(g->n >= 0, "negative Gaussian count %d", g->n);
