@@ -319,12 +319,12 @@ int tdgs_adc_plan(tdgs_ctx* ctx, void* stream, tdgs_adc_buffers* adc, const tdgs
                   float grad_threshold, float log_size_threshold, int32_t* n_new_out);
 
 /* adaptive_density_control! for parameters (gaussians.jl:1526-1694) and Adam moments
- * (optimizer.jl:1304-1378): fills dst (n_new Gaussians; new moments must be zeroed by the
- * caller beforehand or pass zero_moments = 1). Split means use a counter-based normal RNG
- * keyed by (seed, old index, draw). */
+ * (optimizer.jl:1304-1378): fills dst and dst_m (n_new Gaussians, every slot written: moments
+ * copied for carried-over Gaussians and first clones, zero for second clones and splits).
+ * Split means use a counter-based normal generator keyed by (seed, old index, draw). */
 int tdgs_adc_apply(void* stream, const tdgs_adc_buffers* adc, const tdgs_gaussians* src,
                    tdgs_gaussians* dst, const tdgs_adam_state* src_m, tdgs_adam_state* dst_m,
-                   float log_split_factor, uint64_t seed, int32_t zero_moments);
+                   float log_split_factor, uint64_t seed);
 
 /* adjust_fgidx_to_gidx_adc_kernel! (training.jl:514-541). */
 int tdgs_adc_remap_fgidx(void* stream, const tdgs_adc_buffers* adc, int32_t* fgidx_to_gidx,
@@ -336,16 +336,36 @@ int tdgs_adc_reset_stats(void* stream, tdgs_adc_buffers* adc, int32_t n);
 /* ---- training helpers ------------------------------------------------------------------ */
 
 /* L1 part of the loss and its gradient (training.jl:206-215):
- * grad = (rendered > gt ? w : -w) + dssim_weight * grad_in (grad_in may be null),
- * w = l1_weight / count. Writes sum |rendered - gt| into *l1_sum_dev (device float, may be
- * null). */
+ * grad = (rendered > gt ? w : -w) + dssim_weight * dssim_grad (dssim_grad may be null),
+ * w = l1_weight / count. Adds sum |rendered - gt| to *l1_sum_dev (device double, may be
+ * null; the caller zeroes it). */
 int tdgs_l1_loss_grad(void* stream, const float* rendered, const float* gt, int64_t count,
                       float l1_weight, float dssim_weight, const float* dssim_grad,
-                      float* grad_out, float* l1_sum_dev);
+                      float* grad_out, double* l1_sum_dev);
+
+/* Training loss of training_step! (training.jl:196-217) fused with its gradient:
+ * L = (1 - w) mean|K - I| + w DSSIM(K, I), DSSIM = 1 - SSIM (docs/src/math.md:125-126),
+ * SSIM with an 11 x 11 Gaussian window (sigma 1.5), C1 = 0.01^2, C2 = 0.03^2, zero padding,
+ * averaged over pixels and channels (replaces FastCUDASSIM.dssim_with_gradient!).
+ * Images are 3 x h x w. grad_out = dL/dK. sums_dev (device, 2 doubles, zeroed by the
+ * caller) receives sum|K - I| and the sum of the SSIM map: L = (1-w) s0/N + w (1 - s1/N)
+ * with N = 3 w h. temp holds tdgs_loss_temp_bytes(width, height) bytes. */
+size_t tdgs_loss_temp_bytes(int32_t width, int32_t height);
+int tdgs_loss_grad(void* stream, const float* rendered, const float* gt, int32_t width,
+                   int32_t height, float dssim_weight, float* grad_out, double* sums_dev,
+                   void* temp, size_t temp_bytes);
 
 /* reset_opacities! (gaussians.jl:1093-1101) + zero opacity moments (optimizer.jl:754-756). */
 int tdgs_opacity_reset(void* stream, tdgs_gaussians* g, float max_logit,
                        float* opacity_moments);
+
+/* resize_array for a spherical-harmonics degree change (misc.jl:100-125, used by
+ * set_sh_degree! in gaussians.jl:1070-1080 and optimizer.jl:737-747): copies the first
+ * min(h_src, h_dst) coefficients of every (channel, element) from src (interleave x h_src x
+ * 3 x n) to dst (interleave x h_dst x 3 x n) and zero-fills the rest. interleave is 1 for
+ * coefficients and gradients, 2 for Adam moments. */
+int tdgs_sh_resize(void* stream, const float* src, int32_t h_src, float* dst, int32_t h_dst,
+                   int64_t n, int32_t interleave);
 
 #ifdef __cplusplus
 }

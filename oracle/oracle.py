@@ -280,3 +280,81 @@ def normal_pair(seed, stream, pair):
     out = np.zeros(2, np.float32)
     lib().oracle_normal_pair(seed, stream, pair, ptr(out))
     return out
+
+
+class AdcHost:
+    """AdaptiveDensityControlBuffers (training_structs.jl:265-331) as host arrays."""
+
+    def __init__(self, n, new_capacity=None):
+        self.n = n
+        self.accum = np.zeros(n, np.float32)
+        self.counts = np.zeros(n, np.int32)
+        self.prune = np.zeros(n, np.uint8)
+        self.densify = np.zeros(n, np.uint8)
+        self.clone = np.zeros(n, np.uint8)
+        self.cs = np.zeros(n, np.int32)
+        self.new_capacity = new_capacity or 2 * n
+        self.ngidx = np.zeros(self.new_capacity, np.int32)
+
+    def struct(self):
+        abi = _abi()
+        s = abi.AdcBuffersC()
+        s.capacity = self.n
+        s.new_capacity = self.new_capacity
+        s.accum_grad_norms = self.accum.ctypes.data
+        s.contribution_counts = self.counts.ctypes.data
+        s.prune = self.prune.ctypes.data
+        s.densify = self.densify.ctypes.data
+        s.clone = self.clone.ctypes.data
+        s.new_counts_cs = self.cs.ctypes.data
+        s.ngidx_to_gidx = self.ngidx.ctypes.data
+        return s
+
+
+def adc_stats(adc: AdcHost, grads2d, fgidx_to_gidx, width, height):
+    s = adc.struct()
+    g2 = np.ascontiguousarray(grads2d, np.float32)
+    f2g = np.ascontiguousarray(fgidx_to_gidx, np.int32)
+    lib().oracle_adc_stats(C.byref(s), ptr(g2), ptr(f2g), C.c_int32(len(f2g)), C.c_int32(width),
+                           C.c_int32(height))
+
+
+def adc_plan(adc: AdcHost, g, prune_logit, use_max_scale, log_max_scale, grad_threshold, log_size_threshold):
+    s = adc.struct()
+    return lib().oracle_adc_plan(C.byref(s), C.byref(gaussians_struct(g)), C.c_float(prune_logit),
+                                 C.c_int32(int(use_max_scale)), C.c_float(log_max_scale),
+                                 C.c_float(grad_threshold), C.c_float(log_size_threshold))
+
+
+def adc_apply(adc: AdcHost, g, adam: AdamHost, log_split_factor, seed):
+    """Returns (new HostGaussians, new AdamHost)."""
+    from importlib import import_module
+    host = import_module(__package_root__() + ".host")
+    n_new = int(adc.cs[g.n - 1]) if g.n else 0
+    h = (g.sh_degree + 1) ** 2
+    ng = host.HostGaussians(np.zeros((n_new, 4), np.float32), np.zeros((n_new, 3), np.float32),
+                            np.zeros((n_new, 4), np.float32), np.zeros((n_new, 3, h), np.float32))
+    nm = AdamHost(n_new, g.sh_degree, adam.lrs, adam.beta1, adam.beta2, adam.epsilon, adam.update_count)
+    s = adc.struct()
+    lib().oracle_adc_apply(C.byref(s), C.byref(gaussians_struct(g)), C.byref(gaussians_struct(ng)),
+                           C.byref(adam.struct()), C.byref(nm.struct()), C.c_float(log_split_factor),
+                           C.c_uint64(seed))
+    return ng, nm
+
+
+def adc_remap_fgidx(adc: AdcHost, fgidx_to_gidx):
+    f2g = np.ascontiguousarray(fgidx_to_gidx, np.int32).copy()
+    lib().oracle_adc_remap_fgidx(C.byref(adc.struct()), ptr(f2g), C.c_int32(len(f2g)))
+    return f2g
+
+
+def l1_loss_grad(rendered, gt, l1_weight, dssim_weight=0.0, dssim_grad=None):
+    r = np.ascontiguousarray(rendered, np.float32)
+    g = np.ascontiguousarray(gt, np.float32)
+    out = np.zeros_like(r)
+    dg = None if dssim_grad is None else np.ascontiguousarray(dssim_grad, np.float32)
+    L = lib()
+    L.oracle_l1_loss_grad.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_float, C.c_float, C.c_void_p,
+                                      C.c_void_p]
+    s = L.oracle_l1_loss_grad(ptr(r), ptr(g), r.size, l1_weight, dssim_weight, ptr(dg), ptr(out))
+    return s, out

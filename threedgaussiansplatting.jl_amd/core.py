@@ -46,8 +46,10 @@ def lib():
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
         L = C.CDLL(LIB_PATH)
         L.tdgs_last_error.restype = C.c_char_p
-        for name in ("tdgs_scan_temp_bytes", "tdgs_sort_pairs_temp_bytes", "tdgs_render_temp_bytes"):
+        for name in ("tdgs_scan_temp_bytes", "tdgs_sort_pairs_temp_bytes", "tdgs_render_temp_bytes",
+                     "tdgs_loss_temp_bytes"):
             getattr(L, name).restype = C.c_size_t
+        L.tdgs_loss_temp_bytes.argtypes = [C.c_int32, C.c_int32]
         L.tdgs_scan_temp_bytes.argtypes = [C.c_int64]
         L.tdgs_sort_pairs_temp_bytes.argtypes = [C.c_int32, C.c_int32]
         L.tdgs_render_temp_bytes.argtypes = [C.c_int32, C.c_int64, C.c_void_p]

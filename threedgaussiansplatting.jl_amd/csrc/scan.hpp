@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_reduce(In in, int64_t n, 
 }
 
 // Single block: exclusive scan of the tile sums in place; grand total to *total_out.
-__global__ __launch_bounds__(kScanThreads) void k_scan_tiles(int64_t* tile_sums, int64_t ntiles,
+static __global__ __launch_bounds__(kScanThreads) void k_scan_tiles(int64_t* tile_sums, int64_t ntiles,
                                                              int64_t* total_out) {
     int64_t carry = 0;
     for (int64_t start = 0; start < ntiles; start += (int64_t)kScanThreads * kScanItems) {

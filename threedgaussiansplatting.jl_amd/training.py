@@ -1,0 +1,375 @@
+"""Host-side mirror of the reference's optimiser, densification and trainer over libtdgs.so.
+
+Reference: src/optimizer.jl (GaussianAdamMomentsLearningRatesVector :9-195, AdamOptimizer
+:761-854, update! :964-1009, ADC of moments :1304-1378), src/training_structs.jl
+(TrainingOptions :10-228, ADC buffers :265-468), src/training.jl (Trainer :40-151,
+training_step! :173-244, ADC :313-580), src/gaussians.jl:1070-1101, 1526-1694.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import abi
+from .core import (FilteredGaussiansGradientsVector, RenderBuffers, RenderOutputs, TrainableGaussiansVector,
+                   _dev, backward_, check, context, dptr, lib, render_, stream_ptr)
+from .host import PinholeCamera, RenderOptions, Tiling, logit32
+
+f32 = np.float32
+
+# src/optimizer.jl:831-833
+DEFAULT_BETA1 = 0.9
+DEFAULT_BETA2 = 0.999
+DEFAULT_EPSILON = 1e-15
+
+
+@dataclass
+class TrainingOptions:
+    """TrainingOptions with the 3DGS defaults (training_structs.jl:43-85, 139-228); the
+    'base' learning rate and size thresholds are scaled by the scene radius."""
+    nb_iterations: int = 30_000
+    loss_dssim_vs_L1_weight: float = 0.2
+    initial_means_lr: float = 0.00016
+    final_means_lr: float = 0.0000016
+    opacity_features_lr: float = 0.05
+    scaling_features_lr: float = 0.005
+    rotation_features_lr: float = 0.001
+    sh_coeffs_dc_lr: float = 0.0025
+    sh_coeffs_rest_lr: float = 0.0025 / 20
+    nb_lr_annealing_steps: int = 30_000
+    sh_degree_increase_interval: int = 1_000
+    opacity_reset_interval: int = 3_000
+    opacity_reset_start_iteration_nb: int = 0
+    opacity_reset_final_iteration_nb: int = 12_000
+    opacity_reset_max_value: float = 0.01
+    adc_interval: int = 100
+    adc_start_iteration_nb: int = 600
+    adc_final_iteration_nb: int = 14_900
+    densification_mean2d_grad_norm_threshold_ndc: float = 0.0002
+    densification_size_threshold: float = 0.01
+    splitting_scale_factor: float = 1 / (0.8 * 2)
+    pruning_min_opacity: float = 0.005
+    pruning_3d_max_scale: float = 0.1
+
+    @classmethod
+    def for_scene(cls, scene_radius: float, **kw):
+        nb = kw.get("nb_iterations", 30_000)
+        base_lr = kw.pop("base_initial_means_lr", 0.00016)
+        base_final = kw.pop("base_final_means_lr", base_lr / 100.0)
+        dc = kw.get("sh_coeffs_dc_lr", 0.0025)
+        kw.setdefault("sh_coeffs_rest_lr", dc / 20.0)
+        kw.setdefault("nb_lr_annealing_steps", nb)
+        size = kw.pop("base_densification_size_threshold", 0.01)
+        prune_scale = kw.pop("base_pruning_3d_max_scale", 0.1)
+        R = float(f32(scene_radius))
+        return cls(initial_means_lr=float(f32(base_lr) * f32(R)), final_means_lr=float(f32(base_final) * f32(R)),
+                   densification_size_threshold=float(f32(size) * f32(R)),
+                   pruning_3d_max_scale=float(f32(prune_scale) * f32(R)), **kw)
+
+
+class GaussianAdamMomentsLearningRatesVector:
+    """Adam moments (m1, m2 interleaved) and learning rates (optimizer.jl:9-195)."""
+
+    def __init__(self, n, sh_degree, lrs, device=0):
+        d = _dev(device)
+        h = (sh_degree + 1) ** 2
+        self.sh_degree = int(sh_degree)
+        self.means = torch.zeros((n, 3, 2), dtype=torch.float32, device=d)
+        self.opacity = torch.zeros((n, 2), dtype=torch.float32, device=d)
+        self.scaling = torch.zeros((n, 3, 2), dtype=torch.float32, device=d)
+        self.rotation = torch.zeros((n, 4, 2), dtype=torch.float32, device=d)
+        self.sh = torch.zeros((n, 3, h, 2), dtype=torch.float32, device=d)
+        (self.means_lr, self.opacity_lr, self.scaling_lr, self.rotation_lr, self.sh_dc_lr,
+         self.sh_rest_lr) = [float(v) for v in lrs]
+
+    def __len__(self):
+        return self.means.shape[0]
+
+    def lrs(self):
+        return [self.means_lr, self.opacity_lr, self.scaling_lr, self.rotation_lr, self.sh_dc_lr, self.sh_rest_lr]
+
+
+class AdamOptimizer:
+    """MutableAdamOptimizer (optimizer.jl:761-854)."""
+
+    def __init__(self, gaussians: TrainableGaussiansVector, options: TrainingOptions, beta1=DEFAULT_BETA1,
+                 beta2=DEFAULT_BETA2, epsilon=DEFAULT_EPSILON, update_count=0):
+        self.gaussians = gaussians
+        lrs = [options.initial_means_lr, options.opacity_features_lr, options.scaling_features_lr,
+               options.rotation_features_lr, options.sh_coeffs_dc_lr, options.sh_coeffs_rest_lr]
+        self.moments = GaussianAdamMomentsLearningRatesVector(len(gaussians), gaussians.sh_degree, lrs,
+                                                              gaussians.device.index)
+        self.beta1, self.beta2, self.epsilon = float(f32(beta1)), float(f32(beta2)), float(f32(epsilon))
+        self.update_count = int(update_count)
+
+    def struct(self):
+        m = self.moments
+        s = abi.AdamStateC()
+        s.means_moments = dptr(m.means)
+        s.opacity_moments = dptr(m.opacity)
+        s.scaling_moments = dptr(m.scaling)
+        s.rotation_moments = dptr(m.rotation)
+        s.sh_moments = dptr(m.sh)
+        (s.lr_means, s.lr_opacity, s.lr_scaling, s.lr_rotation, s.lr_sh_dc, s.lr_sh_rest) = m.lrs()
+        s.beta1, s.beta2, s.epsilon = self.beta1, self.beta2, self.epsilon
+        s.update_count = self.update_count
+        return s
+
+    def update_(self, fgradients: FilteredGaussiansGradientsVector, fgidx_to_gidx: torch.Tensor,
+                nb_fgaussians: int, sh_degree: int):
+        """update!(opt, fgradients, Val(sh_degree)) (optimizer.jl:964-1009)."""
+        g = self.gaussians
+        st = self.struct()
+        check(lib().tdgs_adam_step(stream_ptr(g.device.index), C.byref(g.struct()), C.byref(st),
+                                   C.byref(fgradients.struct()), C.c_void_p(dptr(fgidx_to_gidx)),
+                                   C.c_int32(nb_fgaussians), C.c_int32(sh_degree)))
+        self.update_count = st.update_count
+        return g
+
+
+class AdaptiveDensityControlBuffers:
+    """AdaptiveDensityControlBuffers (training_structs.jl:265-331)."""
+
+    def __init__(self, n, device=0):
+        d = _dev(device)
+        cap = max(int(n), 1)
+        self.capacity = cap
+        self.accum = torch.zeros(cap, dtype=torch.float32, device=d)
+        self.counts = torch.zeros(cap, dtype=torch.int32, device=d)
+        self.prune = torch.zeros(cap, dtype=torch.uint8, device=d)
+        self.densify = torch.zeros(cap, dtype=torch.uint8, device=d)
+        self.clone = torch.zeros(cap, dtype=torch.uint8, device=d)
+        self.cs = torch.zeros(cap, dtype=torch.int32, device=d)
+        self.new_capacity = 2 * cap
+        self.ngidx = torch.zeros(self.new_capacity, dtype=torch.int32, device=d)
+        self.temp = torch.empty(int(lib().tdgs_scan_temp_bytes(cap)), dtype=torch.uint8, device=d)
+
+    def struct(self):
+        s = abi.AdcBuffersC()
+        s.capacity = self.capacity
+        s.new_capacity = self.new_capacity
+        s.accum_grad_norms = dptr(self.accum)
+        s.contribution_counts = dptr(self.counts)
+        s.prune = dptr(self.prune)
+        s.densify = dptr(self.densify)
+        s.clone = dptr(self.clone)
+        s.new_counts_cs = dptr(self.cs)
+        s.ngidx_to_gidx = dptr(self.ngidx)
+        s.temp = dptr(self.temp)
+        s.temp_bytes = self.temp.numel()
+        return s
+
+
+def adc_stats_(adc: AdaptiveDensityControlBuffers, fgradients, fgidx_to_gidx, nb_fgaussians, camera):
+    """update_adc_stats_kernel! (training.jl:472-497)."""
+    dev = adc.accum.device.index
+    check(lib().tdgs_adc_stats(stream_ptr(dev), C.byref(adc.struct()), C.byref(fgradients.struct()),
+                               C.c_void_p(dptr(fgidx_to_gidx)), C.c_int32(nb_fgaussians),
+                               C.c_int32(camera.width), C.c_int32(camera.height)))
+
+
+def adc_plan_(adc, gaussians, prune_logit, use_max_scale, log_max_scale, grad_threshold, log_size_threshold):
+    """Masks, counts scan and ngidx_to_gidx (training.jl:325-397); returns the new count."""
+    dev = gaussians.device.index
+    nn = C.c_int32(0)
+    check(lib().tdgs_adc_plan(context(dev), stream_ptr(dev), C.byref(adc.struct()), C.byref(gaussians.struct()),
+                              C.c_float(prune_logit), C.c_int32(int(use_max_scale)), C.c_float(log_max_scale),
+                              C.c_float(grad_threshold), C.c_float(log_size_threshold), C.byref(nn)))
+    return int(nn.value)
+
+
+def adaptive_density_control_(adc, gaussians: TrainableGaussiansVector, optimizer: AdamOptimizer, n_new,
+                              log_split_factor, seed):
+    """adaptive_density_control! on parameters and moments (gaussians.jl:1526-1694,
+    optimizer.jl:1304-1378): returns the new Gaussians; the optimizer is updated in place."""
+    dev = gaussians.device
+    h = (gaussians.sh_degree + 1) ** 2
+    new = TrainableGaussiansVector(torch.empty((n_new, 4), dtype=torch.float32, device=dev),
+                                   torch.empty((n_new, 3), dtype=torch.float32, device=dev),
+                                   torch.empty((n_new, 4), dtype=torch.float32, device=dev),
+                                   torch.empty((n_new, 3, h), dtype=torch.float32, device=dev))
+    old_m = optimizer.moments
+    new_m = GaussianAdamMomentsLearningRatesVector(n_new, gaussians.sh_degree, old_m.lrs(), dev.index)
+    src_m, dst_m = optimizer.struct(), None
+    optimizer.moments = new_m
+    dst_m = optimizer.struct()
+    check(lib().tdgs_adc_apply(stream_ptr(dev.index), C.byref(adc.struct()), C.byref(gaussians.struct()),
+                               C.byref(new.struct()), C.byref(src_m), C.byref(dst_m), C.c_float(log_split_factor),
+                               C.c_uint64(seed)))
+    torch.cuda.current_stream(dev).synchronize()  # old arrays may be released after this point
+    del old_m
+    optimizer.gaussians = new
+    return new
+
+
+def adc_remap_fgidx_(adc, fgidx_to_gidx, nb_fgaussians):
+    """adjust_fgidx_to_gidx_adc_kernel! (training.jl:514-541)."""
+    dev = fgidx_to_gidx.device.index
+    check(lib().tdgs_adc_remap_fgidx(stream_ptr(dev), C.byref(adc.struct()), C.c_void_p(dptr(fgidx_to_gidx)),
+                                     C.c_int32(nb_fgaussians)))
+
+
+def l1_loss_grad_(rendered, gt, grad_out, l1_weight, dssim_weight=0.0, dssim_grad=None, l1_sum=None):
+    """L1 part of training_step!'s loss and its gradient (training.jl:206-215)."""
+    dev = rendered.device.index
+    check(lib().tdgs_l1_loss_grad(stream_ptr(dev), C.c_void_p(dptr(rendered)), C.c_void_p(dptr(gt)),
+                                  C.c_int64(rendered.numel()), C.c_float(l1_weight), C.c_float(dssim_weight),
+                                  C.c_void_p(dptr(dssim_grad)), C.c_void_p(dptr(grad_out)),
+                                  C.c_void_p(dptr(l1_sum))))
+
+
+def opacity_reset_(gaussians, max_value, opacity_moments):
+    """reset_opacities! + zero_opacity_features_adam_moments! (gaussians.jl:1093-1101)."""
+    check(lib().tdgs_opacity_reset(stream_ptr(gaussians.device.index), C.byref(gaussians.struct()),
+                                   C.c_float(float(logit32(max_value))), C.c_void_p(dptr(opacity_moments))))
+
+
+def sh_resize(src: torch.Tensor, new_degree: int, interleave: int):
+    """resize_array for a new SH degree (misc.jl:100-125): src is (n, 3, h[, 2])."""
+    n = src.shape[0]
+    hs = src.shape[2]
+    hd = (int(new_degree) + 1) ** 2
+    shape = (n, 3, hd) + ((2,) if interleave == 2 else ())
+    dst = torch.empty(shape, dtype=torch.float32, device=src.device)
+    check(lib().tdgs_sh_resize(stream_ptr(src.device.index), C.c_void_p(dptr(src)), C.c_int32(hs),
+                               C.c_void_p(dptr(dst)), C.c_int32(hd), C.c_int64(n), C.c_int32(interleave)))
+    return dst
+
+
+def loss_grad_(rendered, gt, grad_out, dssim_weight, sums, temp):
+    """L1 + DSSIM loss gradient (training.jl:196-217); sums (2 doubles) must be zeroed."""
+    W, H = rendered.shape[0], rendered.shape[1]
+    check(lib().tdgs_loss_grad(stream_ptr(rendered.device.index), C.c_void_p(dptr(rendered)),
+                               C.c_void_p(dptr(gt)), C.c_int32(W), C.c_int32(H), C.c_float(dssim_weight),
+                               C.c_void_p(dptr(grad_out)), C.c_void_p(dptr(sums)), C.c_void_p(dptr(temp)),
+                               C.c_size_t(temp.numel())))
+
+
+class Trainer:
+    """Trainer (training.jl:40-151) with training_step_ = training_step! (:173-244).
+
+    images[k] is the ground-truth image of cameras[k] as a (w, h, 3) float32 device tensor
+    (the reference's 3 x h x w layout). The camera order is a seeded permutation, redrawn
+    after every pass over the cameras (the reference uses an unseeded randperm!)."""
+
+    def __init__(self, gaussians: TrainableGaussiansVector, cameras, images, render_options: RenderOptions,
+                 tiling: Tiling, training_options: TrainingOptions, optimizer: AdamOptimizer | None = None,
+                 seed: int = 0, device=0):
+        self.device = _dev(device)
+        self.gaussians = gaussians
+        self.cameras = list(cameras)
+        self.images = list(images)
+        self.render_options = render_options
+        self.tiling = tiling
+        self.options = training_options
+        self.optimizer = optimizer or AdamOptimizer(gaussians, training_options)
+        self.rng = np.random.Generator(np.random.PCG64(seed))
+        self.seed = seed
+        self.iteration_nb = 0
+        self.cameras_order = self.rng.permutation(len(self.cameras))
+        self.cameras_order_idx = -1
+        cam0 = self.cameras[0]
+        self.render_outputs = RenderOutputs.for_camera(cam0, device, include_rgb=True, include_transmittance=True,
+                                                       include_depth=False, include_last_contributing_indices=True)
+        self.render_buffers = RenderBuffers(len(gaussians), tiling, device)
+        self.fgradients = FilteredGaussiansGradientsVector(len(gaussians), gaussians.sh_degree, device)
+        self.adc = AdaptiveDensityControlBuffers(len(gaussians), device)
+        self.rgb_image_grad = torch.empty_like(self.render_outputs.rgb)
+        self.loss_sums = torch.zeros(2, dtype=torch.float64, device=self.device)
+        self.loss_temp = torch.empty(int(lib().tdgs_loss_temp_bytes(cam0.width, cam0.height)), dtype=torch.uint8,
+                                     device=self.device)
+        self.last_camera = None
+
+    def current_loss(self):
+        """Loss of the last step (synchronises): (1-w) mean L1 + w (1 - mean SSIM)."""
+        s = self.loss_sums.cpu().numpy()
+        n = self.render_outputs.rgb.numel()
+        w = self.options.loss_dssim_vs_L1_weight
+        return (1 - w) * s[0] / n + w * (1 - s[1] / n)
+
+    def training_step_(self):
+        """training_step! (training.jl:173-244)."""
+        self.iteration_nb += 1
+        self.cameras_order_idx += 1
+        if self.cameras_order_idx >= len(self.cameras_order):
+            self.cameras_order = self.rng.permutation(len(self.cameras))
+            self.cameras_order_idx = 0
+        self.maybe_increase_sh_degree_()
+        k = int(self.cameras_order[self.cameras_order_idx])
+        cam = self.cameras[k]
+        self.last_camera = cam
+        render_(self.render_outputs, self.gaussians, cam, self.tiling, self.render_options, self.render_buffers)
+        self.loss_sums.zero_()
+        loss_grad_(self.render_outputs.rgb, self.images[k], self.rgb_image_grad,
+                   self.options.loss_dssim_vs_L1_weight, self.loss_sums, self.loss_temp)
+        backward_(self.fgradients, self.rgb_image_grad, self.render_outputs, self.gaussians, cam, self.tiling,
+                  self.render_options, self.render_buffers)
+        in_adc = self.maybe_densify_and_prune_()
+        self.update_learning_rates_()
+        self.optimizer.update_(self.fgradients, self.render_buffers.fgidx_to_gidx, self.render_buffers.nb_fgaussians,
+                               self.render_options.sh_degree)
+        if in_adc:
+            self.complete_adc_step_()
+        self.maybe_opacity_reset_()
+
+    def maybe_increase_sh_degree_(self):
+        """maybe_increase_sh_degree! (training.jl:253-263)."""
+        if self.iteration_nb % self.options.sh_degree_increase_interval != 0:
+            return
+        d = self.gaussians.sh_degree
+        if d >= 3:
+            return
+        d += 1
+        self.render_options = self.render_options.with_sh_degree(d)
+        self.gaussians.sh = sh_resize(self.gaussians.sh, d, 1)
+        self.fgradients.sh = sh_resize(self.fgradients.sh, d, 1)
+        self.fgradients.sh_degree = d
+        m = self.optimizer.moments
+        m.sh = sh_resize(m.sh, d, 2)
+        m.sh_degree = d
+
+    def maybe_opacity_reset_(self):
+        """maybe_opacity_reset! (training.jl:272-280)."""
+        o = self.options
+        it = self.iteration_nb
+        if o.opacity_reset_start_iteration_nb <= it <= o.opacity_reset_final_iteration_nb and \
+                it % o.opacity_reset_interval == 0:
+            opacity_reset_(self.gaussians, o.opacity_reset_max_value, self.optimizer.moments.opacity)
+
+    def update_learning_rates_(self):
+        """update_learning_rates! (training.jl:287-302), log-linear in float32."""
+        o = self.options
+        x = f32(min(max((self.iteration_nb - 1) / f32(o.nb_lr_annealing_steps - 1), 0.0), 1.0))
+        lr = np.exp(f32(f32(1 - x) * np.log(f32(o.initial_means_lr)) + x * np.log(f32(o.final_means_lr))))
+        self.optimizer.moments.means_lr = float(f32(lr))
+
+    def maybe_densify_and_prune_(self):
+        """maybe_densify_and_prune! (training.jl:313-444); True when an ADC step ran."""
+        o = self.options
+        it = self.iteration_nb
+        if it > o.adc_final_iteration_nb:
+            return False
+        nbf = self.render_buffers.nb_fgaussians
+        adc_stats_(self.adc, self.fgradients, self.render_buffers.fgidx_to_gidx, nbf, self.last_camera)
+        if not (it >= o.adc_start_iteration_nb and it % o.adc_interval == 0):
+            return False
+        n_new = adc_plan_(self.adc, self.gaussians, float(logit32(o.pruning_min_opacity)),
+                          it > o.opacity_reset_interval, float(np.log(f32(o.pruning_3d_max_scale))),
+                          o.densification_mean2d_grad_norm_threshold_ndc,
+                          float(np.log(f32(o.densification_size_threshold))))
+        new = adaptive_density_control_(self.adc, self.gaussians, self.optimizer, n_new,
+                                        float(np.log(f32(o.splitting_scale_factor))), self.seed * 1_000_003 + it)
+        adc_remap_fgidx_(self.adc, self.render_buffers.fgidx_to_gidx, nbf)
+        self.gaussians = new
+        self.adc = AdaptiveDensityControlBuffers(n_new, self.device.index)
+        return True
+
+    def complete_adc_step_(self):
+        """complete_adc_step! (training.jl:455-459): resize gradients and render buffers."""
+        n = len(self.gaussians)
+        self.fgradients = FilteredGaussiansGradientsVector(n, self.gaussians.sh_degree, self.device.index)
+        self.render_buffers.ensure_capacity(n)
