@@ -31,6 +31,10 @@ __graft_entry__.load_package()
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3       # MI355X vector FP32 (published)
 
+# FLOP of one (pixel, sorted entry) evaluation of the blending loop: exponent 5 FMA (10),
+# exp 19, min/1-alpha/T(1-alpha)/weight 4, colour 3 FMA (6) (contributing evaluations).
+BLEND_FLOP_PER_EVALUATION = 39
+
 STAGES = ["cull_compact", "project", "depth_sort", "count_scan", "emit", "tile_sort", "tile_ranges",
           "blend", "backward_blend", "backward_project", "adam", "adc", "loss"]
 
@@ -41,22 +45,86 @@ def parse():
     p.add_argument("--steps", type=int, default=600)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", type=int, default=2)
+    p.add_argument("--train-steps", type=int, default=100)
+    p.add_argument("--train-warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=0)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run 10 device-to-device copies of 1 GiB (HBM counter calibration)")
     return p.parse_args()
 
 
-def frame_stats(core, g, cams, tiling, opts, outputs, buffers, idx):
-    """N_f, N_b, M for the given cameras (untimed pass)."""
+def copy_calibration():
+    """Known-size traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE: each copy reads and
+    writes exactly 1 GiB."""
     import torch
+    src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_each": 1 << 30, "copies": 10}))
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 counter summary
+    (profiles/hbm_traffic.json, written from two --pmc runs), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    k = t.get("kernels", {}).get(kernel)
+    return None if k is None else k.get("bytes_per_launch")
+
+
+def frame_stats(core, g, cams, tiling, opts, outputs, buffers, idx):
+    """N_f, N_b, M and blending evaluations E for the given cameras (untimed pass)."""
+    import torch
+    L = core.lib()
+    ev = torch.zeros(1, dtype=torch.int64, device="cuda")
     st = []
     for k in idx:
         core.render_(outputs, g, cams[k], tiling, opts, buffers)
         nf = buffers.nb_fgaussians
         nb = int((buffers.counts[:nf] > 0).sum().item())
-        st.append((nf, nb, buffers.nb_keys))
+        ev.zero_()
+        core.check(L.tdgs_blend_evaluations(core.stream_ptr(0), C.byref(cams[k].to_c()), C.byref(tiling.to_c()),
+                                            C.byref(opts.to_c()), C.byref(buffers.struct()),
+                                            C.c_int64(buffers.nb_keys), C.c_void_p(ev.data_ptr())))
+        st.append((nf, nb, buffers.nb_keys, int(ev.item())))
     torch.cuda.synchronize()
     return np.array(st, dtype=np.float64)
+
+
+def train_bench(core, w, cams, tiling, deg, steps, warmup):
+    """Training steps (training_step!: render, L1 + DSSIM loss, backward, ADC statistics,
+    learning-rate annealing, Adam) on the same workload, at iterations before the first
+    densification (iteration 600), against seeded uniform-noise target images."""
+    import torch
+    from tdgs_amd import host, training
+    g = core.TrainableGaussiansVector.from_host(w.gaussians, 0)
+    gen = torch.Generator(device="cuda").manual_seed(0x3D6501)
+    images = [torch.rand((c.width, c.height, 3), generator=gen, device="cuda") for c in cams]
+    opts = host.RenderOptions.for_camera(cams[0], deg)
+    to = training.TrainingOptions.for_scene(host.scene_radius(cams), sh_degree_increase_interval=10**9)
+    tr = training.Trainer(g, cams, images, opts, tiling, to, seed=1)
+    for _ in range(warmup):
+        tr.training_step_()
+    torch.cuda.synchronize()
+    L = core.lib()
+    core.check(L.tdgs_profile_begin(C.c_int32(16 * steps + 64)))
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tr.training_step_()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (C.c_double * 13)()
+    cnt = (C.c_int64 * 13)()
+    core.check(L.tdgs_profile_end(ms, cnt))
+    assert tr.iteration_nb < to.adc_start_iteration_nb
+    stage = {STAGES[i]: round(ms[i] / steps, 4) for i in range(13) if cnt[i] > 0}
+    return steps / (t1 - t0), (t1 - t0) * 1000.0 / steps, stage, tr.current_loss()
 
 
 def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles):
@@ -82,6 +150,9 @@ def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles):
 
 def main():
     args = parse()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by "
               "views or image bands, see DESIGN.md)", file=sys.stderr)
@@ -128,7 +199,7 @@ def main():
     used = sorted({k % ncam for k in range(args.steps)})
     st = frame_stats(core, g, cams, tiling, opts, out, buf, used)
     n = len(g)
-    nf, nb, m = st.mean(axis=0)
+    nf, nb, m, evals = st.mean(axis=0)
     npx = cam0.width * cam0.height
     h = (deg + 1) ** 2
     stage_ms = {STAGES[i]: ms[i] / cnt[i] for i in range(13) if cnt[i] > 0}
@@ -141,8 +212,15 @@ def main():
     b_dom = algorithmic_bytes(dom, n, nf, nb, m, npx, h, tiling.nb_tiles)
     achieved = b_dom / (stage_ms[dom] * 1e-3) / 1e9
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
                 "algorithmic_bytes_per_launch": int(b_dom), "mean_launch_ms": round(stage_ms[dom], 4)}
+    if dom == "blend":
+        flop = BLEND_FLOP_PER_EVALUATION * evals
+        tflops = flop / (stage_ms[dom] * 1e-3) / 1e12
+        if tflops / FP32_PEAK_TFLOPS > roofline["frac"]:
+            roofline.update({"bound": "valu", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+                             "algorithmic_flop_per_launch": int(flop), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)})
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -158,6 +236,12 @@ def main():
                "sample": f"1 frame (camera 0) of the same workload with the reference CPU renderer "
                          f"(forward_core.jl:25-177) restated in C++, {threads} threads by image columns"}
 
+    train = None
+    if args.train_steps > 0:
+        its, ms_it, tstage, loss = train_bench(core, w, cams, tiling, deg, args.train_steps, args.train_warmup)
+        train = {"train_it_per_s": round(its, 2), "ms_per_iteration": round(ms_it, 4), "steps": args.train_steps,
+                 "stage_ms": tstage, "loss_last": round(float(loss), 6)}
+
     res = {
         "metric": "render fps + train it/s at 1M Gaussians 1080p SH3 (1 GPU); % HBM roofline",
         "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
@@ -167,7 +251,9 @@ def main():
                    "sh_degree": deg, "tile": list(w.tile), "cameras": ncam, "outputs": "rgb+T"},
         "frame_ms_p50": round(float(np.percentile(frame_ms, 50)), 4),
         "frame_ms_p99": round(float(np.percentile(frame_ms, 99)), 4),
-        "mean_counts": {"filtered": round(nf), "nonempty": round(nb), "keys": round(m)},
+        "mean_counts": {"filtered": round(nf), "nonempty": round(nb), "keys": round(m),
+                        "blend_evaluations": round(evals)},
+        "train": train,
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
         "stage_algorithmic_GBs": {k: round(v, 1) for k, v in stage_gbs.items()},
         "roofline": roofline,

@@ -273,6 +273,7 @@ struct BlendArgs {
     float* T;
     float* depth;
     int32_t* last;
+    unsigned long long* evaluations;  // COUNT variant: number of pixel x entry evaluations
 };
 
 // One workgroup per tile, one thread per pixel. Thread t covers pixel row t % TH and column
@@ -280,7 +281,7 @@ struct BlendArgs {
 // images. Each batch of TW*TH sorted entries is converted to blending parameters once per
 // tile and staged in LDS, where every lane reads the same record (broadcast). The tile stops
 // loading batches once every pixel is done (block-wide count of live pixels).
-template <bool RGB, bool DEPTH>
+template <bool RGB, bool DEPTH, bool COUNT = false>
 __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     extern __shared__ BlendRec s_rec[];
     const int NT = a.TW * a.TH;
@@ -302,6 +303,7 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f, D = 0.0f;
     int32_t last = 0;
     bool done = !on;
+    unsigned long long evals = 0;
     for (int64_t base = beg; base < end; base += NT) {
         if (__syncthreads_count(done ? 0 : 1) == 0) break;
         const int64_t s = base + t;
@@ -320,6 +322,7 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
         const int nb = (int)((end - base) < NT ? (end - base) : NT);
         if (!done) {
             for (int j = 0; j < nb; ++j) {
+                if (COUNT) ++evals;
                 const float4 ra = s_rec[j].a;
                 const float4 rb = s_rec[j].b;
                 const float e = fmaf(ra.x, uu, fmaf(ra.y, vv, fmaf(ra.z, uv, fmaf(ra.w, cu, fmaf(rb.x, cv, rb.y)))));
@@ -344,6 +347,11 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
                 last = (int32_t)(base + j + 1);
             }
         }
+    }
+    if (COUNT) {
+        for (int d = 32; d >= 1; d >>= 1) evals += __shfl_xor(evals, d, kWave);
+        if (__lane_id() == 0) atomicAdd(a.evaluations, evals);
+        return;
     }
     if (!on) return;
     const int64_t px = (int64_t)(V - 1) + (int64_t)a.H * (U - 1);
@@ -385,7 +393,7 @@ static int launch_render_void(hipStream_t s, const tdgs_camera* cam, const tdgs_
 static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs_tiling* t,
                                const tdgs_render_options* o, int64_t m, const int32_t* tiles_end,
                                const int32_t* sorted_f, const float* f2d, const float* depths,
-                               const tdgs_render_outputs* out) {
+                               const tdgs_render_outputs* out, unsigned long long* evaluations = nullptr) {
     BlendArgs a;
     a.W = cam->width; a.H = cam->height; a.TW = t->tile_width; a.TH = t->tile_height;
     a.ntx = t->nb_tiles_x;
@@ -393,9 +401,15 @@ static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs
     a.min_alpha = o->min_alpha; a.max_alpha = o->max_alpha; a.min_T = o->min_transmittance;
     a.m = m; a.tiles_end = tiles_end; a.sorted_f = sorted_f; a.f2d = f2d; a.depths = depths;
     a.rgb = out->rgb; a.T = out->T; a.depth = out->depth; a.last = out->last;
+    a.evaluations = evaluations;
     const int nt = t->tile_width * t->tile_height;
     const dim3 grid(t->nb_tiles_x, t->nb_tiles_y);
     const size_t lds = (size_t)nt * sizeof(BlendRec);
+    if (evaluations) {
+        k_render_tiles<false, false, true><<<grid, nt, lds, s>>>(a);
+        TDGS_LAUNCHED();
+        return TDGS_OK;
+    }
     const bool rgb = out->rgb != nullptr, dep = out->depth != nullptr;
     if (rgb && dep) k_render_tiles<true, true><<<grid, nt, lds, s>>>(a);
     else if (rgb) k_render_tiles<true, false><<<grid, nt, lds, s>>>(a);
@@ -537,6 +551,18 @@ int tdgs_render_tiles(void* stream, const tdgs_camera* cam, const tdgs_tiling* t
     TDGS_REQUIRE(!out->depth || buf->depths, "depth output needs depths");
     return launch_render_tiles((hipStream_t)stream, cam, tiling, opt, buf->key_capacity, buf->tiles_end,
                                buf->sorted_values, buf->f2d, buf->depths, out);
+}
+
+int tdgs_blend_evaluations(void* stream, const tdgs_camera* cam, const tdgs_tiling* tiling,
+                           const tdgs_render_options* opt, const tdgs_render_buffers* buf, int64_t nb_keys,
+                           uint64_t* evaluations_dev) {
+    TDGS_TRY(check_tiling(tiling, cam));
+    TDGS_REQUIRE(opt && buf && evaluations_dev && buf->tiles_end && buf->sorted_values && buf->f2d,
+                 "null arguments");
+    TDGS_REQUIRE(nb_keys >= 0 && nb_keys <= buf->key_capacity, "bad key count");
+    tdgs_render_outputs none = {nullptr, nullptr, nullptr, nullptr};
+    return launch_render_tiles((hipStream_t)stream, cam, tiling, opt, nb_keys, buf->tiles_end, buf->sorted_values,
+                               buf->f2d, buf->depths, &none, (unsigned long long*)evaluations_dev);
 }
 
 size_t tdgs_render_temp_bytes(int32_t capacity, int64_t key_capacity, const tdgs_tiling* tiling) {
