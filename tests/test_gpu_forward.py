@@ -65,7 +65,8 @@ def test_render_helpers_known_answers(gpu):
 
 
 @pytest.mark.parametrize("n,end_bit,spread", [(1, 41, 4), (1000, 41, 8), (4097, 45, 16), (100_000, 45, 64),
-                                              (300_000, 64, 1 << 40), (70_000, 20, 1000)])
+                                              (300_000, 64, 1 << 40), (70_000, 20, 1000),
+                                              (2_000_000, 46, 5000), (600_000, 40, 1)])
 def test_sort_pairs_matches_stable_sort(gpu, oracle, n, end_bit, spread):
     rng = np.random.default_rng(n + end_bit)
     hi = rng.integers(0, spread, size=n).astype(np.int64)

@@ -145,8 +145,9 @@ struct SortedCounts {
 // a Gaussian, key number `local` is tile (x0 + local % wx, y0 + local / wx): tiles row-major,
 // x fastest, as the reference emits them (forward_core.jl:577-597).
 constexpr int kEmitThreads = 256;
-constexpr int kEmitItems = 8;
+constexpr int kEmitItems = 16;
 constexpr int kEmitTile = kEmitThreads * kEmitItems;
+static_assert(kEmitTile == kRsTile, "one emission workgroup fills one radix count tile");
 
 __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, int64_t x) {
     int64_t lo = 0, hi = n;  // first index with a[i] > x
@@ -157,12 +158,17 @@ __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, 
     return lo;
 }
 
+// It also counts the digit of the first tile-sort pass (key bits [32, 32 + nbits0)) of its
+// keys, which form one radix count tile: counts0[d][blockIdx.x].
 __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     int64_t nbf, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
     const float* __restrict__ depths, const int32_t* __restrict__ ranges, int32_t ntx,
-    int64_t* __restrict__ keys, int32_t* __restrict__ vals) {
+    int64_t* __restrict__ keys, int32_t* __restrict__ vals, int nbits0, uint32_t* __restrict__ counts0,
+    int64_t count_tiles) {
     __shared__ int32_t s_cs[kEmitTile + 1];
     __shared__ int64_t s_range[2];
+    __shared__ uint32_t s_h[kRsBins];
+    s_h[threadIdx.x] = 0;
     const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
     const int64_t d1 = (d0 + kEmitTile < m ? d0 + kEmitTile : m) - 1;  // last key of the block
     if (threadIdx.x < 2) s_range[threadIdx.x] = upper_bound_i32(cs, nbf, threadIdx.x == 0 ? d0 : d1);
@@ -178,10 +184,13 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
         }
     }
     __syncthreads();
+    const uint32_t mask0 = (1u << nbits0) - 1u;
 #pragma unroll 2
     for (int it = 0; it < kEmitItems; ++it) {
         const int64_t d = d0 + (int64_t)it * kEmitThreads + threadIdx.x;
-        if (d >= m) break;
+        const bool valid = d < m;
+        uint32_t digit = 0;
+        if (valid) {
         int64_t j, start;
         if (staged) {
             int lo = 0, hi = (int)cnt;  // largest jj in [0, cnt) with s_cs[jj] <= d
@@ -201,9 +210,16 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
         const int32_t local = (int32_t)(d - start);
         const int32_t ty = r.y + local / wx;
         const int32_t tx = r.x + local % wx;
-        keys[d] = ((int64_t)(tx + (ty - 1) * ntx) << 32) | (int64_t)float_bits(depths[f - 1]);
+        const int32_t tile = tx + (ty - 1) * ntx;
+        keys[d] = ((int64_t)tile << 32) | (int64_t)float_bits(depths[f - 1]);
         vals[d] = f;
+        digit = (uint32_t)tile & mask0;
+        }
+        const uint64_t peers = match_digit(digit, nbits0, valid);
+        if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&s_h[digit], (uint32_t)__popcll(peers));
     }
+    __syncthreads();
+    counts0[(int64_t)threadIdx.x * count_tiles + blockIdx.x] = s_h[threadIdx.x];
 }
 
 // fill_df2dgs_codes_and_dfgidx_to_fgidx_kernel! (forward_core.jl:531-603): reference
@@ -669,15 +685,17 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     int32_t* ev2 = emit_into_sorted ? buf->sorted_values : buf->values;
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
+        const int nbits0 = eb - 32 < 8 ? eb - 32 : 8;
         k_emit_depth_order<<<(unsigned)ceil_div(m, kEmitTile), kEmitThreads, 0, s>>>(
-            nbf, m, sorted_f, cs, buf->depths, buf->tile_ranges, tiling->nb_tiles_x, ek, ev2);
+            nbf, m, sorted_f, cs, buf->depths, buf->tile_ranges, tiling->nb_tiles_x, ek, ev2, nbits0,
+            radix_count_table(rtemp), radix_tiles(m));
         TDGS_LAUNCHED();
     }
     {
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
         TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
                                             buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, 32, eb,
-                                            rtemp, rbytes, s));
+                                            rtemp, rbytes, s, radix_count_table(rtemp)));
     }
     // 8: tile ranges
     const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;

@@ -2,28 +2,34 @@
 // [begin_bit, end_bit), 8-bit digits; replaces CUB DeviceRadixSort::SortPairs
 // (deps/cub_sort_pairs/cub_sort_pairs_wrapper.cu:31-43).
 //
-// One pass per digit, three launches per pass:
-//   count   each 4096-key tile builds its digit histogram in LDS (wave-aggregated: one LDS
-//           atomic per distinct digit per wavefront, found with 8 ballots)
-//   scan    exclusive scan of the digit-major count table [256][tiles] -> global offsets
-//   scatter each tile re-ranks its keys stably (same ballot match gives the rank inside the
-//           wavefront; per-wave digit counts in LDS give the rank across wavefronts) and
-//           writes every pair to offset[digit][tile] + rank.
-// Stability: within a tile keys are ranked in index order (iteration, wave, lane), across
-// tiles by the digit-major scan, so equal digits keep their input order.
+// Each pass is three launches over tiles of kRsTile consecutive keys:
+//   count    per-tile 256-bin digit histogram, written digit-major: counts[d][tile]
+//   scan     one workgroup per digit turns its row into exclusive prefixes over the tiles
+//            and writes the digit total                                     (k_rs_scan_rows)
+//   scatter  each tile ranks its keys stably (wavefront ballot match + per-wave digit
+//            counters in LDS), stages the tile in LDS in digit order, and writes it out in
+//            contiguous per-digit runs at totals-prefix[d] + counts[d][tile]  (k_rs_scatter)
+// Stability: within a tile keys are ranked in index order (wave, item, lane); across tiles
+// the row scan orders tiles by index, so equal digits keep their input order.
+//
+// The count of a pass can come from the kernel that produced the keys (the render pipeline
+// fuses it into key emission and projection), so a pass reads its keys once.
+// Decoupled look-back (Onesweep, Adinets & Merrill 2022) replaces the count and scan
+// launches by a chained prefix over tiles; on this part it was measured slower: with
+// ~800 tiles in flight the walk back to a published prefix takes several dependent
+// round trips of ~2.5 us under load, which halved the scatter's 5.6 TB/s.
 #pragma once
 
 #include "common.hpp"
-#include "scan.hpp"
 
 namespace tdgs {
 
-constexpr int kRsThreads = 256;
-constexpr int kRsItems = 16;
+constexpr int kRsThreads = 512;   // scatter / count: threads and keys per thread
+constexpr int kRsItems = 8;
 constexpr int kRsTile = kRsThreads * kRsItems;
 constexpr int kRsBins = 256;
 constexpr int kRsWaves = kRsThreads / kWave;
-static_assert(kRsThreads == kRsBins, "one thread per digit bin");
+static_assert(kRsThreads >= kRsBins && kRsThreads % kRsBins == 0, "digit owners");
 
 // Lanes of the wavefront holding the same digit as this lane (among lanes with valid).
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, int nbits, bool valid) {
@@ -36,70 +42,202 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, int nbits, bool vali
     return peers;
 }
 
+// Exclusive scan of one value per thread over the first 256 threads of the block (the
+// digit owners); every thread of the block must call it.
+__device__ __forceinline__ uint32_t digit_excl_scan(uint32_t a, uint32_t* s_tmp) {
+    const int lane = __lane_id(), wave = threadIdx.x / kWave;
+    uint32_t ia = a;
+    for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = __shfl_up(ia, d, kWave);
+        if (lane >= d) ia += o;
+    }
+    if (lane == kWave - 1 && wave < kRsBins / kWave) s_tmp[wave] = ia;
+    __syncthreads();
+    uint32_t off = 0;
+    for (int w = 0; w < wave && w < kRsBins / kWave; ++w) off += s_tmp[w];
+    return off + ia - a;
+}
+
+// Histogram of one digit over a tile into LDS (wave-aggregated atomics); returns after a
+// block barrier with s_h complete.
 template <class K>
-__global__ __launch_bounds__(kRsThreads) void k_radix_count(const K* __restrict__ keys, int64_t n,
-                                                            int shift, int nbits,
-                                                            uint32_t* __restrict__ counts,
-                                                            int64_t ntiles) {
-    __shared__ uint32_t hist[kRsBins];
-    hist[threadIdx.x] = 0;
+__device__ __forceinline__ void tile_digit_histogram(const K* __restrict__ keys, int64_t n, int64_t tile, int shift,
+                                                     int nbits, uint32_t* s_h) {
+    const int t = threadIdx.x;
+    for (int i = t; i < kRsBins; i += kRsThreads) s_h[i] = 0;
     __syncthreads();
     const uint32_t mask = (1u << nbits) - 1u;
-    const int64_t base = (int64_t)blockIdx.x * kRsTile + threadIdx.x;
+    const int64_t base = tile * kRsTile + t;
+    K key[kRsItems];
+#pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
         const int64_t i = base + (int64_t)k * kRsThreads;
-        const bool valid = i < n;
-        const uint32_t d = valid ? (uint32_t)(keys[i] >> shift) & mask : 0u;
+        key[k] = i < n ? keys[i] : (K)0;
+    }
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        const bool valid = base + (int64_t)k * kRsThreads < n;
+        const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
         const uint64_t peers = match_digit(d, nbits, valid);
-        if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&hist[d], (uint32_t)__popcll(peers));
+        if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&s_h[d], (uint32_t)__popcll(peers));
     }
     __syncthreads();
-    counts[(int64_t)threadIdx.x * ntiles + blockIdx.x] = hist[threadIdx.x];
 }
 
 template <class K>
-__global__ __launch_bounds__(kRsThreads) void k_radix_scatter(
+__global__ __launch_bounds__(kRsThreads) void k_rs_count(const K* __restrict__ keys, int64_t n, int shift,
+                                                         int nbits, uint32_t* __restrict__ counts, int64_t tiles) {
+    __shared__ uint32_t s_h[kRsBins];
+    tile_digit_histogram(keys, n, blockIdx.x, shift, nbits, s_h);
+    if (threadIdx.x < kRsBins) counts[(int64_t)threadIdx.x * tiles + blockIdx.x] = s_h[threadIdx.x];
+}
+
+// Workgroup d: exclusive prefix of counts[d][0..tiles) in place, total to totals[d].
+static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restrict__ counts, int64_t tiles,
+                                                             uint32_t* __restrict__ totals) {
+    __shared__ uint32_t s_tmp[4];
+    uint32_t* row = counts + (int64_t)blockIdx.x * tiles;
+    const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+    constexpr int IT = 8;
+    uint32_t carry = 0;
+    for (int64_t start = 0; start < tiles; start += 256 * IT) {
+        const int64_t b = start + (int64_t)t * IT;
+        uint32_t v[IT];
+        uint32_t acc = 0;
+#pragma unroll
+        for (int k = 0; k < IT; ++k) {
+            v[k] = b + k < tiles ? row[b + k] : 0u;
+            acc += v[k];
+        }
+        uint32_t incl = acc;
+        for (int d = 1; d < kWave; d <<= 1) {
+            const uint32_t o = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += o;
+        }
+        if (lane == kWave - 1) s_tmp[wave] = incl;
+        __syncthreads();
+        uint32_t off = carry, blk = 0;
+        for (int w = 0; w < 4; ++w) {
+            if (w < wave) off += s_tmp[w];
+            blk += s_tmp[w];
+        }
+        __syncthreads();
+        off += incl - acc;
+#pragma unroll
+        for (int k = 0; k < IT; ++k) {
+            if (b + k < tiles) row[b + k] = off;
+            off += v[k];
+        }
+        carry += blk;
+    }
+    if (t == 0) totals[blockIdx.x] = carry;
+}
+
+template <class K>
+__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_rs_scatter(
     const K* __restrict__ kin, const int32_t* __restrict__ vin, K* __restrict__ kout,
-    int32_t* __restrict__ vout, int64_t n, int shift, int nbits,
-    const uint32_t* __restrict__ offsets, int64_t ntiles) {
-    __shared__ uint32_t running[kRsBins];
-    __shared__ uint32_t wcount[kRsWaves][kRsBins];
-    const int t = threadIdx.x;
-    const int wave = t / kWave;
-    running[t] = offsets[(int64_t)t * ntiles + blockIdx.x];
-#pragma unroll
-    for (int w = 0; w < kRsWaves; ++w) wcount[w][t] = 0;
+    int32_t* __restrict__ vout, int64_t n, int shift, int nbits, const uint32_t* __restrict__ offsets,
+    const uint32_t* __restrict__ totals, int64_t tiles, uint32_t* err) {
+    __shared__ K s_buf[kRsTile];                 // the tile in digit order: keys, then values
+    __shared__ uint32_t s_wh[kRsWaves][kRsBins];  // per-wave digit counts -> offsets
+    __shared__ uint32_t s_local[kRsBins];         // start of each digit inside the tile
+    __shared__ int32_t s_delta[kRsBins];          // output index - tile-local index
+    __shared__ uint32_t s_tmp[kRsWaves];
+
+    const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
+    const bool owner = t < kRsBins;
+    const int64_t tile = blockIdx.x;
+    const uint32_t total_t = owner ? totals[t] : 0u;
+    const uint32_t off_t = owner ? offsets[(int64_t)t * tiles + tile] : 0u;
+    for (int i = t; i < kRsWaves * kRsBins; i += kRsThreads) (&s_wh[0][0])[i] = 0;
     __syncthreads();
+    const int32_t base = (int32_t)(tile * kRsTile);
     const uint32_t mask = (1u << nbits) - 1u;
-    const int64_t base = (int64_t)blockIdx.x * kRsTile + t;
-    for (int k = 0; k < kRsItems; ++k) {
-        const int64_t i = base + (int64_t)k * kRsThreads;
-        const bool valid = i < n;
-        const K key = valid ? kin[i] : (K)0;
-        const int32_t val = valid ? vin[i] : 0;
-        const uint32_t d = (uint32_t)(key >> shift) & mask;
-        const uint64_t peers = match_digit(d, nbits, valid);
-        const uint32_t rank = (uint32_t)__popcll(peers & lanemask_lt());
-        if (valid && rank == 0) wcount[wave][d] = (uint32_t)__popcll(peers);
-        __syncthreads();
-        uint32_t pos = 0;
-        if (valid) {
-            pos = running[d] + rank;
-            for (int w = 0; w < wave; ++w) pos += wcount[w][d];
-        }
-        __syncthreads();
-        uint32_t add = 0;
+    const int32_t wbase = base + w * (kRsItems * kWave) + lane;
+    const int32_t nn = (int32_t)n;
+
+    K key[kRsItems];
+    int32_t val[kRsItems];
+    uint32_t pos[kRsItems];
 #pragma unroll
-        for (int w = 0; w < kRsWaves; ++w) {
-            add += wcount[w][t];
-            wcount[w][t] = 0;
+    for (int k = 0; k < kRsItems; ++k) {
+        const int32_t i = wbase + k * kWave;
+        key[k] = i < nn ? kin[i] : (K)0;
+        val[k] = i < nn ? vin[i] : 0;
+    }
+    // Rank inside the wavefront, items in index order: the first lane of each group of equal
+    // digits advances the wave's counter for that digit after every lane has read it.
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        const bool valid = wbase + k * kWave < nn;
+        const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
+        const uint64_t peers = match_digit(d, nbits, valid);
+        const uint64_t below = peers & lanemask_lt();
+        const uint32_t cnt = s_wh[w][d];
+        pos[k] = cnt + (uint32_t)__popcll(below);
+        if (valid && below == 0) s_wh[w][d] = cnt + (uint32_t)__popcll(peers);
+    }
+    __syncthreads();
+
+    // Digit owners: wave offsets and the tile's count of the digit.
+    uint32_t tot = 0;
+    if (owner) {
+#pragma unroll
+        for (int i = 0; i < kRsWaves; ++i) {
+            const uint32_t c = s_wh[i][t];
+            s_wh[i][t] = tot;
+            tot += c;
         }
-        running[t] += add;
-        __syncthreads();
-        if (valid) {
-            kout[pos] = key;
-            vout[pos] = val;
+    }
+    const uint32_t local = digit_excl_scan(tot, s_tmp);
+    __syncthreads();
+    const uint32_t bin = digit_excl_scan(total_t, s_tmp);
+    if (owner) {
+        s_local[t] = local;
+        s_delta[t] = (int32_t)(bin + off_t) - (int32_t)local;
+    }
+    __syncthreads();
+
+    // Stage keys in digit order, then write contiguous runs per digit.
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        if (wbase + k * kWave < nn) {
+            const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
+            pos[k] += s_local[d] + s_wh[w][d];
+            if (pos[k] < (uint32_t)kRsTile) s_buf[pos[k]] = key[k];
         }
+    }
+    __syncthreads();
+    const int tile_n = nn - base < kRsTile ? nn - base : kRsTile;
+    int32_t opos[kRsItems];
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        const int i = k * kRsThreads + t;
+        opos[k] = -1;
+        if (i < tile_n) {
+            const K kk = s_buf[i];
+            const uint32_t d = (uint32_t)(kk >> shift) & mask;
+            const int32_t o = s_delta[d] + i;
+            if (o >= 0 && o < nn) {
+                kout[o] = kk;
+                opos[k] = o;
+            } else {
+                atomicOr(err, 1u);   // inconsistent counts: never write out of bounds
+            }
+        }
+    }
+    __syncthreads();
+    int32_t* s_val = reinterpret_cast<int32_t*>(s_buf);
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        const int32_t i = wbase + k * kWave;
+        if (i < nn && pos[k] < (uint32_t)kRsTile) s_val[pos[k]] = val[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        const int i = k * kRsThreads + t;
+        if (opos[k] >= 0) vout[opos[k]] = s_val[i];
     }
 }
 
@@ -107,38 +245,49 @@ inline int radix_passes(int begin_bit, int end_bit) {
     return end_bit > begin_bit ? (end_bit - begin_bit + 7) / 8 : 0;
 }
 
-// Scratch for radix_sort_pairs (count table + its scan), excluding ping-pong buffers.
+inline int64_t radix_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kRsTile); }
+
+// The count table inside radix_sort_pairs' scratch, for producers that fill the first
+// pass's counts themselves.
+inline uint32_t* radix_count_table(void* temp) { return (uint32_t*)temp; }
+
+// Scratch for radix_sort_pairs, excluding the ping-pong buffers: the digit-major count
+// table, the digit totals and an error word.
 inline size_t radix_temp_bytes(int64_t n) {
-    const int64_t ntiles = ceil_div(n > 0 ? n : 1, kRsTile);
-    const int64_t cells = ntiles * kRsBins;
-    return align_up((size_t)cells * sizeof(uint32_t)) + scan_temp_bytes_for(cells) + 256;
+    return align_up((size_t)radix_tiles(n) * kRsBins * sizeof(uint32_t)) + align_up((kRsBins + 64) * 4);
 }
 
 // Sort n pairs from (kin, vin) into (kout, vout) on key bits [begin_bit, end_bit).
 // (alt_k, alt_v) is the ping-pong buffer. The first pass writes (kout) when the pass count is
 // odd and (alt) when it is even, so kin may alias whichever of the two the first pass does
-// not write (and it is never written otherwise).
+// not write (and it is never written otherwise). first_counts, when not null, is the count
+// table of the first pass ([256][radix_tiles(n)] digit-major, from the producer of the
+// keys); it is consumed (scanned in place). `err` (device word, may be null) is set nonzero
+// if the counts disagree with the keys (the affected keys are not written).
 template <class K>
 int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K* alt_k,
                      int32_t* alt_v, int64_t n, int begin_bit, int end_bit, void* temp,
-                     size_t temp_bytes, hipStream_t stream) {
+                     size_t temp_bytes, hipStream_t stream, uint32_t* first_counts = nullptr,
+                     uint32_t* err = nullptr) {
     const int passes = radix_passes(begin_bit, end_bit);
     if (n <= 0) return TDGS_OK;
+    if (n > (int64_t)INT32_MAX) {
+        set_error("radix sort of %lld keys exceeds the int32 index range", (long long)n);
+        return TDGS_ERR_INVALID;
+    }
     if (passes == 0) {
         if (kout != kin) TDGS_HIP(hipMemcpyAsync(kout, kin, n * sizeof(K), hipMemcpyDeviceToDevice, stream));
         if (vout != vin) TDGS_HIP(hipMemcpyAsync(vout, vin, n * sizeof(int32_t), hipMemcpyDeviceToDevice, stream));
         return TDGS_OK;
     }
-    const int64_t ntiles = ceil_div(n, kRsTile);
-    const int64_t cells = ntiles * kRsBins;
-    Arena ar(temp, temp_bytes);
-    uint32_t* counts = ar.take<uint32_t>(cells);
-    const size_t sbytes = scan_temp_bytes_for(cells);
-    void* stemp = ar.take<char>((int64_t)sbytes);
-    if (!counts || !stemp) {
+    if (temp_bytes < radix_temp_bytes(n) || temp == nullptr) {
         set_error("radix sort scratch too small (%zu bytes for %lld keys)", temp_bytes, (long long)n);
         return TDGS_ERR_CAPACITY;
     }
+    const int64_t tiles = radix_tiles(n);
+    uint32_t* counts = (uint32_t*)temp;
+    uint32_t* totals = (uint32_t*)((char*)temp + align_up((size_t)tiles * kRsBins * sizeof(uint32_t)));
+    if (!err) err = totals + kRsBins;
     const K* src_k = kin;
     const int32_t* src_v = vin;
     for (int p = 0; p < passes; ++p) {
@@ -147,12 +296,17 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
         const bool to_out = ((passes - 1 - p) % 2) == 0;
         K* dk = to_out ? kout : alt_k;
         int32_t* dv = to_out ? vout : alt_v;
-        k_radix_count<K><<<(unsigned)ntiles, kRsThreads, 0, stream>>>(src_k, n, shift, nbits, counts, ntiles);
+        uint32_t* table = counts;
+        if (p == 0 && first_counts) {
+            table = first_counts;
+        } else {
+            k_rs_count<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, n, shift, nbits, table, tiles);
+            TDGS_LAUNCHED();
+        }
+        k_rs_scan_rows<<<kRsBins, 256, 0, stream>>>(table, tiles, totals);
         TDGS_LAUNCHED();
-        TDGS_TRY(device_scan(ItemsU32{counts}, ItemsU32{counts}, WriteExclusiveU32{counts}, cells,
-                             stemp, sbytes, nullptr, stream));
-        k_radix_scatter<K><<<(unsigned)ntiles, kRsThreads, 0, stream>>>(src_k, src_v, dk, dv, n, shift,
-                                                                         nbits, counts, ntiles);
+        k_rs_scatter<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, src_v, dk, dv, n, shift, nbits, table,
+                                                                     totals, tiles, err);
         TDGS_LAUNCHED();
         src_k = dk;
         src_v = dv;
