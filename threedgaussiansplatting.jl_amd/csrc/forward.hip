@@ -280,6 +280,7 @@ struct __align__(16) BlendRec {
 struct BlendArgs {
     int32_t W, H, TW, TH, ntx;
     float bg0, bg1, bg2, min_alpha, max_alpha, min_T;
+    float e_cut;   // exp_f(e) < min_alpha for every exponent e < e_cut
     int64_t m;
     const int32_t* tiles_end;
     const int32_t* sorted_f;
@@ -292,11 +293,26 @@ struct BlendArgs {
     unsigned long long* evaluations;  // COUNT variant: number of pixel x entry evaluations
 };
 
-// One workgroup per tile, one thread per pixel. Thread t covers pixel row t % TH and column
-// t / TH of the tile, so a wavefront writes whole column segments of the column-major
-// images. Each batch of TW*TH sorted entries is converted to blending parameters once per
-// tile and staged in LDS, where every lane reads the same record (broadcast). The tile stops
-// loading batches once every pixel is done (block-wide count of live pixels).
+// Pixel of thread t inside a TW x TH tile (1-based). With both sides multiples of 8 each
+// wavefront covers an 8x8 block (blocks column-major, lanes column-major inside), which
+// keeps a Gaussian's footprint inside as few wavefronts as possible; otherwise wavefront
+// t/64 covers 64 consecutive pixels of the column-major tile.
+__device__ __forceinline__ void tile_pixel(int t, int TW, int TH, int* u_in, int* v_in) {
+    if ((TW & 7) == 0 && (TH & 7) == 0) {
+        const int w = t >> 6, l = t & 63, bpc = TH >> 3;
+        *v_in = (w % bpc) * 8 + (l & 7) + 1;
+        *u_in = (w / bpc) * 8 + (l >> 3) + 1;
+    } else {
+        *v_in = t % TH + 1;
+        *u_in = t / TH + 1;
+    }
+}
+
+// One workgroup per tile, one thread per pixel (tile_pixel). Each batch of TW*TH sorted
+// entries is converted to blending parameters once per tile and staged in LDS, where every
+// lane reads the same record (broadcast). A wavefront skips an entry when no pixel it still
+// blends can reach min_alpha (exponent below e_cut), leaves the batch when all its pixels
+// are done, and the tile stops loading batches once every pixel is done.
 template <bool RGB, bool DEPTH, bool COUNT = false>
 __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     extern __shared__ BlendRec s_rec[];
@@ -304,7 +320,8 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     const int t = threadIdx.x;
     const int tx = blockIdx.x + 1, ty = blockIdx.y + 1;
     const int tile = tx + (ty - 1) * a.ntx;
-    const int v_in = t % a.TH + 1, u_in = t / a.TH + 1;
+    int u_in, v_in;
+    tile_pixel(t, a.TW, a.TH, &u_in, &v_in);
     const int U = u_in + (tx - 1) * a.TW, V = v_in + (ty - 1) * a.TH;
     const bool on = U <= a.W && V <= a.H;
     const float cu = (float)u_in - 0.5f, cv = (float)v_in - 0.5f;
@@ -338,29 +355,33 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
         const int nb = (int)((end - base) < NT ? (end - base) : NT);
         if (!done) {
             for (int j = 0; j < nb; ++j) {
-                if (COUNT) ++evals;
+                if (COUNT && !done) ++evals;
                 const float4 ra = s_rec[j].a;
                 const float4 rb = s_rec[j].b;
                 const float e = fmaf(ra.x, uu, fmaf(ra.y, vv, fmaf(ra.z, uv, fmaf(ra.w, cu, fmaf(rb.x, cv, rb.y)))));
-                const float alpha = fminf(a.max_alpha, exp_f(e));
-                if (alpha < a.min_alpha) continue;
+                if (!__any(!done && !(e < a.e_cut))) continue;
+                const float alpha = fminf(a.max_alpha, exp_f_sel(e));
+                const bool contrib = !done && !(alpha < a.min_alpha);
                 const float Tn = T * (1.0f - alpha);
-                if (Tn < a.min_T) {
-                    done = true;
-                    break;
-                }
-                const float w = T * alpha;
-                if (RGB || DEPTH) {
-                    const float4 rc = s_rec[j].c;
-                    if (RGB) {
-                        C0 = fmaf(w, rb.z, C0);
-                        C1 = fmaf(w, rb.w, C1);
-                        C2 = fmaf(w, rc.x, C2);
+                const bool stop = contrib && Tn < a.min_T;
+                if (contrib && !stop) {
+                    const float w = T * alpha;
+                    if (RGB || DEPTH) {
+                        const float4 rc = s_rec[j].c;
+                        if (RGB) {
+                            C0 = fmaf(w, rb.z, C0);
+                            C1 = fmaf(w, rb.w, C1);
+                            C2 = fmaf(w, rc.x, C2);
+                        }
+                        if (DEPTH) D = fmaf(w, rc.y, D);
                     }
-                    if (DEPTH) D = fmaf(w, rc.y, D);
+                    T = Tn;
+                    last = (int32_t)(base + j + 1);
                 }
-                T = Tn;
-                last = (int32_t)(base + j + 1);
+                if (__any(stop)) {
+                    done = done || stop;
+                    if (!__any(!done)) break;
+                }
             }
         }
     }
@@ -415,6 +436,7 @@ static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs
     a.ntx = t->nb_tiles_x;
     a.bg0 = o->background[0]; a.bg1 = o->background[1]; a.bg2 = o->background[2];
     a.min_alpha = o->min_alpha; a.max_alpha = o->max_alpha; a.min_T = o->min_transmittance;
+    a.e_cut = exponent_cut(o->min_alpha);
     a.m = m; a.tiles_end = tiles_end; a.sorted_f = sorted_f; a.f2d = f2d; a.depths = depths;
     a.rgb = out->rgb; a.T = out->T; a.depth = out->depth; a.last = out->last;
     a.evaluations = evaluations;

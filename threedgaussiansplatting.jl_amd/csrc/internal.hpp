@@ -1,6 +1,8 @@
 // internal.hpp — pieces shared between the translation units of libtdgs.
 #pragma once
 
+#include <cmath>
+
 #include "common.hpp"
 
 struct tdgs_ctx {
@@ -25,6 +27,14 @@ struct StageScope {
     StageScope(int st, hipStream_t s) : stage(st), stream(s) { profile_mark(stage, true, stream); }
     ~StageScope() { profile_mark(stage, false, stream); }
 };
+
+// Exponent below which blending can skip an entry: for e < exponent_cut(min_alpha),
+// exp_f(e) (relative error a few 1e-7) is below min_alpha, so alpha < min_alpha. A margin of
+// 1e-3 in the exponent covers the rounding; no cut without a positive min_alpha.
+inline float exponent_cut(float min_alpha) {
+    if (!(min_alpha > 0.0f)) return -__builtin_inff();
+    return std::nextafter((float)(std::log((double)min_alpha) - 1e-3), -__builtin_inff());
+}
 
 inline int check_gaussians(const tdgs_gaussians* g, bool trainable_only) {
     TDGS_REQUIRE(g != nullptr, "gaussians is null");

@@ -68,6 +68,30 @@ TDGS_HD float exp_f(float x) {
     return p * bits_float((uint32_t)(ni + 127) << 23);
 }
 
+// exp_f without branches, for wavefront loops: the same operations on a clamped copy of x
+// (identical to x wherever exp_f takes its polynomial path), the special cases chosen by
+// selects. Equal to exp_f(x) bit for bit for every x, NaN and infinities included.
+TDGS_HD float exp_f_sel(float x) {
+    const float xc = fminf(fmaxf(x, -88.0f), 89.0f);
+    const float n = rintf(xc * kLog2e);
+    float r = fmaf(n, -kLn2Hi, xc);
+    r = fmaf(n, -kLn2Lo, r);
+    float p = 1.98412698412698e-4f;
+    p = fmaf(p, r, 1.38888888888889e-3f);
+    p = fmaf(p, r, 8.33333333333333e-3f);
+    p = fmaf(p, r, 4.16666666666667e-2f);
+    p = fmaf(p, r, 1.66666666666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ni = (int)n;                         // in [-127, 128] after the clamp
+    const bool big = ni > 127;
+    p = big ? p * 2.0f : p;
+    ni = big ? 127 : ni;
+    const float v = p * bits_float((uint32_t)((ni + 127) & 0xff) << 23);
+    return x > 88.72283935f ? kInf : (x > -87.33654475f ? v : ((x != x) ? x : 0.0f));
+}
+
 // log(x) for x > 0. x = m 2^e with m in [sqrt(1/2), sqrt(2)); log m = 2 atanh(s),
 // s = (m-1)/(m+1), by the odd series of atanh to s^11 (|s| <= 0.1716, remainder < 1e-11);
 // e ln2 added with the split constant. About 1 ulp. Subnormal inputs are scaled first.
