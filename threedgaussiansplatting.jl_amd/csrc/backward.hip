@@ -45,12 +45,13 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 struct __align__(16) BackRec {
     float4 a;  // mu_x mu_y a M11
     float4 b;  // M21 M22 r g
-    float4 c;  // b - - -
+    float4 c;  // b cut - -   (cut: exponent below which a * G < min_alpha)
 };
 
 struct BackBlendArgs {
     int32_t W, H, TW, TH, ntx;
     float bg0, bg1, bg2, min_alpha, max_alpha;
+    float log_min_alpha;   // log(min_alpha) - 1e-3 (-inf without a positive min_alpha)
     int64_t m;
     const int32_t* tiles_end;
     const int32_t* sorted_f;
@@ -71,7 +72,8 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
     const int lane = __lane_id();
     const int tx = blockIdx.x + 1, ty = blockIdx.y + 1;
     const int tile = tx + (ty - 1) * a.ntx;
-    const int v_in = t % a.TH + 1, u_in = t / a.TH + 1;
+    int u_in, v_in;
+    tile_pixel(t, a.TW, a.TH, &u_in, &v_in);
     const int U = u_in + (tx - 1) * a.TW, V = v_in + (ty - 1) * a.TH;
     const bool on = U <= a.W && V <= a.H;
     int64_t end = a.tiles_end[tile - 1];
@@ -111,7 +113,9 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
             BackRec rec;
             rec.a = make_float4(r[0], r[1], r[2], r[3]);
             rec.b = make_float4(r[4], r[5], r[6], r[7]);
-            rec.c = make_float4(r[8], 0.0f, 0.0f, 0.0f);
+            // a * exp_f(e) < min_alpha for e < cut (log_f and exp_f errors ~1e-6 absolute,
+            // inside the 1e-3 margin of log_min_alpha; a NaN cut never skips)
+            rec.c = make_float4(r[8], a.log_min_alpha - log_f(r[2]), 0.0f, 0.0f);
             s_rec[t] = rec;
         }
         __syncthreads();
@@ -119,13 +123,16 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         for (int j = jtop - 1; j >= 0; --j) {
             float o[9] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
             bool contrib = false;
-            if (on && lo + j < (int64_t)last) {
-                const float4 ra = s_rec[j].a, rb = s_rec[j].b;
-                float du, dv;
-                const float G = backward_gaussian(cu, cv, ra.x, ra.y, ra.w, rb.x, rb.y, &du, &dv);
+            const float4 ra = s_rec[j].a, rb = s_rec[j].b, rc = s_rec[j].c;
+            float du, dv;
+            const float ex = backward_exponent(cu, cv, ra.x, ra.y, ra.w, rb.x, rb.y, &du, &dv);
+            const bool live = on && lo + j < (int64_t)last && !(ex < rc.y);
+            if (!__any(live)) continue;
+            if (live) {
+                const float G = exp_f_sel(ex);
                 const float alpha = fminf(a.max_alpha, ra.z * G);
                 if (!(alpha < a.min_alpha)) {
-                    const float c[3] = {rb.z, rb.w, s_rec[j].c.x};
+                    const float c[3] = {rb.z, rb.w, rc.x};
                     backward_pair(alpha, G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
                     contrib = true;
                 }
@@ -252,6 +259,7 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
     a.ntx = tiling->nb_tiles_x;
     a.bg0 = opt->background[0]; a.bg1 = opt->background[1]; a.bg2 = opt->background[2];
     a.min_alpha = opt->min_alpha; a.max_alpha = opt->max_alpha;
+    a.log_min_alpha = opt->min_alpha > 0.0f ? (float)(std::log((double)opt->min_alpha) - 1e-3) : -__builtin_inff();
     a.m = buf->key_capacity;
     a.tiles_end = buf->tiles_end; a.sorted_f = buf->sorted_values; a.f2d = buf->f2d;
     a.rgb_grad = rgb_grad; a.T = out->T; a.last = out->last; a.grads2d = grads->grads2d;

@@ -293,21 +293,6 @@ struct BlendArgs {
     unsigned long long* evaluations;  // COUNT variant: number of pixel x entry evaluations
 };
 
-// Pixel of thread t inside a TW x TH tile (1-based). With both sides multiples of 8 each
-// wavefront covers an 8x8 block (blocks column-major, lanes column-major inside), which
-// keeps a Gaussian's footprint inside as few wavefronts as possible; otherwise wavefront
-// t/64 covers 64 consecutive pixels of the column-major tile.
-__device__ __forceinline__ void tile_pixel(int t, int TW, int TH, int* u_in, int* v_in) {
-    if ((TW & 7) == 0 && (TH & 7) == 0) {
-        const int w = t >> 6, l = t & 63, bpc = TH >> 3;
-        *v_in = (w % bpc) * 8 + (l & 7) + 1;
-        *u_in = (w / bpc) * 8 + (l >> 3) + 1;
-    } else {
-        *v_in = t % TH + 1;
-        *u_in = t / TH + 1;
-    }
-}
-
 // One workgroup per tile, one thread per pixel (tile_pixel). Each batch of TW*TH sorted
 // entries is converted to blending parameters once per tile and staged in LDS, where every
 // lane reads the same record (broadcast). A wavefront skips an entry when no pixel it still

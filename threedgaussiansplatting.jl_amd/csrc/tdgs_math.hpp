@@ -447,15 +447,21 @@ TDGS_HD float blend_exponent(const float p[6], float u, float v, float uu, float
     return fmaf(p[0], uu, fmaf(p[1], vv, fmaf(p[2], uv, fmaf(p[3], u, fmaf(p[4], v, p[5])))));
 }
 
-// Gaussian value in the backward pass (direct form, backward_core.jl:236-240), at global
-// continuous pixel coordinates (cu, cv) = (u - 0.5, v - 0.5).
-TDGS_HD float backward_gaussian(float cu, float cv, float mux, float muy, float m11, float m21,
+// Exponent of the Gaussian in the backward pass (direct form, backward_core.jl:236-240), at
+// global continuous pixel coordinates (cu, cv) = (u - 0.5, v - 0.5).
+TDGS_HD float backward_exponent(float cu, float cv, float mux, float muy, float m11, float m21,
                                 float m22, float* du_out, float* dv_out) {
     const float du = cu - mux, dv = cv - muy;
     *du_out = du;
     *dv_out = dv;
     const float q = fmaf(m11 * du, du, m22 * dv * dv);
-    return exp_f(fmaf(-0.5f, q, -(m21 * du) * dv));
+    return fmaf(-0.5f, q, -(m21 * du) * dv);
+}
+
+// Gaussian value in the backward pass (direct form, backward_core.jl:236-240).
+TDGS_HD float backward_gaussian(float cu, float cv, float mux, float muy, float m11, float m21,
+                                float m22, float* du_out, float* dv_out) {
+    return exp_f(backward_exponent(cu, cv, mux, muy, m11, m21, m22, du_out, dv_out));
 }
 
 // Per-(pixel, Gaussian) gradient contribution of the backward blend
