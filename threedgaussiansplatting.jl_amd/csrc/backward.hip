@@ -8,30 +8,70 @@
 // issues 9 float atomics per (pixel, Gaussian) pair. Here the wavefront walks the tile's
 // sorted list back to front in lock step (a lane whose last contributor lies before the
 // current entry contributes zero), so the per-pixel order of operations is the reference's.
-// The 9 gradient contributions of an entry are summed over the wavefront with DPP
-// row-shift/broadcast adds, over the workgroup's wavefronts with LDS atomics, and reach
-// global memory once per (tile, Gaussian) — 9 atomics per tile instead of 9 per pixel.
+// The 9 gradient contributions of 7 contributing entries at a time are summed over the
+// wavefront in one transpose-sum (permlane swaps and DPP, one add per value), over the
+// workgroup's wavefronts with LDS atomics, and reach global memory once per
+// (tile, Gaussian) — 9 atomics per tile instead of 9 per pixel.
 #include "internal.hpp"
 
 namespace tdgs {
 
-// Sum of v over the 64 lanes of the wavefront, valid in lane 63 (all lanes must be active).
-// quad_perm [1,0,3,2] and [2,3,0,1], row_shr 4 and 8 (zero fill), row_bcast 15 and 31.
-__device__ __forceinline__ float wave_sum_to_lane63(float v) {
-    int x = __builtin_bit_cast(int, v);
-#define TDGS_DPP_ADD(ctrl, rmask)                                                               \
-    {                                                                                           \
-        const int t = __builtin_amdgcn_update_dpp(0, x, ctrl, rmask, 0xf, true);                \
-        x = __builtin_bit_cast(int, __builtin_bit_cast(float, x) + __builtin_bit_cast(float, t)); \
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+
+// (x + y) after v_permlane32_swap / v_permlane16_swap of x and y: lanes whose bit 5 (resp. 4)
+// is clear get x summed with its partner lane's x, the others y with the partner's y. The
+// empty asm on the second result keeps the compiler from folding the two results of the
+// swap into one (this toolchain compiles a plain r[0] + r[1] to r[0] + r[0]).
+__device__ __forceinline__ float halve_swap32(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, y),
+                                                    false, false);
+    uint32_t hi = r[1];
+    asm volatile("" : "+v"(hi));
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, hi);
+}
+__device__ __forceinline__ float halve_swap16(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, y),
+                                                    false, false);
+    uint32_t hi = r[1];
+    asm volatile("" : "+v"(hi));
+    return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, hi);
+}
+
+// Sums 64 values per lane over the wavefront by recursive halving: at the step of lane
+// distance D each lane keeps the half of its values whose index has the lane's bit D,
+// adds the partner lane's copy of that half and passes on the other half. Six steps
+// (D = 32, 16 by permlane swaps; 8, 4, 2, 1 by DPP inside a row) and 63 adds in total leave
+// in lane l the wavefront sum of v[l]. v is destroyed.
+__device__ __forceinline__ float wave_transpose_sum64(float (&v)[64]) {
+    const int lane = __lane_id();
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = halve_swap32(v[i], v[i + 32]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = halve_swap16(v[i], v[i + 16]);
+    const bool b3 = lane & 8, b2 = lane & 4, b1 = lane & 2, b0 = lane & 1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float send = b3 ? v[i] : v[i + 8], keep = b3 ? v[i + 8] : v[i];
+        v[i] = keep + dpp_f32<0x128>(send);                       // row_ror:8 = lane ^ 8
     }
-    TDGS_DPP_ADD(0xb1, 0xf)
-    TDGS_DPP_ADD(0x4e, 0xf)
-    TDGS_DPP_ADD(0x114, 0xf)
-    TDGS_DPP_ADD(0x118, 0xf)
-    TDGS_DPP_ADD(0x142, 0xa)
-    TDGS_DPP_ADD(0x143, 0xc)
-#undef TDGS_DPP_ADD
-    return __builtin_bit_cast(float, x);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float send = b2 ? v[i] : v[i + 4], keep = b2 ? v[i + 4] : v[i];
+        // lane ^ 4 by ds_swizzle in bit-mask mode (and 0x1f, xor 4). One unconditional
+        // cross-lane read: a select between two DPP rotations gets turned into a branch, and
+        // a DPP read from a lane switched off by that branch returns 0.
+        v[i] = keep + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x101f));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float send = b1 ? v[i] : v[i + 2], keep = b1 ? v[i + 2] : v[i];
+        v[i] = keep + dpp_f32<0x4e>(send);                        // quad_perm [2,3,0,1]
+    }
+    const float send = b0 ? v[0] : v[1], keep = b0 ? v[1] : v[0];
+    return keep + dpp_f32<0xb1>(send);                            // quad_perm [1,0,3,2]
 }
 
 __device__ __forceinline__ int wave_max_i32(int v) {
@@ -41,6 +81,8 @@ __device__ __forceinline__ int wave_max_i32(int v) {
     }
     return v;
 }
+
+constexpr int kSlots = 7;   // 7 entries x 9 gradient components = 63 of the 64 lanes
 
 struct __align__(16) BackRec {
     float4 a;  // mu_x mu_y a M11
@@ -120,31 +162,50 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         }
         __syncthreads();
         const int jtop = (int)((int64_t)wave_last - lo < nb ? (int64_t)wave_last - lo : nb);
-        for (int j = jtop - 1; j >= 0; --j) {
-            float o[9] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-            bool contrib = false;
-            const float4 ra = s_rec[j].a, rb = s_rec[j].b, rc = s_rec[j].c;
-            float du, dv;
-            const float ex = backward_exponent(cu, cv, ra.x, ra.y, ra.w, rb.x, rb.y, &du, &dv);
-            const bool live = on && lo + j < (int64_t)last && !(ex < rc.y);
-            if (!__any(live)) continue;
-            if (live) {
-                const float G = exp_f_sel(ex);
-                const float alpha = fminf(a.max_alpha, ra.z * G);
-                if (!(alpha < a.min_alpha)) {
-                    const float c[3] = {rb.z, rb.w, rc.x};
-                    backward_pair(alpha, G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
-                    contrib = true;
-                }
-            }
-            if (__ballot(contrib) != 0ull) {
+        // Entries back to front; the 9 contributions of up to kSlots consecutive contributing
+        // entries are kept per lane and summed over the wavefront in one transpose-sum, after
+        // which lane l holds component l % 9 of slot l / 9 and adds it to the tile's LDS sum.
+        int j = __builtin_amdgcn_readfirstlane(jtop - 1);   // wave-uniform: scalar loop control
+        while (j >= 0) {
+            float v[64];
+            int js[kSlots];
 #pragma unroll
-                for (int k = 0; k < 9; ++k) o[k] = wave_sum_to_lane63(o[k]);
-                if (lane == 63) {
-#pragma unroll
-                    for (int k = 0; k < 9; ++k) atomicAdd(&s_acc[9 * j + k], o[k]);
+            for (int e = 0; e < kSlots; ++e) {
+                js[e] = -1;
+                float o[9] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+                while (j >= 0) {
+                    const int jj = j--;
+                    const float4 ra = s_rec[jj].a, rb = s_rec[jj].b, rc = s_rec[jj].c;
+                    float du, dv;
+                    const float ex = backward_exponent(cu, cv, ra.x, ra.y, ra.w, rb.x, rb.y, &du, &dv);
+                    const bool live = on && lo + jj < (int64_t)last && !(ex < rc.y);
+                    if (!__any(live)) continue;
+                    bool contrib = false;
+                    if (live) {
+                        const float G = exp_f_sel(ex);
+                        const float alpha = fminf(a.max_alpha, ra.z * G);
+                        if (!(alpha < a.min_alpha)) {
+                            const float c[3] = {rb.z, rb.w, rc.x};
+                            backward_pair(alpha, G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
+                            contrib = true;
+                        }
+                    }
+                    if (__any(contrib)) {
+                        js[e] = __builtin_amdgcn_readfirstlane(jj);
+                        break;
+                    }
                 }
+#pragma unroll
+                for (int k = 0; k < 9; ++k) v[9 * e + k] = o[k];
             }
+            if (js[0] < 0) break;
+            v[63] = 0.0f;
+            const float sum = wave_transpose_sum64(v);
+            const int slot = lane / 9;
+            int jl = -1;
+#pragma unroll
+            for (int e = 0; e < kSlots; ++e) jl = slot == e ? js[e] : jl;
+            if (lane < 9 * kSlots && jl >= 0) atomicAdd(&s_acc[9 * jl + (lane - 9 * slot)], sum);
         }
         __syncthreads();
         if (t < nb) {
