@@ -181,9 +181,11 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
                     const bool live = on && lo + jj < (int64_t)last && !(ex < rc.y);
                     if (!__any(live)) continue;
                     bool contrib = false;
+                    const bool wide = __any(live && !(ex >= -87.0f && ex <= 88.0f));
                     if (live) {
-                        const float G = exp_f_sel(ex);
-                        const float alpha = fminf(a.max_alpha, ra.z * G);
+                        const float G = wide ? exp_f_sel(ex) : exp_f_core(ex);   // exp_f(ex)
+                        const float aG = ra.z * G;
+                        const float alpha = aG < a.max_alpha ? aG : a.max_alpha;   // fminf, non-NaN max_alpha
                         if (!(alpha < a.min_alpha)) {
                             const float c[3] = {rb.z, rb.w, rc.x};
                             backward_pair(alpha, G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
@@ -313,6 +315,7 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
     TDGS_REQUIRE(grads && grads->grads2d && rgb_grad && out && out->T && out->last && opt && buf,
                  "backward blending needs gradients, rgb_grad, T and last");
     TDGS_REQUIRE(buf->tiles_end && buf->sorted_values && buf->f2d, "null render buffers");
+    TDGS_TRY(check_thresholds(opt));
     hipStream_t s = (hipStream_t)stream;
     StageScope sc(TDGS_STAGE_BACKWARD_BLEND, s);
     BackBlendArgs a;

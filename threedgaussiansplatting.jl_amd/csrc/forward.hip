@@ -344,8 +344,11 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
                 const float4 ra = s_rec[j].a;
                 const float4 rb = s_rec[j].b;
                 const float e = fmaf(ra.x, uu, fmaf(ra.y, vv, fmaf(ra.z, uv, fmaf(ra.w, cu, fmaf(rb.x, cv, rb.y)))));
-                if (!__any(!done && !(e < a.e_cut))) continue;
-                const float alpha = fminf(a.max_alpha, exp_f_sel(e));
+                const bool live = !done && !(e < a.e_cut);
+                if (!__any(live)) continue;
+                // exp_f(e): polynomial core unless a live lane is outside [-87, 88] (or NaN)
+                const float ex = __any(live && !(e >= -87.0f && e <= 88.0f)) ? exp_f_sel(e) : exp_f_core(e);
+                const float alpha = ex < a.max_alpha ? ex : a.max_alpha;   // fminf for a non-NaN max_alpha
                 const bool contrib = !done && !(alpha < a.min_alpha);
                 const float Tn = T * (1.0f - alpha);
                 const bool stop = contrib && Tn < a.min_T;
@@ -571,6 +574,7 @@ int tdgs_render_tiles(void* stream, const tdgs_camera* cam, const tdgs_tiling* t
     TDGS_TRY(check_tiling(tiling, cam));
     TDGS_REQUIRE(opt && buf && out, "null arguments");
     TDGS_REQUIRE(buf->tiles_end && buf->sorted_values && buf->f2d, "null buffers");
+    TDGS_TRY(check_thresholds(opt));
     TDGS_REQUIRE(!out->depth || buf->depths, "depth output needs depths");
     return launch_render_tiles((hipStream_t)stream, cam, tiling, opt, buf->key_capacity, buf->tiles_end,
                                buf->sorted_values, buf->f2d, buf->depths, out);
@@ -583,6 +587,7 @@ int tdgs_blend_evaluations(void* stream, const tdgs_camera* cam, const tdgs_tili
     TDGS_REQUIRE(opt && buf && evaluations_dev && buf->tiles_end && buf->sorted_values && buf->f2d,
                  "null arguments");
     TDGS_REQUIRE(nb_keys >= 0 && nb_keys <= buf->key_capacity, "bad key count");
+    TDGS_TRY(check_thresholds(opt));
     tdgs_render_outputs none = {nullptr, nullptr, nullptr, nullptr};
     return launch_render_tiles((hipStream_t)stream, cam, tiling, opt, nb_keys, buf->tiles_end, buf->sorted_values,
                                buf->f2d, buf->depths, &none, (unsigned long long*)evaluations_dev);

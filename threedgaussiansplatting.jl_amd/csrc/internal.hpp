@@ -77,11 +77,22 @@ inline int check_tiling(const tdgs_tiling* t, const tdgs_camera* cam) {
     return TDGS_OK;
 }
 
+// The blending kernels compare against these thresholds with selects that equal fminf only
+// for non-NaN operands.
+inline int check_thresholds(const tdgs_render_options* o) {
+    TDGS_REQUIRE(o != nullptr, "null options");
+    TDGS_REQUIRE(o->min_alpha == o->min_alpha && o->max_alpha == o->max_alpha &&
+                     o->min_transmittance == o->min_transmittance,
+                 "NaN alpha or transmittance threshold");
+    return TDGS_OK;
+}
+
 inline int check_options(const tdgs_render_options* o, int data_degree) {
     TDGS_REQUIRE(o != nullptr, "null options");
     TDGS_REQUIRE(o->sh_degree >= 0 && o->sh_degree <= data_degree,
                  "render SH degree %d exceeds the data's %d", o->sh_degree, data_degree);
     TDGS_REQUIRE(o->clip_mode == TDGS_CLIP_CLAMP || o->clip_mode == TDGS_CLIP_FILTER, "bad clip mode");
+    return check_thresholds(o);
     return TDGS_OK;
 }
 

@@ -92,6 +92,24 @@ TDGS_HD float exp_f_sel(float x) {
     return x > 88.72283935f ? kInf : (x > -87.33654475f ? v : ((x != x) ? x : 0.0f));
 }
 
+// exp_f on its polynomial range only: equal to exp_f(x) bit for bit for -87 <= x <= 88
+// (there n = rint(x log2 e) lies in [-126, 127], so neither special case nor the overflow
+// adjustment of exp_f applies). Callers check the range.
+TDGS_HD float exp_f_core(float x) {
+    const float n = rintf(x * kLog2e);
+    float r = fmaf(n, -kLn2Hi, x);
+    r = fmaf(n, -kLn2Lo, r);
+    float p = 1.98412698412698e-4f;
+    p = fmaf(p, r, 1.38888888888889e-3f);
+    p = fmaf(p, r, 8.33333333333333e-3f);
+    p = fmaf(p, r, 4.16666666666667e-2f);
+    p = fmaf(p, r, 1.66666666666667e-1f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return p * bits_float((uint32_t)((int)n + 127) << 23);
+}
+
 // log(x) for x > 0. x = m 2^e with m in [sqrt(1/2), sqrt(2)); log m = 2 atanh(s),
 // s = (m-1)/(m+1), by the odd series of atanh to s^11 (|s| <= 0.1716, remainder < 1e-11);
 // e ln2 added with the split constant. About 1 ulp. Subnormal inputs are scaled first.
