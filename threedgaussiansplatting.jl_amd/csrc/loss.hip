@@ -8,7 +8,9 @@
 //   k_ssim_forward   filters x, y, x^2, y^2, xy with the separable window (LDS tile with a
 //                    5-pixel halo), evaluates the SSIM map S and its partial derivatives
 //                    D1 = dS/dmu_x, D2 = dS/dE[x^2], D3 = dS/dE[xy] per pixel, and sums S
-//                    and |x - y| (workgroup reduction, one double atomic each)
+//                    and |x - y| per workgroup (one partial pair per workgroup; a one-block
+//                    launch adds the partials to the caller's sums, so no workgroup waits on
+//                    an atomic to a shared address)
 //   k_ssim_backward  filters D1, D2, D3 with the same window and forms
 //                    dL/dx = (1-lambda) sign(x - y)/N - lambda/N (G*D1 + 2 x G*D2 + y G*D3)
 // Images use the reference layout 3 x h x w (pixel (v, u) channel c at 3 (v + h u) + c).
@@ -24,6 +26,17 @@ constexpr int kSsimIn = kSsimT + 2 * kSsimR;
 constexpr float kC1 = 0.01f * 0.01f;
 constexpr float kC2 = 0.03f * 0.03f;
 
+// LDS layouts: a pixel's values are an odd number of words apart and a tile column starts at
+// a word offset = 16 (mod 32). A half-wavefront reads 16 consecutive rows of two adjacent
+// columns, so its 32 words fall on 32 distinct banks.
+constexpr int kInF = 7;                // forward input: x, y (3 channels each) + 1 pad
+constexpr int kPitchF = 208;           // >= kSsimIn * kInF, = 16 (mod 32)
+constexpr int kInB = 9;                // backward input: D1, D2, D3 (3 channels each)
+constexpr int kPitchB = 240;           // >= kSsimIn * kInB, = 16 (mod 32)
+static_assert(kPitchF >= kSsimIn * kInF && kPitchF % 32 == 16, "forward pitch");
+static_assert(kPitchB >= kSsimIn * kInB && kPitchB % 32 == 16, "backward pitch");
+static_assert((kSsimT * 15) % 32 == 16 && (kSsimT * 9) % 32 == 16, "filtered column pitch");
+
 struct SsimWindow {
     float w[2 * kSsimR + 1];
 };
@@ -32,8 +45,8 @@ struct SsimWindow {
 // v-filtered values of 5 quantities x 3 channels for 26 columns x 16 rows.
 __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ x, const float* __restrict__ y,
                                                       int W, int H, SsimWindow win, float* __restrict__ dmap,
-                                                      double* __restrict__ sums) {
-    __shared__ float s_in[kSsimIn * kSsimIn][6];
+                                                      double* __restrict__ partials) {
+    __shared__ float s_in[kSsimIn * kPitchF];      // (column iu, row iv, value) at iu*kPitchF + iv*kInF
     __shared__ float s_v[kSsimIn][kSsimT][15];
     __shared__ double s_red[2][256 / kWave];
     const int t = threadIdx.x;
@@ -43,10 +56,11 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
         const int v = v0 + iv, u = u0 + iu;
         const bool in = v >= 0 && v < H && u >= 0 && u < W;
         const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
+        float* d = s_in + iu * kPitchF + iv * kInF;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            s_in[k][c] = in ? x[p + c] : 0.0f;
-            s_in[k][3 + c] = in ? y[p + c] : 0.0f;
+            d[c] = in ? x[p + c] : 0.0f;
+            d[3 + c] = in ? y[p + c] : 0.0f;
         }
     }
     __syncthreads();
@@ -58,7 +72,7 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
         for (int q = 0; q < 15; ++q) acc[q] = 0.0f;
 #pragma unroll
         for (int d = 0; d < 2 * kSsimR + 1; ++d) {
-            const float* s = s_in[(ov + d) + kSsimIn * iu];
+            const float* s = s_in + iu * kPitchF + (ov + d) * kInF;
             const float wd = win.w[d];
 #pragma unroll
             for (int c = 0; c < 3; ++c) {
@@ -104,8 +118,8 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
             dmap[3 * p + 3 + c] = -S / b2;            // dS/dE[x^2]
             dmap[3 * p + 6 + c] = 2.0f * a1 / B;      // dS/dE[xy]
             ssum += (double)S;
-            l1 += fabs((double)s_in[(ov + kSsimR) + kSsimIn * (ou + kSsimR)][c] -
-                       (double)s_in[(ov + kSsimR) + kSsimIn * (ou + kSsimR)][3 + c]);
+            const float* px = s_in + (ou + kSsimR) * kPitchF + (ov + kSsimR) * kInF;
+            l1 += fabs((double)px[c] - (double)px[3 + c]);
         }
     }
     for (int d = 32; d >= 1; d >>= 1) {
@@ -120,8 +134,35 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     if (t == 0) {
         double a = 0.0, b = 0.0;
         for (int k = 0; k < 256 / kWave; ++k) { a += s_red[0][k]; b += s_red[1][k]; }
-        atomicAdd(&sums[0], b);  // sum |x - y|
-        atomicAdd(&sums[1], a);  // sum of the SSIM map
+        const int64_t blk = (int64_t)blockIdx.x + (int64_t)gridDim.x * blockIdx.y;
+        partials[2 * blk] = b;      // sum |x - y|
+        partials[2 * blk + 1] = a;  // sum of the SSIM map
+    }
+}
+
+// One workgroup: sums[k] += sum over the nblk partial pairs.
+__global__ __launch_bounds__(1024) void k_ssim_sums(const double* __restrict__ partials, int64_t nblk,
+                                                    double* __restrict__ sums) {
+    __shared__ double s_red[2][1024 / kWave];
+    double a = 0.0, b = 0.0;
+    for (int64_t i = threadIdx.x; i < nblk; i += 1024) {
+        a += partials[2 * i];
+        b += partials[2 * i + 1];
+    }
+    for (int d = 32; d >= 1; d >>= 1) {
+        a += __shfl_xor(a, d, kWave);
+        b += __shfl_xor(b, d, kWave);
+    }
+    if (__lane_id() == 0) {
+        s_red[0][threadIdx.x / kWave] = a;
+        s_red[1][threadIdx.x / kWave] = b;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double ta = 0.0, tb = 0.0;
+        for (int k = 0; k < 1024 / kWave; ++k) { ta += s_red[0][k]; tb += s_red[1][k]; }
+        sums[0] += ta;
+        sums[1] += tb;
     }
 }
 
@@ -129,7 +170,7 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
                                                        int W, int H, SsimWindow win,
                                                        const float* __restrict__ dmap, float w_l1, float w_ssim,
                                                        float* __restrict__ grad) {
-    __shared__ float s_in[kSsimIn * kSsimIn][9];
+    __shared__ float s_in[kSsimIn * kPitchB];      // (column iu, row iv, value) at iu*kPitchB + iv*kInB
     __shared__ float s_v[kSsimIn][kSsimT][9];
     const int t = threadIdx.x;
     const int v0 = blockIdx.x * kSsimT - kSsimR, u0 = blockIdx.y * kSsimT - kSsimR;
@@ -138,8 +179,9 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         const int v = v0 + iv, u = u0 + iu;
         const bool in = v >= 0 && v < H && u >= 0 && u < W;
         const int64_t p = 9 * ((int64_t)v + (int64_t)H * u);
+        float* d = s_in + iu * kPitchB + iv * kInB;
 #pragma unroll
-        for (int q = 0; q < 9; ++q) s_in[k][q] = in ? dmap[p + q] : 0.0f;
+        for (int q = 0; q < 9; ++q) d[q] = in ? dmap[p + q] : 0.0f;
     }
     __syncthreads();
     for (int k = t; k < kSsimIn * kSsimT; k += 256) {
@@ -149,7 +191,7 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         for (int q = 0; q < 9; ++q) acc[q] = 0.0f;
 #pragma unroll
         for (int d = 0; d < 2 * kSsimR + 1; ++d) {
-            const float* s = s_in[(ov + d) + kSsimIn * iu];
+            const float* s = s_in + iu * kPitchB + (ov + d) * kInB;
             const float wd = win.w[d];
 #pragma unroll
             for (int q = 0; q < 9; ++q) acc[q] = fmaf(wd, s[q], acc[q]);
@@ -198,8 +240,16 @@ using namespace tdgs;
 
 extern "C" {
 
-size_t tdgs_loss_temp_bytes(int32_t width, int32_t height) {
+// Scratch: the 9 SSIM partial-derivative maps, then one (|x - y|, S) sum pair per workgroup.
+static size_t loss_dmap_bytes(int32_t width, int32_t height) {
     return align_up((size_t)9 * sizeof(float) * (size_t)(width > 0 ? width : 1) * (size_t)(height > 0 ? height : 1));
+}
+static int64_t loss_blocks(int32_t width, int32_t height) {
+    return ceil_div(height > 0 ? height : 1, kSsimT) * ceil_div(width > 0 ? width : 1, kSsimT);
+}
+
+size_t tdgs_loss_temp_bytes(int32_t width, int32_t height) {
+    return loss_dmap_bytes(width, height) + align_up((size_t)loss_blocks(width, height) * 2 * sizeof(double));
 }
 
 int tdgs_loss_grad(void* stream, const float* rendered, const float* gt, int32_t width, int32_t height,
@@ -212,7 +262,10 @@ int tdgs_loss_grad(void* stream, const float* rendered, const float* gt, int32_t
     const SsimWindow win = gaussian_window();
     const int64_t count = 3 * (int64_t)width * height;
     const dim3 grid((unsigned)ceil_div(height, kSsimT), (unsigned)ceil_div(width, kSsimT));
-    k_ssim_forward<<<grid, 256, 0, s>>>(rendered, gt, width, height, win, (float*)temp, sums_dev);
+    double* partials = (double*)((char*)temp + loss_dmap_bytes(width, height));
+    k_ssim_forward<<<grid, 256, 0, s>>>(rendered, gt, width, height, win, (float*)temp, partials);
+    TDGS_LAUNCHED();
+    k_ssim_sums<<<1, 1024, 0, s>>>(partials, loss_blocks(width, height), sums_dev);
     TDGS_LAUNCHED();
     const float w_l1 = (1.0f - dssim_weight) / (float)count;
     const float w_ssim = dssim_weight / (float)count;
