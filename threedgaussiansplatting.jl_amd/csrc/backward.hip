@@ -242,50 +242,168 @@ struct BackProjectArgs {
 };
 
 // backward_project_fgaussians_kernel! (backward_core.jl:309-452) + compute_sh_coeffs_grad!
-__global__ __launch_bounds__(256) void k_backward_project(BackProjectArgs a) {
-    const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (f >= a.nbf) return;
+// A workgroup takes kBpThreads consecutive filtered Gaussians. Its non-empty ones (count > 0)
+// are compacted to the first lanes, so only ceil(active / 64) wavefronts run the projection
+// chain; empty ones get zero gradients. SH coefficient blocks (read) and SH gradient blocks
+// (written) pass through one LDS array with an odd row stride, so global memory sees
+// contiguous runs instead of one 192-byte block per lane.
+constexpr int kBpThreads = 256;
+constexpr int kShRow = 49;   // >= 48 coefficients, odd: rows of consecutive lanes hit distinct banks
+constexpr int kBpUnroll = 16;
+
+__global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs a) {
+    __shared__ float s_sh[kBpThreads * kShRow];   // row = local index of the Gaussian
+    __shared__ int32_t s_gi[kBpThreads];          // gidx (0-based) of active Gaussians, else -1
+    __shared__ int16_t s_list[kBpThreads];        // local indices of the active Gaussians
+    __shared__ int32_t s_wcnt[kBpThreads / kWave];
+    const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+    const int64_t f0 = (int64_t)blockIdx.x * kBpThreads;
+    const int64_t fz = f0 + t;
+    const bool valid = fz < a.nbf;
+    const bool active = valid && a.counts[fz] != 0;
+    s_gi[t] = active ? a.fgidx_to_gidx[fz] - 1 : -1;
+    const uint64_t act = __ballot(active);
+    if (lane == 0) s_wcnt[wave] = __popcll(act);
+    if (valid && !active) {
+        a.gr.mean3d[3 * fz] = 0.0f; a.gr.mean3d[3 * fz + 1] = 0.0f; a.gr.mean3d[3 * fz + 2] = 0.0f;
+        a.gr.opacity_feature[fz] = 0.0f;
+        a.gr.scaling_features[3 * fz] = 0.0f; a.gr.scaling_features[3 * fz + 1] = 0.0f;
+        a.gr.scaling_features[3 * fz + 2] = 0.0f;
+        reinterpret_cast<float4*>(a.gr.rotation_features)[fz] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     const int hg = (a.gr.sh_degree + 1) * (a.gr.sh_degree + 1);
     const int hr = (a.opt.sh_degree + 1) * (a.opt.sh_degree + 1);
-    float* dsh = a.gr.sh + (int64_t)3 * hg * f;
-    if (a.counts[f] == 0) {
-        for (int k = 0; k < 3; ++k) a.gr.mean3d[3 * f + k] = 0.0f;
-        a.gr.opacity_feature[f] = 0.0f;
-        for (int k = 0; k < 3; ++k) a.gr.scaling_features[3 * f + k] = 0.0f;
-        reinterpret_cast<float4*>(a.gr.rotation_features)[f] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int c = 0; c < 3; ++c)
-            for (int k = 0; k < hr; ++k) dsh[c * hg + k] = 0.0f;
-        return;
-    }
-    const int64_t gi = (int64_t)a.fgidx_to_gidx[f] - 1;
     const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
-    BackwardProjectIn in;
-    const float4 mo = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
-    in.m[0] = mo.x; in.m[1] = mo.y; in.m[2] = mo.z;
-    in.logit = mo.w;
-    in.logs[0] = a.g.scaling[3 * gi];
-    in.logs[1] = a.g.scaling[3 * gi + 1];
-    in.logs[2] = a.g.scaling[3 * gi + 2];
-    const float4 q = reinterpret_cast<const float4*>(a.g.rotation)[gi];
-    in.q[0] = q.x; in.q[1] = q.y; in.q[2] = q.z; in.q[3] = q.w;
-    in.sh = a.g.sh + (int64_t)3 * hs * gi;
-    in.h_storage = hs;
-    const float* r = a.f2d + 9 * f;
-    in.mux = r[0]; in.muy = r[1]; in.a = r[2]; in.m11 = r[3]; in.m21 = r[4]; in.m22 = r[5];
-    in.rgb[0] = r[6]; in.rgb[1] = r[7]; in.rgb[2] = r[8];
-    const float* g2 = a.gr.grads2d + 9 * f;
+    __syncthreads();
+    int before = 0, n_act = 0;
+    for (int w = 0; w < kBpThreads / kWave; ++w) {
+        if (w < wave) before += s_wcnt[w];
+        n_act += s_wcnt[w];
+    }
+    if (active) s_list[before + __popcll(act & lanemask_lt())] = (int16_t)t;
+    // coefficients of the active Gaussians: thread t moves flat items i = t + kBpThreads r
+    // (r < 3hs) of the [kBpThreads][3hs] block, (row j, column e) stepped without a division;
+    // kBpUnroll loads are issued before their LDS stores so they overlap
+    if (hs == 16) {
+        // 48-float rows as 12 float4 each: thread t moves float4 items t + kBpThreads r (r < 12),
+        // all in flight at once
+        float4 val[12];
 #pragma unroll
-    for (int k = 0; k < 9; ++k) in.g2[k] = g2[k];
-    const BackwardProjectOut o = backward_project(in, a.cam, a.opt);
-    for (int k = 0; k < 3; ++k) a.gr.mean3d[3 * f + k] = o.dm[k];
-    a.gr.opacity_feature[f] = o.dlogit;
-    for (int k = 0; k < 3; ++k) a.gr.scaling_features[3 * f + k] = o.dlogs[k];
-    reinterpret_cast<float4*>(a.gr.rotation_features)[f] = make_float4(o.dq[0], o.dq[1], o.dq[2], o.dq[3]);
+        for (int r = 0; r < 12; ++r) {
+            const int i = t + kBpThreads * r, j = i / 12, q = i - 12 * j;
+            const int32_t gj = s_gi[j];
+            if (gj >= 0) val[r] = reinterpret_cast<const float4*>(a.g.sh)[(int64_t)12 * gj + q];
+        }
+#pragma unroll
+        for (int r = 0; r < 12; ++r) {
+            const int i = t + kBpThreads * r, j = i / 12, q = i - 12 * j;
+            if (s_gi[j] >= 0) {
+                float* d = s_sh + j * kShRow + 4 * q;
+                d[0] = val[r].x; d[1] = val[r].y; d[2] = val[r].z; d[3] = val[r].w;
+            }
+        }
+    } else {
+        const int w = 3 * hs, dj = kBpThreads / w, de = kBpThreads - dj * w;
+        int j = t / w, e = t - j * w;
+        for (int r0 = 0; r0 < w; r0 += kBpUnroll) {
+            float val[kBpUnroll];
+            int dst[kBpUnroll];
+#pragma unroll
+            for (int u = 0; u < kBpUnroll; ++u) {
+                dst[u] = -1;
+                if (r0 + u < w) {
+                    const int32_t gj = s_gi[j];
+                    if (gj >= 0) {
+                        val[u] = a.g.sh[(int64_t)w * gj + e];
+                        dst[u] = j * kShRow + e;
+                    }
+                    j += dj;
+                    e += de;
+                    if (e >= w) { e -= w; ++j; }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kBpUnroll; ++u)
+                if (dst[u] >= 0) s_sh[dst[u]] = val[u];
+        }
+    }
+    __syncthreads();
+    const bool worker = t < n_act;
+    const int jl = worker ? s_list[t] : 0;
+    const int64_t f = f0 + jl;
     float b[16];
-    sh_grad_basis(a.cam, a.opt.sh_degree, in.m, b);
-    for (int c = 0; c < 3; ++c) {
-        const float dc = in.g2[6 + c];
-        for (int k = 0; k < hr; ++k) dsh[c * hg + k] = dc * b[k];
+    float dcol[3] = {0.0f, 0.0f, 0.0f};
+    if (worker) {
+        const int64_t gi = s_gi[jl];
+        BackwardProjectIn in;
+        const float4 mo = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
+        in.m[0] = mo.x; in.m[1] = mo.y; in.m[2] = mo.z;
+        in.logit = mo.w;
+        in.logs[0] = a.g.scaling[3 * gi];
+        in.logs[1] = a.g.scaling[3 * gi + 1];
+        in.logs[2] = a.g.scaling[3 * gi + 2];
+        const float4 q = reinterpret_cast<const float4*>(a.g.rotation)[gi];
+        in.q[0] = q.x; in.q[1] = q.y; in.q[2] = q.z; in.q[3] = q.w;
+        in.sh = s_sh + jl * kShRow;
+        in.h_storage = hs;
+        const float* r = a.f2d + 9 * f;
+        in.mux = r[0]; in.muy = r[1]; in.a = r[2]; in.m11 = r[3]; in.m21 = r[4]; in.m22 = r[5];
+        in.rgb[0] = r[6]; in.rgb[1] = r[7]; in.rgb[2] = r[8];
+        const float* g2 = a.gr.grads2d + 9 * f;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) in.g2[k] = g2[k];
+        const BackwardProjectOut o = backward_project(in, a.cam, a.opt);
+        for (int k = 0; k < 3; ++k) a.gr.mean3d[3 * f + k] = o.dm[k];
+        a.gr.opacity_feature[f] = o.dlogit;
+        for (int k = 0; k < 3; ++k) a.gr.scaling_features[3 * f + k] = o.dlogs[k];
+        reinterpret_cast<float4*>(a.gr.rotation_features)[f] = make_float4(o.dq[0], o.dq[1], o.dq[2], o.dq[3]);
+        sh_grad_basis(a.cam, a.opt.sh_degree, in.m, b);
+        dcol[0] = in.g2[6]; dcol[1] = in.g2[7]; dcol[2] = in.g2[8];
+    }
+    __syncthreads();   // every coefficient read is done: s_sh now takes the SH gradients
+    // SH gradients: channel c, coefficient k at column c * hg + k (k < hr); the rows of empty
+    // Gaussians are zero; columns k >= hr are left untouched in global memory
+    if (worker)
+        for (int c = 0; c < 3; ++c)
+            for (int k = 0; k < hr; ++k) s_sh[jl * kShRow + c * hg + k] = dcol[c] * b[k];
+    if (!active)
+        for (int c = 0; c < 3; ++c)
+            for (int k = 0; k < hr; ++k) s_sh[t * kShRow + c * hg + k] = 0.0f;
+    __syncthreads();
+    float* dsh = a.gr.sh + (int64_t)3 * hg * f0;
+    const int nrows = (int)(a.nbf - f0 < kBpThreads ? a.nbf - f0 : kBpThreads);
+    if (hg == 16 && hr == 16) {
+        // every column written: float4 stores of 12 items per thread
+#pragma unroll
+        for (int r = 0; r < 12; ++r) {
+            const int i = t + kBpThreads * r, j = i / 12, q = i - 12 * j;
+            if (j < nrows) {
+                const float* sv = s_sh + j * kShRow + 4 * q;
+                reinterpret_cast<float4*>(dsh)[i] = make_float4(sv[0], sv[1], sv[2], sv[3]);
+            }
+        }
+    } else {
+        const int w = 3 * hg, dj = kBpThreads / w, de = kBpThreads - dj * w;
+        int j = t / w, e = t - j * w;
+        for (int r0 = 0; r0 < w; r0 += kBpUnroll) {
+            float val[kBpUnroll];
+            bool st[kBpUnroll];
+#pragma unroll
+            for (int u = 0; u < kBpUnroll; ++u) {
+                st[u] = false;
+                if (r0 + u < w) {
+                    const int k = e - (e >= hg ? hg : 0) - (e >= 2 * hg ? hg : 0);   // e mod hg
+                    st[u] = j < nrows && k < hr;
+                    if (st[u]) val[u] = s_sh[j * kShRow + e];
+                    j += dj;
+                    e += de;
+                    if (e >= w) { e -= w; ++j; }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kBpUnroll; ++u)
+                if (st[u]) dsh[t + kBpThreads * (r0 + u)] = val[u];
+        }
     }
 }
 

@@ -78,38 +78,91 @@ struct ProjectArgs {
     int32_t* depth_vals;      // optional: fgidx (1-based), 0 for unused slots
 };
 
-__global__ __launch_bounds__(256) void k_project(ProjectArgs a) {
-    const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (f >= a.cap) return;
+// One thread per filtered Gaussian. The SH blocks of the workgroup's non-empty Gaussians are
+// staged in LDS (odd row stride) by cooperative loads (float4 for 16-coefficient storage,
+// all in flight at once) before the colours are evaluated.
+constexpr int kProjThreads = 256;
+constexpr int kProjShRow = 49;
+constexpr int kProjUnroll = 16;
+
+__global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
+    __shared__ float s_sh[kProjThreads * kProjShRow];
+    __shared__ int32_t s_gi[kProjThreads];   // gidx (0-based) of non-empty Gaussians, else -1
+    const int t = threadIdx.x;
+    const int64_t f = (int64_t)blockIdx.x * kProjThreads + t;
     const int64_t nbf = a.d_nbf ? *a.d_nbf : a.nbf;
-    if (f >= nbf) {
-        if (a.depth_keys) {
-            a.depth_keys[f] = 0xffffffffu;
-            a.depth_vals[f] = 0;
-        }
-        return;
-    }
-    const int64_t gi = (int64_t)a.fgidx_to_gidx[f] - 1;
-    const float4 m = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
-    const float op = opacity_of(a.g.kind, m.w);
-    float params[7];
-    if (a.g.kind == TDGS_TRAINABLE) {
-        params[0] = a.g.scaling[3 * gi];
-        params[1] = a.g.scaling[3 * gi + 1];
-        params[2] = a.g.scaling[3 * gi + 2];
-        const float4 q = reinterpret_cast<const float4*>(a.g.rotation)[gi];
-        params[3] = q.x; params[4] = q.y; params[5] = q.z; params[6] = q.w;
-    } else {
+    const bool valid = f < a.cap && f < nbf;
+    Projected pr;
+    pr.count = 0;
+    int64_t gi = -1;
+    float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (valid) {
+        gi = (int64_t)a.fgidx_to_gidx[f] - 1;
+        m = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
+        const float op = opacity_of(a.g.kind, m.w);
+        float params[7];
+        if (a.g.kind == TDGS_TRAINABLE) {
+            params[0] = a.g.scaling[3 * gi];
+            params[1] = a.g.scaling[3 * gi + 1];
+            params[2] = a.g.scaling[3 * gi + 2];
+            const float4 q = reinterpret_cast<const float4*>(a.g.rotation)[gi];
+            params[3] = q.x; params[4] = q.y; params[5] = q.z; params[6] = q.w;
+        } else {
 #pragma unroll
-        for (int k = 0; k < 6; ++k) params[k] = a.g.covariances[6 * gi + k];
+            for (int k = 0; k < 6; ++k) params[k] = a.g.covariances[6 * gi + k];
+        }
+        pr = project_geometry(a.cam, a.opt, a.tiling, a.g.kind, m.x, m.y, m.z, op, params);
+        a.counts[f] = pr.count;
     }
-    const Projected pr = project_geometry(a.cam, a.opt, a.tiling, a.g.kind, m.x, m.y, m.z, op, params);
-    a.counts[f] = pr.count;
+    s_gi[t] = pr.count > 0 ? (int32_t)gi : -1;
+    const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
+    __syncthreads();
+    if (hs == 16) {
+        float4 val[12];
+#pragma unroll
+        for (int r = 0; r < 12; ++r) {
+            const int i = t + kProjThreads * r, j = i / 12, q = i - 12 * j;
+            const int32_t gj = s_gi[j];
+            if (gj >= 0) val[r] = reinterpret_cast<const float4*>(a.g.sh)[(int64_t)12 * gj + q];
+        }
+#pragma unroll
+        for (int r = 0; r < 12; ++r) {
+            const int i = t + kProjThreads * r, j = i / 12, q = i - 12 * j;
+            if (s_gi[j] >= 0) {
+                float* d = s_sh + j * kProjShRow + 4 * q;
+                d[0] = val[r].x; d[1] = val[r].y; d[2] = val[r].z; d[3] = val[r].w;
+            }
+        }
+    } else {
+        const int w = 3 * hs, dj = kProjThreads / w, de = kProjThreads - dj * w;
+        int j = t / w, e = t - j * w;
+        for (int r0 = 0; r0 < w; r0 += kProjUnroll) {
+            float val[kProjUnroll];
+            int dst[kProjUnroll];
+#pragma unroll
+            for (int u = 0; u < kProjUnroll; ++u) {
+                dst[u] = -1;
+                if (r0 + u < w) {
+                    const int32_t gj = s_gi[j];
+                    if (gj >= 0) {
+                        val[u] = a.g.sh[(int64_t)w * gj + e];
+                        dst[u] = j * kProjShRow + e;
+                    }
+                    j += dj;
+                    e += de;
+                    if (e >= w) { e -= w; ++j; }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kProjUnroll; ++u)
+                if (dst[u] >= 0) s_sh[dst[u]] = val[u];
+        }
+    }
+    __syncthreads();
     uint32_t dk = 0xffffffffu;
     if (pr.count > 0) {
-        const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
         float rgb[3];
-        project_color(a.cam, a.opt.sh_degree, a.g.sh + (int64_t)3 * hs * gi, hs, m.x, m.y, m.z, rgb);
+        project_color(a.cam, a.opt.sh_degree, s_sh + t * kProjShRow, hs, m.x, m.y, m.z, rgb);
         a.depths[f] = pr.depth;
         reinterpret_cast<int4*>(a.ranges)[f] = make_int4(pr.rect[0], pr.rect[1], pr.rect[2], pr.rect[3]);
         float* r = a.f2d + 9 * f;
@@ -118,9 +171,9 @@ __global__ __launch_bounds__(256) void k_project(ProjectArgs a) {
         r[6] = rgb[0]; r[7] = rgb[1]; r[8] = rgb[2];
         dk = float_bits(pr.depth);
     }
-    if (a.depth_keys) {
+    if (a.depth_keys && f < a.cap) {
         a.depth_keys[f] = dk;
-        a.depth_vals[f] = (int32_t)(f + 1);
+        a.depth_vals[f] = valid ? (int32_t)(f + 1) : 0;
     }
 }
 
