@@ -10,12 +10,16 @@
 namespace tdgs {
 
 // ------------------------------------------------------------------------------------
-// Adam (update!, optimizer.jl:964-1009): one wavefront per filtered Gaussian, one lane per
-// scalar parameter — lanes 0-2 mean, 3 opacity logit, 4-6 log-scales, 7-10 quaternion,
-// 11.. the first (d+1)^2 coefficients of each colour channel (d = render SH degree). The
-// reference runs five launches (one per component); here one launch streams every
-// component, and the per-Gaussian SH segments (params, gradients, moment pairs) are read
-// and written contiguously by consecutive lanes.
+// Adam (update!, optimizer.jl:964-1009) over the filtered Gaussians; entries whose
+// fgidx_to_gidx is 0 (removed by adaptive density control) are skipped. The reference runs five
+// launches (one per component); here one launch streams every component, as two kinds of
+// items in one grid:
+//   SH items        the first (d+1)^2 coefficients of each colour channel (d = render SH
+//                   degree). When the parameter, gradient and render blocks coincide and
+//                   hold a multiple of 4 floats, an item is a float4 of parameters with its
+//                   float4 of gradients and two float4 of (m, v) moment pairs, so every
+//                   array is streamed in 16-byte pieces; otherwise an item is one scalar.
+//   geometry items  one Gaussian: mean (3), opacity logit, log-scales (3), quaternion (4).
 // ------------------------------------------------------------------------------------
 
 struct AdamArgs {
@@ -36,49 +40,89 @@ struct AdamArgs {
     const int32_t* fgidx_to_gidx;
     int64_t nbf;
     int hs, hg, hr;
-    float lr[6];   // means, opacity, scaling, rotation, sh dc, sh rest
+    int vec;            // SH items are float4 (hs == hg == hr, 3 hr % 4 == 0)
+    int64_t sh_items;   // number of SH items
+    int64_t sh_blocks;  // blocks [0, sh_blocks) take SH items, the rest geometry items
+    float lr[6];        // means, opacity, scaling, rotation, sh dc, sh rest
     float beta1, beta2, omb1, omb2, bc1, bc2, eps;
 };
 
+__device__ __forceinline__ void adam1(const AdamArgs& a, float& p, float g, float& m1, float& m2, float lr) {
+    adam_scalar(p, g, m1, m2, lr, a.beta1, a.beta2, a.omb1, a.omb2, a.bc1, a.bc2, a.eps);
+}
+
 __global__ __launch_bounds__(256) void k_adam(AdamArgs a) {
-    const int lane = __lane_id();
-    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
-    const int64_t nwaves = ((int64_t)gridDim.x * blockDim.x) / kWave;
-    const int nscalar = 11 + 3 * a.hr;
-    for (int64_t f = wave; f < a.nbf; f += nwaves) {
-        const int64_t gi = (int64_t)a.fgidx_to_gidx[f] - 1;
-        if (gi < 0 || lane >= nscalar) continue;
-        float* p;
-        float* m;
-        float g, lr;
-        if (lane < 3) {
-            p = a.mo + 4 * gi + lane; m = a.m_means + 6 * gi + 2 * lane;
-            g = a.g_mean[3 * f + lane]; lr = a.lr[0];
-        } else if (lane == 3) {
-            p = a.mo + 4 * gi + 3; m = a.m_op + 2 * gi;
-            g = a.g_op[f]; lr = a.lr[1];
-        } else if (lane < 7) {
-            const int k = lane - 4;
-            p = a.sc + 3 * gi + k; m = a.m_sc + 6 * gi + 2 * k;
-            g = a.g_sc[3 * f + k]; lr = a.lr[2];
-        } else if (lane < 11) {
-            const int k = lane - 7;
-            p = a.rot + 4 * gi + k; m = a.m_rot + 8 * gi + 2 * k;
-            g = a.g_rot[4 * f + k]; lr = a.lr[3];
+    if ((int64_t)blockIdx.x < a.sh_blocks) {
+        const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= a.sh_items) return;
+        if (a.vec) {
+            const int q4 = 3 * a.hr / 4;                 // float4 per Gaussian block
+            const int64_t f = i / q4;
+            const int q = (int)(i - f * q4);
+            const int64_t gi = (int64_t)a.fgidx_to_gidx[f] - 1;
+            if (gi < 0) return;                          // entry removed by density control
+            const int k0 = (4 * q) % a.hr;               // coefficient index of the first lane
+            float4* pp = reinterpret_cast<float4*>(a.sh + (int64_t)3 * a.hs * gi) + q;
+            float4* mp = reinterpret_cast<float4*>(a.m_sh + (int64_t)6 * a.hs * gi) + 2 * q;
+            const float4 g = reinterpret_cast<const float4*>(a.g_sh + (int64_t)3 * a.hg * f)[q];
+            float4 p = *pp, m0 = mp[0], m1 = mp[1];
+            adam1(a, p.x, g.x, m0.x, m0.y, k0 == 0 ? a.lr[4] : a.lr[5]);
+            adam1(a, p.y, g.y, m0.z, m0.w, a.lr[5]);
+            adam1(a, p.z, g.z, m1.x, m1.y, a.lr[5]);
+            adam1(a, p.w, g.w, m1.z, m1.w, a.lr[5]);
+            *pp = p;
+            mp[0] = m0;
+            mp[1] = m1;
         } else {
-            const int l = lane - 11;
-            const int c = l / a.hr, k = l - c * a.hr;
+            const int per = 3 * a.hr;
+            const int64_t f = i / per;
+            const int e = (int)(i - f * per), c = e / a.hr, k = e - c * a.hr;
+            const int64_t gi = (int64_t)a.fgidx_to_gidx[f] - 1;
+            if (gi < 0) return;
             const int64_t pi = (int64_t)3 * a.hs * gi + (int64_t)c * a.hs + k;
-            p = a.sh + pi; m = a.m_sh + 2 * pi;
-            g = a.g_sh[(int64_t)3 * a.hg * f + (int64_t)c * a.hg + k];
-            lr = k == 0 ? a.lr[4] : a.lr[5];
+            float p = a.sh[pi];
+            float2 m = reinterpret_cast<float2*>(a.m_sh)[pi];
+            adam1(a, p, a.g_sh[(int64_t)3 * a.hg * f + (int64_t)c * a.hg + k], m.x, m.y, k == 0 ? a.lr[4] : a.lr[5]);
+            a.sh[pi] = p;
+            reinterpret_cast<float2*>(a.m_sh)[pi] = m;
         }
-        float pv = *p;
-        float2 mv = *reinterpret_cast<float2*>(m);
-        adam_scalar(pv, g, mv.x, mv.y, lr, a.beta1, a.beta2, a.omb1, a.omb2, a.bc1, a.bc2, a.eps);
-        *p = pv;
-        *reinterpret_cast<float2*>(m) = mv;
+        return;
     }
+    const int64_t f = ((int64_t)blockIdx.x - a.sh_blocks) * blockDim.x + threadIdx.x;
+    if (f >= a.nbf) return;
+    const int64_t gi = (int64_t)a.fgidx_to_gidx[f] - 1;
+    if (gi < 0) return;
+    float4 mo = reinterpret_cast<float4*>(a.mo)[gi];
+    float2* mm = reinterpret_cast<float2*>(a.m_means) + 3 * gi;
+    float2 m0 = mm[0], m1 = mm[1], m2 = mm[2];
+    adam1(a, mo.x, a.g_mean[3 * f], m0.x, m0.y, a.lr[0]);
+    adam1(a, mo.y, a.g_mean[3 * f + 1], m1.x, m1.y, a.lr[0]);
+    adam1(a, mo.z, a.g_mean[3 * f + 2], m2.x, m2.y, a.lr[0]);
+    float2 mop = reinterpret_cast<float2*>(a.m_op)[gi];
+    adam1(a, mo.w, a.g_op[f], mop.x, mop.y, a.lr[1]);
+    reinterpret_cast<float4*>(a.mo)[gi] = mo;
+    mm[0] = m0; mm[1] = m1; mm[2] = m2;
+    reinterpret_cast<float2*>(a.m_op)[gi] = mop;
+    float2* ms = reinterpret_cast<float2*>(a.m_sc) + 3 * gi;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        float p = a.sc[3 * gi + k];
+        float2 m = ms[k];
+        adam1(a, p, a.g_sc[3 * f + k], m.x, m.y, a.lr[2]);
+        a.sc[3 * gi + k] = p;
+        ms[k] = m;
+    }
+    float4 r = reinterpret_cast<float4*>(a.rot)[gi];
+    const float4 gr = reinterpret_cast<const float4*>(a.g_rot)[f];
+    float4* mr = reinterpret_cast<float4*>(a.m_rot) + 2 * gi;
+    float4 ma = mr[0], mb = mr[1];
+    adam1(a, r.x, gr.x, ma.x, ma.y, a.lr[3]);
+    adam1(a, r.y, gr.y, ma.z, ma.w, a.lr[3]);
+    adam1(a, r.z, gr.z, mb.x, mb.y, a.lr[3]);
+    adam1(a, r.w, gr.w, mb.z, mb.w, a.lr[3]);
+    reinterpret_cast<float4*>(a.rot)[gi] = r;
+    mr[0] = ma;
+    mr[1] = mb;
 }
 
 // ------------------------------------------------------------------------------------
@@ -341,10 +385,11 @@ int tdgs_adam_step(void* stream, tdgs_gaussians* g, tdgs_adam_state* st, const t
         a.bc1 = (float)(1.0 - pow((double)st->beta1, t));
         a.bc2 = (float)(1.0 - pow((double)st->beta2, t));
         a.eps = st->epsilon;
-        const int64_t waves_needed = nb_fgaussians;
-        const int64_t blocks = ceil_div(waves_needed * kWave, 256);
-        const unsigned grid = (unsigned)(blocks < 65536 ? blocks : 65536);
-        k_adam<<<grid, 256, 0, s>>>(a);
+        a.vec = (a.hs == a.hg && a.hg == a.hr && (3 * a.hr) % 4 == 0) ? 1 : 0;
+        a.sh_items = (int64_t)nb_fgaussians * (a.vec ? 3 * a.hr / 4 : 3 * a.hr);
+        a.sh_blocks = ceil_div(a.sh_items, 256);
+        const int64_t blocks = a.sh_blocks + ceil_div(nb_fgaussians, 256);
+        k_adam<<<(unsigned)blocks, 256, 0, s>>>(a);
         TDGS_LAUNCHED();
     }
     st->update_count += 1;
