@@ -37,6 +37,19 @@ static_assert(kPitchF >= kSsimIn * kInF && kPitchF % 32 == 16, "forward pitch");
 static_assert(kPitchB >= kSsimIn * kInB && kPitchB % 32 == 16, "backward pitch");
 static_assert((kSsimT * 15) % 32 == 16 && (kSsimT * 9) % 32 == 16, "filtered column pitch");
 
+// XCD-aware tile order: workgroups are handed to the 8 XCDs round-robin by linear id, so the
+// workgroups with id = x (mod 8) all run on XCD x. They get one contiguous band of tiles (v
+// fastest), whose shared halos then stay in that XCD's L2. A bijection on the first
+// 8 * floor(n / 8) ids; the remainder keeps its own index.
+constexpr int kXcds = 8;
+__device__ __forceinline__ void ssim_tile(int ntv, int n, int* tv, int* tu) {
+    const int b = blockIdx.x;
+    const int per = n / kXcds;
+    const int L = b < per * kXcds ? (b % kXcds) * per + b / kXcds : b;
+    *tv = L % ntv;
+    *tu = L / ntv;
+}
+
 struct SsimWindow {
     float w[2 * kSsimR + 1];
 };
@@ -50,7 +63,9 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     __shared__ float s_v[kSsimIn][kSsimT][15];
     __shared__ double s_red[2][256 / kWave];
     const int t = threadIdx.x;
-    const int v0 = blockIdx.x * kSsimT - kSsimR, u0 = blockIdx.y * kSsimT - kSsimR;
+    int tv, tu;
+    ssim_tile((H + kSsimT - 1) / kSsimT, gridDim.x, &tv, &tu);
+    const int v0 = tv * kSsimT - kSsimR, u0 = tu * kSsimT - kSsimR;
     for (int k = t; k < kSsimIn * kSsimIn; k += 256) {
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
@@ -134,7 +149,7 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     if (t == 0) {
         double a = 0.0, b = 0.0;
         for (int k = 0; k < 256 / kWave; ++k) { a += s_red[0][k]; b += s_red[1][k]; }
-        const int64_t blk = (int64_t)blockIdx.x + (int64_t)gridDim.x * blockIdx.y;
+        const int64_t blk = blockIdx.x;
         partials[2 * blk] = b;      // sum |x - y|
         partials[2 * blk + 1] = a;  // sum of the SSIM map
     }
@@ -173,7 +188,9 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
     __shared__ float s_in[kSsimIn * kPitchB];      // (column iu, row iv, value) at iu*kPitchB + iv*kInB
     __shared__ float s_v[kSsimIn][kSsimT][9];
     const int t = threadIdx.x;
-    const int v0 = blockIdx.x * kSsimT - kSsimR, u0 = blockIdx.y * kSsimT - kSsimR;
+    int tv, tu;
+    ssim_tile((H + kSsimT - 1) / kSsimT, gridDim.x, &tv, &tu);
+    const int v0 = tv * kSsimT - kSsimR, u0 = tu * kSsimT - kSsimR;
     for (int k = t; k < kSsimIn * kSsimIn; k += 256) {
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
@@ -261,7 +278,7 @@ int tdgs_loss_grad(void* stream, const float* rendered, const float* gt, int32_t
     StageScope sc(TDGS_STAGE_LOSS, s);
     const SsimWindow win = gaussian_window();
     const int64_t count = 3 * (int64_t)width * height;
-    const dim3 grid((unsigned)ceil_div(height, kSsimT), (unsigned)ceil_div(width, kSsimT));
+    const unsigned grid = (unsigned)loss_blocks(width, height);
     double* partials = (double*)((char*)temp + loss_dmap_bytes(width, height));
     k_ssim_forward<<<grid, 256, 0, s>>>(rendered, gt, width, height, win, (float*)temp, partials);
     TDGS_LAUNCHED();
