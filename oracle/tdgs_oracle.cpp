@@ -280,7 +280,7 @@ void oracle_backward_render_tiles(const tdgs_camera* cam, const tdgs_tiling* t,
                         const float alpha = fminf(opt->max_alpha, r[2] * G);
                         if (alpha < opt->min_alpha) continue;
                         float o[9];
-                        backward_pair(alpha, G, du, dv, r[3], r[4], r[5], r + 6, g, &T, psi, o);
+                        backward_pair(alpha, 1.0f / (1.0f - alpha), G, du, dv, r[3], r[4], r[5], r + 6, g, &T, psi, o);
                         for (int k = 0; k < 9; ++k) grads2d_acc[9 * f + k] += (double)o[k];
                     }
                 }

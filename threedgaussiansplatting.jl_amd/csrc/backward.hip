@@ -162,6 +162,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         }
         __syncthreads();
         const int jtop = (int)((int64_t)wave_last - lo < nb ? (int64_t)wave_last - lo : nb);
+        const int last_rel = (int)((int64_t)last - lo);   // entry jj of the batch is before last iff jj < last_rel
         // Entries back to front; the 9 contributions of up to kSlots consecutive contributing
         // entries are kept per lane and summed over the wavefront in one transpose-sum, after
         // which lane l holds component l % 9 of slot l / 9 and adds it to the tile's LDS sum.
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
                     const float4 ra = s_rec[jj].a, rb = s_rec[jj].b, rc = s_rec[jj].c;
                     float du, dv;
                     const float ex = backward_exponent(cu, cv, ra.x, ra.y, ra.w, rb.x, rb.y, &du, &dv);
-                    const bool live = on && lo + jj < (int64_t)last && !(ex < rc.y);
+                    const bool live = on && jj < last_rel && !(ex < rc.y);
                     if (!__any(live)) continue;
                     bool contrib = false;
                     const bool wide = __any(live && !(ex >= -87.0f && ex <= 88.0f));
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
                         const float alpha = aG < a.max_alpha ? aG : a.max_alpha;   // fminf, non-NaN max_alpha
                         if (!(alpha < a.min_alpha)) {
                             const float c[3] = {rb.z, rb.w, rc.x};
-                            backward_pair(alpha, G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
+                            backward_pair(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
                             contrib = true;
                         }
                     }

@@ -486,10 +486,11 @@ TDGS_HD float backward_gaussian(float cu, float cv, float mux, float muy, float 
 // (backward_core.jl:249-272). T is the transmittance after this Gaussian on entry and
 // before it on exit; psi (partial colour) is updated. out = [dmu_x, dmu_y, da, dM11,
 // dM21, dM22, dr, dg, db].
-TDGS_HD void backward_pair(float alpha, float G, float du, float dv, float m11, float m21,
+// inv1ma is 1 / (1 - alpha) (the CPU restatement divides; the GPU kernel uses the hardware
+// reciprocal, within 1 ulp).
+TDGS_HD void backward_pair(float alpha, float inv1ma, float G, float du, float dv, float m11, float m21,
                            float m22, const float c[3], const float g[3], float* T,
                            float psi[3], float out[9]) {
-    const float inv1ma = 1.0f / (1.0f - alpha);
     const float Tn = *T * inv1ma;
     *T = Tn;
     const float tc0 = Tn * c[0], tc1 = Tn * c[1], tc2 = Tn * c[2];
