@@ -48,6 +48,9 @@ def parse():
     p.add_argument("--train-steps", type=int, default=100)
     p.add_argument("--train-warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra-configs", action="store_true",
+                   help="skip the config 1 / 3 training and config 4 stress legs")
+    p.add_argument("--cfg3-iterations", type=int, default=3000)
     p.add_argument("--cpu-threads", type=int, default=0)
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 10 device-to-device copies of 1 GiB (HBM counter calibration)")
@@ -125,6 +128,114 @@ def train_bench(core, w, cams, tiling, deg, steps, warmup):
     assert tr.iteration_nb < to.adc_start_iteration_nb
     stage = {STAGES[i]: round(ms[i] / steps, 4) for i in range(13) if cnt[i] > 0}
     return steps / (t1 - t0), (t1 - t0) * 1000.0 / steps, stage, tr.current_loss()
+
+
+def train_cfg1(core, steps=100, warmup=5):
+    """Config 1: one training step (200k Gaussians, 800x800, SH3, L1 + 0.2 DSSIM against a seeded
+    uniform target) repeated `steps` times on its single camera."""
+    import torch
+    from tdgs_amd import host, synthetic, training
+    w = synthetic.config(1)
+    cam = w.cameras[0]
+    tiling = synthetic.tiling_for(w, cam)
+    g = core.TrainableGaussiansVector.from_host(w.gaussians, 0)
+    gen = torch.Generator(device="cuda").manual_seed(0x3D6501)
+    images = [torch.rand((cam.width, cam.height, 3), generator=gen, device="cuda")]
+    opts = host.RenderOptions.for_camera(cam, 3)
+    # one camera: scene_radius (spread of the camera centres, scene.jl:64-73) would be 0 and
+    # the annealed means learning rate log-linear in 0; use 1.1 x the camera's distance to the
+    # point it looks at (the origin) instead
+    radius = 1.1 * float(np.linalg.norm(cam.position))
+    to = training.TrainingOptions.for_scene(radius, sh_degree_increase_interval=10**9)
+    tr = training.Trainer(g, w.cameras, images, opts, tiling, to, seed=1)
+    for _ in range(warmup):
+        tr.training_step_()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tr.training_step_()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"workload": w.name, "train_it_per_s": round(steps / dt, 2), "ms_per_iteration": round(dt * 1e3 / steps, 4),
+            "steps": steps, "loss_last": round(float(tr.current_loss()), 6)}
+
+
+def train_cfg3(core, iterations):
+    """Config 3: the full training loop from 500k Gaussians (1297x840, SH3, 100 orbit cameras,
+    seeded uniform-noise targets) with the reference TrainingOptions defaults for
+    `iterations` iterations: density control every 100 iterations from 600, opacity reset at
+    3000. Wall time of all iterations, densification and pruning included."""
+    import torch
+    from tdgs_amd import host, synthetic, training
+    w = synthetic.config(3)
+    cams = w.cameras
+    tiling = synthetic.tiling_for(w, cams[0])
+    g = core.TrainableGaussiansVector.from_host(w.gaussians, 0)
+    gen = torch.Generator(device="cuda").manual_seed(0x3D6503)
+    images = [torch.rand((c.width, c.height, 3), generator=gen, device="cuda") for c in cams]
+    opts = host.RenderOptions.for_camera(cams[0], 3)
+    to = training.TrainingOptions.for_scene(host.scene_radius(cams), nb_iterations=iterations)
+    tr = training.Trainer(g, cams, images, opts, tiling, to, seed=3)
+    n0 = len(tr.gaussians)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    nmax = n0
+    for _ in range(iterations):
+        tr.training_step_()
+        nmax = max(nmax, len(tr.gaussians))
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"workload": w.name + f", {iterations} iterations with density control",
+            "train_it_per_s": round(iterations / dt, 2), "seconds": round(dt, 3), "iterations": iterations,
+            "gaussians_initial": n0, "gaussians_final": len(tr.gaussians), "gaussians_max": nmax,
+            "loss_last": round(float(tr.current_loss()), 6)}
+
+
+def stress_cfg4(core, repeats=5):
+    """Config 4: 3M Gaussians at 3840x2160 (SH3, 16x32 tiles), forward and backward of one
+    camera against a seeded uniform target; more than 100M duplicated keys."""
+    import torch
+    from tdgs_amd import host, synthetic, training
+    w = synthetic.config(4)
+    cam = w.cameras[0]
+    tiling = synthetic.tiling_for(w, cam)
+    g = core.TrainableGaussiansVector.from_host(w.gaussians, 0)
+    opts = host.RenderOptions.for_camera(cam, 3)
+    out = core.RenderOutputs.for_camera(cam, 0, include_rgb=True, include_transmittance=True, include_depth=False,
+                                        include_last_contributing_indices=True)
+    buf = core.RenderBuffers(len(g), tiling, 0)
+    fg = core.FilteredGaussiansGradientsVector(len(g), 3, 0)
+    gen = torch.Generator(device="cuda").manual_seed(0x3D6504)
+    gt = torch.rand((cam.width, cam.height, 3), generator=gen, device="cuda")
+    grad = torch.empty_like(out.rgb)
+    sums = torch.zeros(2, dtype=torch.float64, device="cuda")
+    temp = torch.empty(int(core.lib().tdgs_loss_temp_bytes(cam.width, cam.height)), dtype=torch.uint8, device="cuda")
+    core.render_(out, g, cam, tiling, opts, buf)
+    training.loss_grad_(out.rgb, gt, grad, 0.2, sums, temp)
+    core.backward_(fg, grad, out, g, cam, tiling, opts, buf)
+    torch.cuda.synchronize()
+    L = core.lib()
+    core.check(L.tdgs_profile_begin(C.c_int32(16 * repeats + 64)))
+    fw, bw = [], []
+    for _ in range(repeats):
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        e[0].record()
+        core.render_(out, g, cam, tiling, opts, buf)
+        e[1].record()
+        core.backward_(fg, grad, out, g, cam, tiling, opts, buf)
+        e[2].record()
+        torch.cuda.synchronize()
+        fw.append(e[0].elapsed_time(e[1]))
+        bw.append(e[1].elapsed_time(e[2]))
+    ms = (C.c_double * 13)()
+    cnt = (C.c_int64 * 13)()
+    core.check(L.tdgs_profile_end(ms, cnt))
+    stage = {STAGES[i]: round(ms[i] / cnt[i], 4) for i in range(13) if cnt[i] > 0}
+    m = buf.nb_keys
+    sort_gbs = 2 * 24 * m / (stage["tile_sort"] * 1e-3) / 1e9
+    return {"workload": w.name, "keys": m, "filtered": buf.nb_fgaussians, "forward_ms": round(float(np.median(fw)), 3),
+            "backward_ms": round(float(np.median(bw)), 3), "stage_ms": stage,
+            "tile_sort_algorithmic_GBs": round(sort_gbs, 1), "tile_sort_hbm_frac": round(sort_gbs / HBM_PEAK_GBS, 4)}
 
 
 def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles):
@@ -242,6 +353,15 @@ def main():
         train = {"train_it_per_s": round(its, 2), "ms_per_iteration": round(ms_it, 4), "steps": args.train_steps,
                  "stage_ms": tstage, "loss_last": round(float(loss), 6)}
 
+    extra = None
+    if not args.no_extra_configs:
+        torch.cuda.empty_cache()
+        extra = {"train_cfg1": train_cfg1(core)}
+        torch.cuda.empty_cache()
+        extra["train_cfg3"] = train_cfg3(core, args.cfg3_iterations)
+        torch.cuda.empty_cache()
+        extra["stress_cfg4"] = stress_cfg4(core)
+
     res = {
         "metric": "render fps + train it/s at 1M Gaussians 1080p SH3 (1 GPU); % HBM roofline",
         "value": round(fps, 2), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
@@ -258,6 +378,7 @@ def main():
         "stage_algorithmic_GBs": {k: round(v, 1) for k, v in stage_gbs.items()},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "extra_configs": extra,
     }
     print(json.dumps(res))
 

@@ -104,6 +104,21 @@ def test_render_synthetic_bit_exact(gpu, oracle, cfg, n, tile):
     _assert_forward_equal(r, out, buf)
 
 
+def test_render_large_footprints_bit_exact(gpu, oracle):
+    """Gaussians covering tens of tiles each (M > 32 N_f): tiles_end then comes from the tile
+    rectangles (difference array) instead of the sorted keys; it must be the same."""
+    w = synthetic.config(0, n=3000)
+    g = w.gaussians
+    g.scaling[...] = g.scaling + np.float32(2.0)   # log-scales ~ N(-1.5, 0.4)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.3, 0.2, 0.1))
+    r = oracle.render(g, cam, t, opts)
+    out, buf = _gpu_render(gpu, g, cam, t, opts)
+    assert r["nb_keys"] > 32 * r["nb_fgaussians"]
+    _assert_forward_equal(r, out, buf)
+
+
 def test_render_filter_mode_and_antialiasing(gpu, oracle):
     w = synthetic.config(0, n=5000)
     cam = w.cameras[0]

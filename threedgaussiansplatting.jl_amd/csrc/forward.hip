@@ -35,7 +35,10 @@ struct KeepEval {
     tdgs_camera cam;
     tdgs_render_options opt;
     uint8_t* keep;
+    int32_t* zero = nullptr;   // optional array zeroed on the side (first zero_n entries)
+    int64_t zero_n = 0;
     __device__ int32_t operator()(int64_t i) const {
+        if (i < zero_n) zero[i] = 0;
         const float4 m = reinterpret_cast<const float4*>(mo)[i];
         const bool k = keep_gaussian(cam, opt, m.x, m.y, m.z, opacity_of(kind, m.w));
         keep[i] = k ? 1 : 0;
@@ -51,6 +54,11 @@ struct CompactOut {
         if (item) fgidx_to_gidx[incl - 1] = (int32_t)(i + 1);
     }
 };
+
+__global__ void k_fill_i32(int32_t* p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
 
 __global__ void k_fill_keep(KeepEval ev, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -77,6 +85,30 @@ struct ProjectArgs {
     uint32_t* depth_keys;     // optional: depth bits (0xffffffff when empty or unused)
     int32_t* depth_vals;      // optional: fgidx (1-based), 0 for unused slots
 };
+
+// Tile ranges from tile rectangles (used when Gaussians cover many tiles, where reading the
+// M sorted keys costs more than 4 atomics per Gaussian): each non-empty Gaussian adds its
+// rectangle to a 2D difference array, +1 at (x0, y0), -1 at (x1+1, y0) and (x0, y1+1), +1 at
+// (x1+1, y1+1) (0-based corners). Workgroup b adds into copy b % kRectCopies, which spreads
+// the atomics on popular corners (and, with round-robin dispatch over the 8 XCDs, keeps each
+// copy on one XCD); k_merge_rect_diff sums the copies.
+constexpr int kRectCopies = 32;
+constexpr int64_t kRectKeysPerGaussian = 32;   // use rectangles when M > this x N_f
+
+__global__ __launch_bounds__(256) void k_rect_diff(int64_t nbf, const int32_t* __restrict__ counts,
+                                                   const int32_t* __restrict__ ranges, int ntx,
+                                                   int32_t* __restrict__ diff, int64_t ndiff) {
+    const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (f >= nbf || counts[f] == 0) return;
+    const int4 r = reinterpret_cast<const int4*>(ranges)[f];
+    const int64_t w = ntx + 1;
+    const int x0 = r.x - 1, y0 = r.y - 1, x1 = r.z, y1 = r.w;
+    int32_t* d = diff + (int64_t)(blockIdx.x % kRectCopies) * ndiff;
+    atomicAdd(d + y0 * w + x0, 1);
+    atomicAdd(d + y0 * w + x1, -1);
+    atomicAdd(d + y1 * w + x0, -1);
+    atomicAdd(d + y1 * w + x1, 1);
+}
 
 // One thread per filtered Gaussian. The SH blocks of the workgroup's non-empty Gaussians are
 // staged in LDS (odd row stride) by cooperative loads (float4 for 16-coefficient storage,
@@ -113,6 +145,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
         }
         pr = project_geometry(a.cam, a.opt, a.tiling, a.g.kind, m.x, m.y, m.z, op, params);
         a.counts[f] = pr.count;
+
     }
     s_gi[t] = pr.count > 0 ? (int32_t)gi : -1;
     const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
@@ -320,6 +353,86 @@ __global__ __launch_bounds__(256) void k_tile_ranges(int64_t m, const int64_t* _
     }
 }
 
+// tiles_end from the tile-coverage difference array D ((ntx+1) x (nty+1), 0-based corners).
+// With col_y(x) = sum_{y' <= y} D[y'][x], the keys of tile (x, y) number
+// count(x, y) = sum_{x' <= x} col_y(x'), tiles_end(x, y) = sum_{x' <= x} count(x', y) plus the
+// keys of all rows above, sum_{y' < y, x' < ntx} (y - y') (ntx - x') D[y'][x']. Workgroup y
+// reads rows 0..y (L2-resident) and scans its row twice, so tiles_end needs no pass over the M
+// sorted keys and equals fill_tiles_end_sdfgidx_kernel!'s (forward_core.jl:676-734) exactly.
+constexpr int kTeThreads = 256;
+
+// copy 0 <- sum of the kRectCopies copies
+__global__ __launch_bounds__(256) void k_merge_rect_diff(int32_t* __restrict__ diff, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int32_t s = diff[i];
+#pragma unroll 8
+    for (int k = 1; k < kRectCopies; ++k) s += diff[(int64_t)k * n + i];
+    diff[i] = s;
+}
+
+// Inclusive block scan of one int64 per thread (kTeThreads threads); *total gets the sum.
+__device__ __forceinline__ int64_t te_block_scan(int64_t v, int64_t* s_red, int64_t* total) {
+    const int lane = __lane_id(), wave = threadIdx.x / kWave;
+    int64_t incl = v;
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int64_t o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) s_red[wave] = incl;
+    __syncthreads();
+    int64_t off = 0, tot = 0;
+    for (int k = 0; k < kTeThreads / kWave; ++k) {
+        if (k < wave) off += s_red[k];
+        tot += s_red[k];
+    }
+    __syncthreads();
+    *total = tot;
+    return off + incl;
+}
+
+__global__ __launch_bounds__(kTeThreads) void k_tiles_end_from_rects(const int32_t* __restrict__ diff, int ntx,
+                                                                    int32_t* __restrict__ te) {
+    __shared__ int64_t s_red[kTeThreads / kWave];
+    const int y = blockIdx.x, t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+    const int w = ntx + 1;
+    int64_t above = 0;   // this thread's share of the keys in rows < y
+    int64_t carry_col = 0, carry_cnt = 0;
+    for (int x0 = 0; x0 < ntx; x0 += kTeThreads) {
+        const int x = x0 + t;
+        int64_t col = 0;
+        if (x < ntx) {
+            const int64_t wx = ntx - x;
+            int yy = 0;
+            for (; yy + 4 <= y; yy += 4) {
+                const int32_t d0 = diff[(int64_t)yy * w + x], d1 = diff[(int64_t)(yy + 1) * w + x];
+                const int32_t d2 = diff[(int64_t)(yy + 2) * w + x], d3 = diff[(int64_t)(yy + 3) * w + x];
+                col += (int64_t)d0 + d1 + d2 + d3;
+                above += wx * ((int64_t)(y - yy) * d0 + (int64_t)(y - yy - 1) * d1 + (int64_t)(y - yy - 2) * d2 +
+                               (int64_t)(y - yy - 3) * d3);
+            }
+            for (; yy < y; ++yy) {
+                const int32_t d = diff[(int64_t)yy * w + x];
+                col += d;
+                above += wx * (int64_t)(y - yy) * d;
+            }
+            col += diff[(int64_t)y * w + x];
+        }
+        int64_t tot;
+        const int64_t count = te_block_scan(col, s_red, &tot) + carry_col;   // keys of tile (x, y)
+        carry_col += tot;
+        const int64_t incl = te_block_scan(x < ntx ? count : 0, s_red, &tot) + carry_cnt;
+        carry_cnt += tot;
+        if (x < ntx) te[(int64_t)y * ntx + x] = (int32_t)incl;   // rows above added below
+    }
+    for (int d = 32; d >= 1; d >>= 1) above += __shfl_xor(above, d, kWave);
+    if (lane == 0) s_red[wave] = above;
+    __syncthreads();
+    int64_t rows_above = 0;
+    for (int k = 0; k < kTeThreads / kWave; ++k) rows_above += s_red[k];
+    for (int x = t; x < ntx; x += kTeThreads) te[(int64_t)y * ntx + x] += (int32_t)rows_above;
+}
+
 // ------------------------------------------------------------------------------------
 // Blending (render_tiles_kernel!, forward_core.jl:756-993)
 // ------------------------------------------------------------------------------------
@@ -506,8 +619,12 @@ static int end_bit_of(const tdgs_tiling* t) {
 }
 
 // Scratch layout of tdgs_render.
+static int64_t rect_diff_size(const tdgs_tiling* t) {
+    return t ? (int64_t)(t->nb_tiles_x + 1) * (t->nb_tiles_y + 1) : 0;
+}
+
 template <class A>
-static void render_layout(A& ar, int64_t cap, int64_t key_cap) {
+static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling* t) {
     ar.template take<int64_t>(kCounters);                 // unused slot (alignment)
     ar.template take<uint8_t>(cap);                       // keep flags when buf->keep is null
     ar.template take<uint32_t>(cap);                      // depth keys
@@ -520,6 +637,7 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap) {
     ar.template take<char>((int64_t)scan_temp_bytes_for(cap));
     const int64_t big = cap > key_cap ? cap : key_cap;
     ar.template take<char>((int64_t)radix_temp_bytes(big));
+    ar.template take<int32_t>(kRectCopies * rect_diff_size(t));   // tile-coverage difference arrays
 }
 
 }  // namespace tdgs
@@ -649,7 +767,7 @@ int tdgs_blend_evaluations(void* stream, const tdgs_camera* cam, const tdgs_tili
 size_t tdgs_render_temp_bytes(int32_t capacity, int64_t key_capacity, const tdgs_tiling* tiling) {
     (void)tiling;
     ArenaSize sz;
-    render_layout(sz, capacity, key_capacity);
+    render_layout(sz, capacity, key_capacity, tiling);
     return sz.used + 256;
 }
 
@@ -691,6 +809,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     const int64_t big = cap > buf->key_capacity ? cap : buf->key_capacity;
     const size_t rbytes = radix_temp_bytes(big);
     void* rtemp = ar.take<char>((int64_t)rbytes);
+    const int64_t ndiff = rect_diff_size(tiling);
+    int32_t* rect_diff = ar.take<int32_t>(kRectCopies * ndiff);
     uint8_t* keep = buf->keep ? buf->keep : keep_tmp;
     int64_t* d_nbf = ctx->d_counters;
     int64_t* d_m = ctx->d_counters + 1;
@@ -699,6 +819,13 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     {
         StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
         KeepEval ev{g->means_opacity, g->kind, *cam, *opt, keep};
+        if (n >= kRectCopies * ndiff) {
+            ev.zero = rect_diff;   // zeroed on the side of the keep pass
+            ev.zero_n = kRectCopies * ndiff;
+        } else {
+            k_fill_i32<<<(unsigned)ceil_div(kRectCopies * ndiff, 256), 256, 0, s>>>(rect_diff, kRectCopies * ndiff, 0);
+            TDGS_LAUNCHED();
+        }
         TDGS_TRY(device_scan(ev, ItemsU8{keep}, CompactOut{buf->fgidx_to_gidx, nullptr}, n, stemp, sbytes,
                              d_nbf, s));
     }
@@ -709,6 +836,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
     pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
     pa.depth_keys = dkey; pa.depth_vals = dval;
+
     {
         StageScope sc(TDGS_STAGE_PROJECT, s);
         k_project<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(pa);
@@ -766,7 +894,17 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
     {
         StageScope sc(TDGS_STAGE_TILE_RANGES, s);
-        k_tile_ranges<<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles, buf->tiles_end);
+        if (m > kRectKeysPerGaussian * nbf) {
+            k_rect_diff<<<(unsigned)ceil_div(nbf, 256), 256, 0, s>>>(nbf, buf->counts, buf->tile_ranges,
+                                                                    tiling->nb_tiles_x, rect_diff, ndiff);
+            TDGS_LAUNCHED();
+            k_merge_rect_diff<<<(unsigned)ceil_div(ndiff, 256), 256, 0, s>>>(rect_diff, ndiff);
+            TDGS_LAUNCHED();
+            k_tiles_end_from_rects<<<(unsigned)tiling->nb_tiles_y, kTeThreads, 0, s>>>(
+                rect_diff, tiling->nb_tiles_x, buf->tiles_end);
+        } else {
+            k_tile_ranges<<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles, buf->tiles_end);
+        }
         TDGS_LAUNCHED();
     }
     // 9: blending
