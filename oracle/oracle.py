@@ -59,14 +59,20 @@ def ptr(a):
 def gaussians_struct(g):
     abi = _abi()
     s = abi.Gaussians()
-    s.kind = abi.TDGS_TRAINABLE
     s.n = g.n
     s.sh_degree = g.sh_degree
     s.means_opacity = g.means_opacity.ctypes.data
-    s.scaling = g.scaling.ctypes.data
-    s.rotation = g.rotation.ctypes.data
-    s.covariances = None
     s.sh = g.sh.ctypes.data
+    if hasattr(g, "covariances"):  # render-only: activated opacities, 3D covariances
+        s.kind = abi.TDGS_RENDER_ONLY
+        s.scaling = None
+        s.rotation = None
+        s.covariances = g.covariances.ctypes.data
+    else:
+        s.kind = abi.TDGS_TRAINABLE
+        s.scaling = g.scaling.ctypes.data
+        s.rotation = g.rotation.ctypes.data
+        s.covariances = None
     return s
 
 

@@ -19,7 +19,7 @@ import numpy as np
 import torch
 
 from . import abi
-from .host import HostGaussians, PinholeCamera, RenderOptions, Tiling
+from .host import HostGaussians, HostRenderOnlyGaussians, PinholeCamera, RenderOptions, Tiling
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libtdgs.so")
@@ -158,6 +158,12 @@ class RenderOnlyGaussiansVector:
         self.means_opacity = means_opacities.contiguous()
         self.covariances = covariances.contiguous()
         self.sh = sh.contiguous()
+
+    @classmethod
+    def from_host(cls, g: HostRenderOnlyGaussians, device=0):
+        d = _dev(device)
+        return cls(*(torch.from_numpy(np.ascontiguousarray(a)).to(d)
+                     for a in (g.means_opacity, g.covariances, g.sh)))
 
     def __len__(self):
         return self.means_opacity.shape[0]

@@ -251,6 +251,24 @@ class HostGaussians:
         return int(round(math.sqrt(self.sh.shape[2]))) - 1
 
 
+@dataclass
+class HostRenderOnlyGaussians:
+    """RenderOnlyGaussiansVector contents (src/gaussians.jl:342-392) as host arrays: means with
+    activated opacities (n, 4), covariance lower halves [V11, V21, V31, V22, V32, V33] (n, 6),
+    sh (n, 3, h)."""
+    means_opacity: np.ndarray
+    covariances: np.ndarray
+    sh: np.ndarray
+
+    @property
+    def n(self):
+        return self.means_opacity.shape[0]
+
+    @property
+    def sh_degree(self):
+        return int(round(math.sqrt(self.sh.shape[2]))) - 1
+
+
 def create_test_scene(sh_degree=0, two_cameras=False):
     """create_test_scene (src/scene.jl:123-188): four Gaussians (red, white behind the camera,
     green, purple) and a 320 x 240 camera with a 90 degree horizontal field of view."""
