@@ -16,6 +16,7 @@ from __future__ import annotations
 import argparse
 import ctypes as C
 import json
+import math
 import os
 import sys
 import time
@@ -259,6 +260,36 @@ def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles):
     return None
 
 
+def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit):
+    """Per-kernel HBM fractions under the accounting convention of the metric: K1 = cull,
+    compaction and projection (16 N + (28 + 12h) N_f read, 8 N_f + 56 N_b written); K2 = count
+    scan and key emission (8 N_f + 24 N_b + 12 M); K3 = the sort, priced as a full-width
+    8-bit-digit LSD sort of the 64-bit keys (8 M + 24 M ceil(end_bit / 8)) whatever digit
+    width and pass count the build uses, over the depth and tile sort times; K4 = tile ranges
+    (8 M + 4 T); K5 = blend bytes (40 M + 20 P); K7 = backward projection ((160 + 24h) N_f);
+    K8 = Adam (28 (11 + 3h) N_f + 4 N_f). K7 and K8 use the render leg's counts (same
+    Gaussians and cameras, before any densification)."""
+    rows = {
+        "K1_project": (16 * n + (28 + 12 * h) * nf + 8 * nf + 56 * nb, ["cull_compact", "project"], stage_ms),
+        "K2_scan_keys": (8 * nf + 24 * nb + 12 * m, ["count_scan", "emit"], stage_ms),
+        "K3_sort": (8 * m + 24 * m * math.ceil(end_bit / 8), ["depth_sort", "tile_sort"], stage_ms),
+        "K4_ranges": (8 * m + 4 * ntiles, ["tile_ranges"], stage_ms),
+        "K5_blend": (40 * m + 20 * npx, ["blend"], stage_ms),
+    }
+    if train_stage:
+        rows["K7_backward_project"] = ((160 + 24 * h) * nf, ["backward_project"], train_stage)
+        rows["K8_adam"] = (28 * (11 + 3 * h) * nf + 4 * nf, ["adam"], train_stage)
+    out = {}
+    for k, (b, stages, src) in rows.items():
+        if not all(s_ in src for s_ in stages):
+            continue
+        t = sum(src[s_] for s_ in stages)
+        gbs = b / (t * 1e-3) / 1e9
+        out[k] = {"stages": stages, "ms": round(t, 4), "bytes": int(b), "GBs": round(gbs, 1),
+                  "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def main():
     args = parse()
     if args.copy_calibration:
@@ -377,6 +408,8 @@ def main():
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
         "stage_algorithmic_GBs": {k: round(v, 1) for k, v in stage_gbs.items()},
         "roofline": roofline,
+        "survey_kernels": survey_kernels(stage_ms, train["stage_ms"] if train else None, n, nf, nb, m, npx, h,
+                                         tiling.nb_tiles, tiling.end_bit()),
         "cpu_baseline": cpu,
         "extra_configs": extra,
     }

@@ -4,10 +4,11 @@
 // Reference: src/forward_core.jl:196-993, src/forward_structs.jl:743-757.
 //
 // Pipeline of tdgs_render (one host synchronisation, to learn N_f and M):
-//   1. keep flags + per-tile sums                 scan pass 1 (KeepEval)
-//   2. fgidx_to_gidx compaction                   scan pass 3 (CompactOut)
-//   3. projection of the N_f kept Gaussians       k_project (grid over capacity; N_f read on
-//                                                 the device), also writes a 32-bit depth key
+//   1. keep flags + kept count per 256 Gaussians  k_keep_counts
+//   2. exclusive scan of the block counts -> N_f  k_scan_tiles
+//   3. compaction + projection, gidx order        k_project (each kept Gaussian's fgidx from
+//                                                 its block offset and rank), also writes a
+//                                                 32-bit depth key
 //   4. stable sort of (depth bits, fgidx)         radix, bits [0, 32)
 //   5. scan of tile counts in depth order -> M    scan (SortedCounts)
 //   6. key emission in depth order                k_emit_depth_order
@@ -34,14 +35,14 @@ struct KeepEval {
     int kind;
     tdgs_camera cam;
     tdgs_render_options opt;
-    uint8_t* keep;
+    uint8_t* keep;             // optional keep flags
     int32_t* zero = nullptr;   // optional array zeroed on the side (first zero_n entries)
     int64_t zero_n = 0;
     __device__ int32_t operator()(int64_t i) const {
         if (i < zero_n) zero[i] = 0;
         const float4 m = reinterpret_cast<const float4*>(mo)[i];
         const bool k = keep_gaussian(cam, opt, m.x, m.y, m.z, opacity_of(kind, m.w));
-        keep[i] = k ? 1 : 0;
+        if (keep) keep[i] = k ? 1 : 0;
         return k ? 1 : 0;
     }
 };
@@ -74,16 +75,15 @@ struct ProjectArgs {
     tdgs_camera cam;
     tdgs_tiling tiling;
     tdgs_render_options opt;
-    int64_t cap;
-    const int64_t* d_nbf;     // device count of filtered Gaussians (or null: use nbf)
-    int64_t nbf;
-    const int32_t* fgidx_to_gidx;
+    const int64_t* block_offsets;   // kept Gaussians before each 256-Gaussian block (exclusive)
+    const int64_t* d_nbf;           // device count of filtered Gaussians
+    int32_t* fgidx_to_gidx;         // written: the order-preserving compaction
     float* depths;
     float* f2d;
     int32_t* ranges;
     int32_t* counts;
-    uint32_t* depth_keys;     // optional: depth bits (0xffffffff when empty or unused)
-    int32_t* depth_vals;      // optional: fgidx (1-based), 0 for unused slots
+    uint32_t* depth_keys;     // depth bits by fgidx (0xffffffff when empty); culled: slots past N_f
+    int32_t* depth_vals;      // fgidx (1-based); 0 for the slots past N_f
 };
 
 // Tile ranges from tile rectangles (used when Gaussians cover many tiles, where reading the
@@ -110,29 +110,57 @@ __global__ __launch_bounds__(256) void k_rect_diff(int64_t nbf, const int32_t* _
     atomicAdd(d + y1 * w + x1, 1);
 }
 
-// One thread per filtered Gaussian. The SH blocks of the workgroup's non-empty Gaussians are
-// staged in LDS (odd row stride) by cooperative loads (float4 for 16-coefficient storage,
-// all in flight at once) before the colours are evaluated.
+// Keep counts per 256-Gaussian block (fill_keep_gaussians_kernel! and the count half of the
+// compaction scan, forward_core.jl:231-244, 326-355): workgroup b evaluates the keep test of
+// Gaussians [2048 b, 2048 b + 2048) with coalesced loads and writes the 8 block counts.
+// (A single pass with a decoupled look-back over per-workgroup counts measured slower: the
+// cross-workgroup status round trips cost more than this pass and the scan of its counts.)
+constexpr int kKeepSub = 8;
+__global__ __launch_bounds__(256) void k_keep_counts(KeepEval ev, int64_t n, int64_t* __restrict__ block_counts,
+                                                     int64_t nblocks) {
+    __shared__ int32_t s_cnt[kKeepSub][256 / kWave];
+    const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+    bool kp[kKeepSub];
+#pragma unroll
+    for (int k = 0; k < kKeepSub; ++k) {
+        const int64_t i = ((int64_t)blockIdx.x * kKeepSub + k) * 256 + t;
+        kp[k] = i < n && ev(i) != 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kKeepSub; ++k) {
+        const uint64_t bal = __ballot(kp[k]);
+        if (lane == 0) s_cnt[k][wave] = __popcll(bal);
+    }
+    __syncthreads();
+    if (t < kKeepSub) {
+        const int64_t sb = (int64_t)blockIdx.x * kKeepSub + t;
+        int32_t c = 0;
+        for (int w = 0; w < 256 / kWave; ++w) c += s_cnt[t][w];
+        if (sb < nblocks) block_counts[sb] = c;
+    }
+}
+
+// Compaction + projection (fill_fgidx_to_gidx_kernel! and project_fgaussians_kernel!,
+// forward_core.jl:371-386, 411-517), one thread per Gaussian in gidx order: the keep test is
+// repeated, and a kept Gaussian's fgidx is its block's offset plus its rank among the block's
+// kept Gaussians (wave ballots), so parameter reads are coalesced and the compaction costs no
+// pass of its own. All parameter loads issue at once; a non-empty Gaussian's 48 SH
+// coefficients (12 float4 for 16-coefficient storage) are loaded by its own thread and its
+// colour evaluated before the workgroup barrier that resolves the ranks. (Staging the SH
+// blocks through LDS for coalescing measured slower once the loads overlap like this.)
 constexpr int kProjThreads = 256;
-constexpr int kProjShRow = 49;
-constexpr int kProjUnroll = 16;
 
 __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
-    __shared__ float s_sh[kProjThreads * kProjShRow];
-    __shared__ int32_t s_gi[kProjThreads];   // gidx (0-based) of non-empty Gaussians, else -1
-    const int t = threadIdx.x;
-    const int64_t f = (int64_t)blockIdx.x * kProjThreads + t;
-    const int64_t nbf = a.d_nbf ? *a.d_nbf : a.nbf;
-    const bool valid = f < a.cap && f < nbf;
-    Projected pr;
-    pr.count = 0;
-    int64_t gi = -1;
+    __shared__ int32_t s_wave[kProjThreads / kWave];
+    __shared__ float s_rec[kProjThreads * 9];   // the block's f2d records, by rank
+    const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+    const int64_t gi = (int64_t)blockIdx.x * kProjThreads + t;
+    const int64_t n = a.g.n;
+    // all parameter loads issue together (the culled few percent are read for nothing)
     float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (valid) {
-        gi = (int64_t)a.fgidx_to_gidx[f] - 1;
+    float params[7];
+    if (gi < n) {
         m = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
-        const float op = opacity_of(a.g.kind, m.w);
-        float params[7];
         if (a.g.kind == TDGS_TRAINABLE) {
             params[0] = a.g.scaling[3 * gi];
             params[1] = a.g.scaling[3 * gi + 1];
@@ -143,71 +171,75 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
 #pragma unroll
             for (int k = 0; k < 6; ++k) params[k] = a.g.covariances[6 * gi + k];
         }
-        pr = project_geometry(a.cam, a.opt, a.tiling, a.g.kind, m.x, m.y, m.z, op, params);
-        a.counts[f] = pr.count;
-
     }
-    s_gi[t] = pr.count > 0 ? (int32_t)gi : -1;
-    const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
-    __syncthreads();
-    if (hs == 16) {
-        float4 val[12];
-#pragma unroll
-        for (int r = 0; r < 12; ++r) {
-            const int i = t + kProjThreads * r, j = i / 12, q = i - 12 * j;
-            const int32_t gj = s_gi[j];
-            if (gj >= 0) val[r] = reinterpret_cast<const float4*>(a.g.sh)[(int64_t)12 * gj + q];
-        }
-#pragma unroll
-        for (int r = 0; r < 12; ++r) {
-            const int i = t + kProjThreads * r, j = i / 12, q = i - 12 * j;
-            if (s_gi[j] >= 0) {
-                float* d = s_sh + j * kProjShRow + 4 * q;
-                d[0] = val[r].x; d[1] = val[r].y; d[2] = val[r].z; d[3] = val[r].w;
-            }
-        }
-    } else {
-        const int w = 3 * hs, dj = kProjThreads / w, de = kProjThreads - dj * w;
-        int j = t / w, e = t - j * w;
-        for (int r0 = 0; r0 < w; r0 += kProjUnroll) {
-            float val[kProjUnroll];
-            int dst[kProjUnroll];
-#pragma unroll
-            for (int u = 0; u < kProjUnroll; ++u) {
-                dst[u] = -1;
-                if (r0 + u < w) {
-                    const int32_t gj = s_gi[j];
-                    if (gj >= 0) {
-                        val[u] = a.g.sh[(int64_t)w * gj + e];
-                        dst[u] = j * kProjShRow + e;
-                    }
-                    j += dj;
-                    e += de;
-                    if (e >= w) { e -= w; ++j; }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < kProjUnroll; ++u)
-                if (dst[u] >= 0) s_sh[dst[u]] = val[u];
-        }
-    }
-    __syncthreads();
-    uint32_t dk = 0xffffffffu;
+    const float op = opacity_of(a.g.kind, m.w);
+    const bool keep = gi < n && keep_gaussian(a.cam, a.opt, m.x, m.y, m.z, op);
+    const uint64_t bal = __ballot(keep);
+    if (lane == 0) s_wave[wave] = __popcll(bal);
+    Projected pr;
+    pr.count = 0;
+    if (keep) pr = project_geometry(a.cam, a.opt, a.tiling, a.g.kind, m.x, m.y, m.z, op, params);
+    float rgb[3];
     if (pr.count > 0) {
-        float rgb[3];
-        project_color(a.cam, a.opt.sh_degree, s_sh + t * kProjShRow, hs, m.x, m.y, m.z, rgb);
-        a.depths[f] = pr.depth;
-        reinterpret_cast<int4*>(a.ranges)[f] = make_int4(pr.rect[0], pr.rect[1], pr.rect[2], pr.rect[3]);
-        float* r = a.f2d + 9 * f;
-        r[0] = pr.mux; r[1] = pr.muy; r[2] = pr.a;
-        r[3] = pr.m11; r[4] = pr.m21; r[5] = pr.m22;
-        r[6] = rgb[0]; r[7] = rgb[1]; r[8] = rgb[2];
-        dk = float_bits(pr.depth);
+        const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
+        float bs[16];
+        if (hs == 16) {
+            const float4* p = reinterpret_cast<const float4*>(a.g.sh) + (int64_t)12 * gi;
+            float cc[48];
+#pragma unroll
+            for (int r = 0; r < 12; ++r) {
+                const float4 v = p[r];
+                cc[4 * r] = v.x; cc[4 * r + 1] = v.y; cc[4 * r + 2] = v.z; cc[4 * r + 3] = v.w;
+            }
+            view_sh_basis(a.cam, a.opt.sh_degree, m.x, m.y, m.z, bs);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) rgb[c] = sh_channel_to_color(a.opt.sh_degree, cc + 16 * c, bs);
+        } else {
+            view_sh_basis(a.cam, a.opt.sh_degree, m.x, m.y, m.z, bs);
+            sh_to_color(a.opt.sh_degree, a.g.sh + 3 * (int64_t)hs * gi, hs, bs, rgb);
+        }
     }
-    if (a.depth_keys && f < a.cap) {
-        a.depth_keys[f] = dk;
-        a.depth_vals[f] = valid ? (int32_t)(f + 1) : 0;
+    __syncthreads();
+    int before = 0, kept = 0;
+#pragma unroll
+    for (int w = 0; w < kProjThreads / kWave; ++w) {
+        if (w < wave) before += s_wave[w];
+        kept += s_wave[w];
     }
+    const int local = before + __popcll(bal & lanemask_lt());
+    const int64_t off = a.block_offsets[blockIdx.x];
+    const int64_t f = off + local;   // 0-based fgidx if kept
+    if (keep) {
+        a.fgidx_to_gidx[f] = (int32_t)(gi + 1);
+        a.counts[f] = pr.count;
+        uint32_t dk = 0xffffffffu;
+        float* r = s_rec + 9 * local;   // empty Gaussians get a zero record
+        if (pr.count > 0) {
+            a.depths[f] = pr.depth;
+            reinterpret_cast<int4*>(a.ranges)[f] = make_int4(pr.rect[0], pr.rect[1], pr.rect[2], pr.rect[3]);
+            r[0] = pr.mux; r[1] = pr.muy; r[2] = pr.a;
+            r[3] = pr.m11; r[4] = pr.m21; r[5] = pr.m22;
+            r[6] = rgb[0]; r[7] = rgb[1]; r[8] = rgb[2];
+            dk = float_bits(pr.depth);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 9; ++k) r[k] = 0.0f;
+        }
+        if (a.depth_keys) {
+            a.depth_keys[f] = dk;
+            a.depth_vals[f] = (int32_t)(f + 1);
+        }
+    } else if (gi < n && a.depth_keys) {
+        const int64_t slot = *a.d_nbf + (gi - f);   // culled Gaussians fill the slots past N_f
+        a.depth_keys[slot] = 0xffffffffu;
+        a.depth_vals[slot] = 0;
+    }
+    // the block's records are one contiguous run of f2d: write it with consecutive lanes on
+    // consecutive floats (36-byte strided stores from each thread split into many partial
+    // requests)
+    __syncthreads();
+    float* dst = a.f2d + 9 * off;
+    for (int e = t; e < 9 * kept; e += kProjThreads) dst[e] = s_rec[e];
 }
 
 // ------------------------------------------------------------------------------------
@@ -626,7 +658,6 @@ static int64_t rect_diff_size(const tdgs_tiling* t) {
 template <class A>
 static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling* t) {
     ar.template take<int64_t>(kCounters);                 // unused slot (alignment)
-    ar.template take<uint8_t>(cap);                       // keep flags when buf->keep is null
     ar.template take<uint32_t>(cap);                      // depth keys
     ar.template take<uint32_t>(cap);                      // depth keys, ping-pong
     ar.template take<uint32_t>(cap);                      // depth keys, sorted
@@ -635,6 +666,7 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(cap);                       // depth values, sorted (fgidx)
     ar.template take<int32_t>(cap);                       // counts scan in depth order
     ar.template take<char>((int64_t)scan_temp_bytes_for(cap));
+    ar.template take<int64_t>(ceil_div(cap, kProjThreads));    // keep counts per projection block
     const int64_t big = cap > key_cap ? cap : key_cap;
     ar.template take<char>((int64_t)radix_temp_bytes(big));
     ar.template take<int32_t>(kRectCopies * rect_diff_size(t));   // tile-coverage difference arrays
@@ -796,7 +828,6 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     const int64_t cap = buf->capacity;
     Arena ar(buf->temp, buf->temp_bytes);
     ar.take<int64_t>(kCounters);
-    uint8_t* keep_tmp = ar.take<uint8_t>(cap);
     uint32_t* dkey = ar.take<uint32_t>(cap);
     uint32_t* dkey_alt = ar.take<uint32_t>(cap);
     uint32_t* dkey_sorted = ar.take<uint32_t>(cap);
@@ -806,19 +837,21 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     int32_t* cs = ar.take<int32_t>(cap);
     const size_t sbytes = scan_temp_bytes_for(cap);
     void* stemp = ar.take<char>((int64_t)sbytes);
+    int64_t* block_offsets = ar.take<int64_t>(ceil_div(cap, kProjThreads));
     const int64_t big = cap > buf->key_capacity ? cap : buf->key_capacity;
     const size_t rbytes = radix_temp_bytes(big);
     void* rtemp = ar.take<char>((int64_t)rbytes);
     const int64_t ndiff = rect_diff_size(tiling);
     int32_t* rect_diff = ar.take<int32_t>(kRectCopies * ndiff);
-    uint8_t* keep = buf->keep ? buf->keep : keep_tmp;
     int64_t* d_nbf = ctx->d_counters;
     int64_t* d_m = ctx->d_counters + 1;
 
-    // 1-2: keep flags and compaction
+
+    // 1-2: keep flags, keep counts per projection block, their scan (N_f)
+    const int64_t nblocks = ceil_div(n, kProjThreads);
     {
         StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
-        KeepEval ev{g->means_opacity, g->kind, *cam, *opt, keep};
+        KeepEval ev{g->means_opacity, g->kind, *cam, *opt, buf->keep};
         if (n >= kRectCopies * ndiff) {
             ev.zero = rect_diff;   // zeroed on the side of the keep pass
             ev.zero_n = kRectCopies * ndiff;
@@ -826,20 +859,21 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
             k_fill_i32<<<(unsigned)ceil_div(kRectCopies * ndiff, 256), 256, 0, s>>>(rect_diff, kRectCopies * ndiff, 0);
             TDGS_LAUNCHED();
         }
-        TDGS_TRY(device_scan(ev, ItemsU8{keep}, CompactOut{buf->fgidx_to_gidx, nullptr}, n, stemp, sbytes,
-                             d_nbf, s));
+        k_keep_counts<<<(unsigned)ceil_div(nblocks, kKeepSub), 256, 0, s>>>(ev, n, block_offsets, nblocks);
+        TDGS_LAUNCHED();
+        k_scan_tiles<<<1, kScanThreads, 0, s>>>(block_offsets, nblocks, d_nbf);
+        TDGS_LAUNCHED();
     }
-    // 3: projection
+    // 3: compaction + projection
     ProjectArgs pa;
     pa.g = *g; pa.cam = *cam; pa.tiling = *tiling; pa.opt = *opt;
-    pa.cap = n; pa.d_nbf = d_nbf; pa.nbf = 0;
+    pa.block_offsets = block_offsets; pa.d_nbf = d_nbf;
     pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
     pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
     pa.depth_keys = dkey; pa.depth_vals = dval;
-
     {
         StageScope sc(TDGS_STAGE_PROJECT, s);
-        k_project<<<(unsigned)ceil_div(n, 256), 256, 0, s>>>(pa);
+        k_project<<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
         TDGS_LAUNCHED();
     }
     // 4: Gaussians by (depth bits, fgidx)

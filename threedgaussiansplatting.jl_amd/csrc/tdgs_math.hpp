@@ -296,29 +296,31 @@ TDGS_HD void sh_basis(int degree, float x, float y, float z, float b[16]) {
 }
 
 // sh_coeffs_to_color (src/sh.jl:38-112): per channel sum_k b_k c_k + 0.5, clamped below
-// at 0. coeffs points at one Gaussian's (h_storage, 3) block; only the first
-// (degree+1)^2 coefficients of each channel are used.
-TDGS_HD void sh_to_color(int degree, const float* coeffs, int h_storage, const float b[16],
-                         float rgb[3]) {
-    for (int c = 0; c < 3; ++c) {
-        const float* cc = coeffs + c * h_storage;
-        float v = b[0] * cc[0];
-        if (degree >= 1) {
-            v += fmaf(b[3], cc[3], fmaf(b[2], cc[2], b[1] * cc[1]));
-            if (degree >= 2) {
-                float t = b[4] * cc[4];
-                for (int k = 5; k < 9; ++k) t = fmaf(b[k], cc[k], t);
-                v += t;
-                if (degree >= 3) {
-                    float u = b[9] * cc[9];
-                    for (int k = 10; k < 16; ++k) u = fmaf(b[k], cc[k], u);
-                    v += u;
-                }
+// at 0; only the first (degree+1)^2 coefficients of each channel are used. This is one
+// channel, cc pointing at its coefficients.
+TDGS_HD float sh_channel_to_color(int degree, const float* cc, const float b[16]) {
+    float v = b[0] * cc[0];
+    if (degree >= 1) {
+        v += fmaf(b[3], cc[3], fmaf(b[2], cc[2], b[1] * cc[1]));
+        if (degree >= 2) {
+            float t = b[4] * cc[4];
+            for (int k = 5; k < 9; ++k) t = fmaf(b[k], cc[k], t);
+            v += t;
+            if (degree >= 3) {
+                float u = b[9] * cc[9];
+                for (int k = 10; k < 16; ++k) u = fmaf(b[k], cc[k], u);
+                v += u;
             }
         }
-        v += 0.5f;
-        rgb[c] = v < 0.0f ? 0.0f : v;
     }
+    v += 0.5f;
+    return v < 0.0f ? 0.0f : v;
+}
+
+// All three channels; coeffs points at one Gaussian's (h_storage, 3) block.
+TDGS_HD void sh_to_color(int degree, const float* coeffs, int h_storage, const float b[16],
+                         float rgb[3]) {
+    for (int c = 0; c < 3; ++c) rgb[c] = sh_channel_to_color(degree, coeffs + c * h_storage, b);
 }
 
 // ------------------------------------------------------------------------------------
@@ -421,9 +423,7 @@ TDGS_HD Projected project_geometry(const tdgs_camera& cam, const tdgs_render_opt
 }
 
 // Colour of a projected Gaussian: SH evaluated along normalize(m - camera position).
-TDGS_HD void project_color(const tdgs_camera& cam, int degree, const float* coeffs,
-                           int h_storage, float x, float y, float z, float rgb[3]) {
-    float b[16];
+TDGS_HD void view_sh_basis(const tdgs_camera& cam, int degree, float x, float y, float z, float b[16]) {
     if (degree > 0) {
         const float vx = x - cam.position[0], vy = y - cam.position[1], vz = z - cam.position[2];
         const float inv = 1.0f / sqrtf(fmaf(vz, vz, fmaf(vy, vy, vx * vx)));
@@ -431,6 +431,12 @@ TDGS_HD void project_color(const tdgs_camera& cam, int degree, const float* coef
     } else {
         b[0] = kSH[0];
     }
+}
+
+TDGS_HD void project_color(const tdgs_camera& cam, int degree, const float* coeffs,
+                           int h_storage, float x, float y, float z, float rgb[3]) {
+    float b[16];
+    view_sh_basis(cam, degree, x, y, z, b);
     sh_to_color(degree, coeffs, h_storage, b, rgb);
 }
 
