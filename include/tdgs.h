@@ -113,7 +113,7 @@ typedef struct tdgs_render_buffers {
     uint8_t* keep;           /* capacity; keep flags (written when non-null) */
     int32_t* fgidx_to_gidx;  /* capacity; 1-based */
     float* depths;           /* capacity */
-    float* f2d;              /* 9 x capacity: [mu_x, mu_y, a, M11, M21, M22, r, g, b] */
+    float* f2d;              /* 9 x capacity: [mu_x, mu_y, a, M11, M21, M22, r, g, b]; 16-byte aligned */
     int32_t* tile_ranges;    /* 4 x capacity: [tx_min, ty_min, tx_max, ty_max] */
     int32_t* counts;         /* capacity; overlapped tiles per filtered Gaussian */
     int64_t* keys;           /* key_capacity; emitted keys (depth order) */

@@ -4,11 +4,11 @@
 // Reference: src/forward_core.jl:196-993, src/forward_structs.jl:743-757.
 //
 // Pipeline of tdgs_render (one host synchronisation, to learn N_f and M):
-//   1. keep flags + kept count per 256 Gaussians  k_keep_counts
-//   2. exclusive scan of the block counts -> N_f  k_scan_tiles
-//   3. compaction + projection, gidx order        k_project (each kept Gaussian's fgidx from
-//                                                 its block offset and rank), also writes a
-//                                                 32-bit depth key
+//   1. keep flags + kept counts per 256 and 1024  k_keep_counts
+//   2-3. compaction + projection, gidx order      k_project (each kept Gaussian's fgidx from
+//                                                 its block's offset, summed from the counts,
+//                                                 and its rank), also writes N_f and a 32-bit
+//                                                 depth key
 //   4. stable sort of (depth bits, fgidx)         radix, bits [0, 32)
 //   5. scan of tile counts in depth order -> M    scan (SortedCounts)
 //   6. key emission in depth order                k_emit_depth_order
@@ -38,12 +38,14 @@ struct KeepEval {
     uint8_t* keep;             // optional keep flags
     int32_t* zero = nullptr;   // optional array zeroed on the side (first zero_n entries)
     int64_t zero_n = 0;
-    __device__ int32_t operator()(int64_t i) const {
+    __device__ bool test(int64_t i, float4 m) const {
         if (i < zero_n) zero[i] = 0;
-        const float4 m = reinterpret_cast<const float4*>(mo)[i];
         const bool k = keep_gaussian(cam, opt, m.x, m.y, m.z, opacity_of(kind, m.w));
         if (keep) keep[i] = k ? 1 : 0;
-        return k ? 1 : 0;
+        return k;
+    }
+    __device__ int32_t operator()(int64_t i) const {
+        return test(i, reinterpret_cast<const float4*>(mo)[i]) ? 1 : 0;
     }
 };
 
@@ -75,8 +77,10 @@ struct ProjectArgs {
     tdgs_camera cam;
     tdgs_tiling tiling;
     tdgs_render_options opt;
-    const int64_t* block_offsets;   // kept Gaussians before each 256-Gaussian block (exclusive)
-    const int64_t* d_nbf;           // device count of filtered Gaussians
+    const int32_t* block_counts;    // kept Gaussians per 256-Gaussian block
+    const int32_t* group_counts;    // kept Gaussians per kKeepSub blocks
+    int64_t ngroups;
+    int64_t* d_nbf;                 // written by workgroup 0: N_f
     int32_t* fgidx_to_gidx;         // written: the order-preserving compaction
     float* depths;
     float* f2d;
@@ -110,21 +114,29 @@ __global__ __launch_bounds__(256) void k_rect_diff(int64_t nbf, const int32_t* _
     atomicAdd(d + y1 * w + x1, 1);
 }
 
-// Keep counts per 256-Gaussian block (fill_keep_gaussians_kernel! and the count half of the
-// compaction scan, forward_core.jl:231-244, 326-355): workgroup b evaluates the keep test of
-// Gaussians [2048 b, 2048 b + 2048) with coalesced loads and writes the 8 block counts.
-// (A single pass with a decoupled look-back over per-workgroup counts measured slower: the
-// cross-workgroup status round trips cost more than this pass and the scan of its counts.)
-constexpr int kKeepSub = 8;
-__global__ __launch_bounds__(256) void k_keep_counts(KeepEval ev, int64_t n, int64_t* __restrict__ block_counts,
-                                                     int64_t nblocks) {
+// Keep counts (fill_keep_gaussians_kernel! and the count half of the compaction scan,
+// forward_core.jl:231-244, 326-355): workgroup g evaluates the keep test of Gaussians
+// [1024 g, 1024 g + 1024) with coalesced loads and writes the counts of its 4 blocks of 256
+// (block_counts) and their sum (group_counts). The projection derives each block's offset
+// from these directly, so no scan pass runs in between. (A single pass with a decoupled
+// look-back over per-workgroup counts measured slower: the cross-workgroup status round
+// trips cost more than this pass.)
+constexpr int kKeepSub = 4;
+__global__ __launch_bounds__(256) void k_keep_counts(KeepEval ev, int64_t n, int32_t* __restrict__ block_counts,
+                                                     int32_t* __restrict__ group_counts, int64_t nblocks) {
     __shared__ int32_t s_cnt[kKeepSub][256 / kWave];
     const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+    float4 mv[kKeepSub];   // all loads in flight before any test
+#pragma unroll
+    for (int k = 0; k < kKeepSub; ++k) {
+        const int64_t i = ((int64_t)blockIdx.x * kKeepSub + k) * 256 + t;
+        mv[k] = i < n ? reinterpret_cast<const float4*>(ev.mo)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     bool kp[kKeepSub];
 #pragma unroll
     for (int k = 0; k < kKeepSub; ++k) {
         const int64_t i = ((int64_t)blockIdx.x * kKeepSub + k) * 256 + t;
-        kp[k] = i < n && ev(i) != 0;
+        kp[k] = i < n && ev.test(i, mv[k]);
     }
 #pragma unroll
     for (int k = 0; k < kKeepSub; ++k) {
@@ -138,6 +150,12 @@ __global__ __launch_bounds__(256) void k_keep_counts(KeepEval ev, int64_t n, int
         for (int w = 0; w < 256 / kWave; ++w) c += s_cnt[t][w];
         if (sb < nblocks) block_counts[sb] = c;
     }
+    if (t == 0) {
+        int32_t c = 0;
+        for (int k = 0; k < kKeepSub; ++k)
+            for (int w = 0; w < 256 / kWave; ++w) c += s_cnt[k][w];
+        group_counts[blockIdx.x] = c;
+    }
 }
 
 // Compaction + projection (fill_fgidx_to_gidx_kernel! and project_fgaussians_kernel!,
@@ -149,36 +167,68 @@ __global__ __launch_bounds__(256) void k_keep_counts(KeepEval ev, int64_t n, int
 // colour evaluated before the workgroup barrier that resolves the ranks. (Staging the SH
 // blocks through LDS for coalescing measured slower once the loads overlap like this.)
 constexpr int kProjThreads = 256;
+constexpr int kGroupLoads = 4;   // group counts per thread per round
 
+template <int KIND>
 __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
     __shared__ int32_t s_wave[kProjThreads / kWave];
+    __shared__ int64_t s_red[2][kProjThreads / kWave];
     __shared__ float s_rec[kProjThreads * 9];   // the block's f2d records, by rank
     const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
     const int64_t gi = (int64_t)blockIdx.x * kProjThreads + t;
     const int64_t n = a.g.n;
-    // all parameter loads issue together (the culled few percent are read for nothing)
-    float4 m = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // all parameter loads issue together, without branches (the culled few percent are read
+    // for nothing; threads past n read the last Gaussian and are not kept)
+    const int64_t gl = gi < n ? gi : n - 1;
+    const float4 m = reinterpret_cast<const float4*>(a.g.means_opacity)[gl];
     float params[7];
-    if (gi < n) {
-        m = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
-        if (a.g.kind == TDGS_TRAINABLE) {
-            params[0] = a.g.scaling[3 * gi];
-            params[1] = a.g.scaling[3 * gi + 1];
-            params[2] = a.g.scaling[3 * gi + 2];
-            const float4 q = reinterpret_cast<const float4*>(a.g.rotation)[gi];
-            params[3] = q.x; params[4] = q.y; params[5] = q.z; params[6] = q.w;
-        } else {
+    if constexpr (KIND == TDGS_TRAINABLE) {
+        params[0] = a.g.scaling[3 * gl];
+        params[1] = a.g.scaling[3 * gl + 1];
+        params[2] = a.g.scaling[3 * gl + 2];
+        const float4 q = reinterpret_cast<const float4*>(a.g.rotation)[gl];
+        params[3] = q.x; params[4] = q.y; params[5] = q.z; params[6] = q.w;
+    } else {
 #pragma unroll
-            for (int k = 0; k < 6; ++k) params[k] = a.g.covariances[6 * gi + k];
-        }
+        for (int k = 0; k < 6; ++k) params[k] = a.g.covariances[6 * gl + k];
     }
-    const float op = opacity_of(a.g.kind, m.w);
+    // this block's offset (kept Gaussians in earlier groups, then in earlier blocks of its
+    // group) and N_f, summed from the group counts (a few KB, read from L2 by every block;
+    // the loads of one round are all in flight together)
+    {
+        const int64_t grp = blockIdx.x / kKeepSub;
+        int64_t before = 0, total = 0;
+        for (int64_t k0 = 0; k0 < a.ngroups; k0 += kGroupLoads * kProjThreads) {
+            int32_t c[kGroupLoads];
+#pragma unroll
+            for (int u = 0; u < kGroupLoads; ++u) {
+                const int64_t k = k0 + u * kProjThreads + t;
+                c[u] = a.group_counts[k < a.ngroups ? k : a.ngroups - 1];   // clamped: no branch
+            }
+#pragma unroll
+            for (int u = 0; u < kGroupLoads; ++u) {
+                const int64_t k = k0 + u * kProjThreads + t;
+                const int32_t cu = k < a.ngroups ? c[u] : 0;
+                total += cu;
+                if (k < grp) before += cu;
+            }
+        }
+        const int32_t bc = a.block_counts[grp * kKeepSub + (t & (kKeepSub - 1))];
+        if (t < (int)(blockIdx.x - grp * kKeepSub)) before += bc;
+#pragma unroll
+        for (int d = kWave / 2; d > 0; d >>= 1) {
+            before += __shfl_xor(before, d, kWave);
+            total += __shfl_xor(total, d, kWave);
+        }
+        if (lane == 0) { s_red[0][wave] = before; s_red[1][wave] = total; }
+    }
+    const float op = opacity_of(KIND, m.w);
     const bool keep = gi < n && keep_gaussian(a.cam, a.opt, m.x, m.y, m.z, op);
     const uint64_t bal = __ballot(keep);
     if (lane == 0) s_wave[wave] = __popcll(bal);
     Projected pr;
     pr.count = 0;
-    if (keep) pr = project_geometry(a.cam, a.opt, a.tiling, a.g.kind, m.x, m.y, m.z, op, params);
+    if (keep) pr = project_geometry(a.cam, a.opt, a.tiling, KIND, m.x, m.y, m.z, op, params);
     float rgb[3];
     if (pr.count > 0) {
         const int hs = (a.g.sh_degree + 1) * (a.g.sh_degree + 1);
@@ -207,7 +257,13 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
         kept += s_wave[w];
     }
     const int local = before + __popcll(bal & lanemask_lt());
-    const int64_t off = a.block_offsets[blockIdx.x];
+    int64_t off = 0, nbf = 0;
+#pragma unroll
+    for (int w = 0; w < kProjThreads / kWave; ++w) {
+        off += s_red[0][w];
+        nbf += s_red[1][w];
+    }
+    if (blockIdx.x == 0 && t == 0) *a.d_nbf = nbf;
     const int64_t f = off + local;   // 0-based fgidx if kept
     if (keep) {
         a.fgidx_to_gidx[f] = (int32_t)(gi + 1);
@@ -230,7 +286,7 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
             a.depth_vals[f] = (int32_t)(f + 1);
         }
     } else if (gi < n && a.depth_keys) {
-        const int64_t slot = *a.d_nbf + (gi - f);   // culled Gaussians fill the slots past N_f
+        const int64_t slot = nbf + (gi - f);   // culled Gaussians fill the slots past N_f
         a.depth_keys[slot] = 0xffffffffu;
         a.depth_vals[slot] = 0;
     }
@@ -239,7 +295,16 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
     // requests)
     __syncthreads();
     float* dst = a.f2d + 9 * off;
-    for (int e = t; e < 9 * kept; e += kProjThreads) dst[e] = s_rec[e];
+    const int total = 9 * kept;
+    const int head = (int)((4 - ((9 * off) & 3)) & 3);   // floats before the first 16-byte boundary
+    if (t < head && t < total) dst[t] = s_rec[t];
+    const int quads = total > head ? (total - head) >> 2 : 0;
+    for (int q = t; q < quads; q += kProjThreads) {
+        const int e = head + 4 * q;
+        *reinterpret_cast<float4*>(dst + e) = make_float4(s_rec[e], s_rec[e + 1], s_rec[e + 2], s_rec[e + 3]);
+    }
+    const int tail = head + 4 * quads;
+    if (tail + t < total) dst[tail + t] = s_rec[tail + t];
 }
 
 // ------------------------------------------------------------------------------------
@@ -265,6 +330,7 @@ struct SortedCounts {
 constexpr int kEmitThreads = 256;
 constexpr int kEmitItems = 16;
 constexpr int kEmitTile = kEmitThreads * kEmitItems;
+static_assert((kKeepSub & (kKeepSub - 1)) == 0, "power of two");
 static_assert(kEmitTile == kRsTile, "one emission workgroup fills one radix count tile");
 
 __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, int64_t x) {
@@ -666,7 +732,8 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(cap);                       // depth values, sorted (fgidx)
     ar.template take<int32_t>(cap);                       // counts scan in depth order
     ar.template take<char>((int64_t)scan_temp_bytes_for(cap));
-    ar.template take<int64_t>(ceil_div(cap, kProjThreads));    // keep counts per projection block
+    ar.template take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub) * kKeepSub);   // keep counts per block
+    ar.template take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub));   // and per kKeepSub blocks
     const int64_t big = cap > key_cap ? cap : key_cap;
     ar.template take<char>((int64_t)radix_temp_bytes(big));
     ar.template take<int32_t>(kRectCopies * rect_diff_size(t));   // tile-coverage difference arrays
@@ -820,6 +887,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     TDGS_REQUIRE(buf->fgidx_to_gidx && buf->depths && buf->f2d && buf->tile_ranges && buf->counts &&
                      buf->tiles_end && buf->temp,
                  "null render buffers");
+    TDGS_REQUIRE(((uintptr_t)buf->f2d & 15) == 0, "render buffers: f2d must be 16-byte aligned");
     const size_t need = tdgs_render_temp_bytes(buf->capacity, buf->key_capacity, tiling);
     if (buf->temp_bytes < need) {
         set_error("render scratch too small: need %zu bytes, have %zu", need, buf->temp_bytes);
@@ -837,7 +905,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     int32_t* cs = ar.take<int32_t>(cap);
     const size_t sbytes = scan_temp_bytes_for(cap);
     void* stemp = ar.take<char>((int64_t)sbytes);
-    int64_t* block_offsets = ar.take<int64_t>(ceil_div(cap, kProjThreads));
+    int32_t* block_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub) * kKeepSub);
+    int32_t* group_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub));
     const int64_t big = cap > buf->key_capacity ? cap : buf->key_capacity;
     const size_t rbytes = radix_temp_bytes(big);
     void* rtemp = ar.take<char>((int64_t)rbytes);
@@ -849,6 +918,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
 
     // 1-2: keep flags, keep counts per projection block, their scan (N_f)
     const int64_t nblocks = ceil_div(n, kProjThreads);
+    const int64_t ngroups = ceil_div(nblocks, kKeepSub);
     {
         StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
         KeepEval ev{g->means_opacity, g->kind, *cam, *opt, buf->keep};
@@ -859,21 +929,22 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
             k_fill_i32<<<(unsigned)ceil_div(kRectCopies * ndiff, 256), 256, 0, s>>>(rect_diff, kRectCopies * ndiff, 0);
             TDGS_LAUNCHED();
         }
-        k_keep_counts<<<(unsigned)ceil_div(nblocks, kKeepSub), 256, 0, s>>>(ev, n, block_offsets, nblocks);
-        TDGS_LAUNCHED();
-        k_scan_tiles<<<1, kScanThreads, 0, s>>>(block_offsets, nblocks, d_nbf);
+        k_keep_counts<<<(unsigned)ngroups, 256, 0, s>>>(ev, n, block_counts, group_counts, nblocks);
         TDGS_LAUNCHED();
     }
     // 3: compaction + projection
     ProjectArgs pa;
     pa.g = *g; pa.cam = *cam; pa.tiling = *tiling; pa.opt = *opt;
-    pa.block_offsets = block_offsets; pa.d_nbf = d_nbf;
+    pa.block_counts = block_counts; pa.group_counts = group_counts; pa.ngroups = ngroups; pa.d_nbf = d_nbf;
     pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
     pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
     pa.depth_keys = dkey; pa.depth_vals = dval;
     {
         StageScope sc(TDGS_STAGE_PROJECT, s);
-        k_project<<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
+        if (g->kind == TDGS_TRAINABLE)
+            k_project<TDGS_TRAINABLE><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
+        else
+            k_project<TDGS_RENDER_ONLY><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
         TDGS_LAUNCHED();
     }
     // 4: Gaussians by (depth bits, fgidx)
