@@ -149,6 +149,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
     while (hi > beg) {
         const int64_t lo = hi - NT > beg ? hi - NT : beg;
         const int nb = (int)(hi - lo);
+        bool low = false;   // a cut below -87 (tiny min_alpha, huge or NaN opacity)
         if (t < nb) {
             const int64_t f = (int64_t)a.sorted_f[lo + t] - 1;
             const float* r = a.f2d + 9 * f;
@@ -159,8 +160,11 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
             // inside the 1e-3 margin of log_min_alpha; a NaN cut never skips)
             rec.c = make_float4(r[8], a.log_min_alpha - log_f(r[2]), 0.0f, 0.0f);
             s_rec[t] = rec;
+            low = !(rec.c.y >= -87.0f);
         }
-        __syncthreads();
+        // A live exponent lies in [cut, 0]; with every cut of the batch at least -87 that is
+        // inside exp_f's polynomial range, so the range vote is skipped.
+        const bool checked = __syncthreads_or(low);
         const int jtop = (int)((int64_t)wave_last - lo < nb ? (int64_t)wave_last - lo : nb);
         const int last_rel = (int)((int64_t)last - lo);   // entry jj of the batch is before last iff jj < last_rel
         // Entries back to front; the 9 contributions of up to kSlots consecutive contributing
@@ -180,20 +184,22 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
                     float du, dv;
                     const float ex = backward_exponent(cu, cv, ra.x, ra.y, ra.w, rb.x, rb.y, &du, &dv);
                     const bool live = on && jj < last_rel && !(ex < rc.y);
-                    if (!__any(live)) continue;
+                    if (!wave_any(live)) continue;
                     bool contrib = false;
-                    const bool wide = __any(live && !(ex >= -87.0f && ex <= 88.0f));
+                    const bool wide = checked && wave_any(live && !(ex >= -87.0f && ex <= 88.0f));
                     if (live) {
                         const float G = wide ? exp_f_sel(ex) : exp_f_core(ex);   // exp_f(ex)
                         const float aG = ra.z * G;
-                        const float alpha = aG < a.max_alpha ? aG : a.max_alpha;   // fminf, non-NaN max_alpha
+                        // min(aG, max_alpha): the select aG < max_alpha ? aG : max_alpha for a
+                        // non-NaN max_alpha, NaN aG included
+                        const float alpha = __builtin_fminf(aG, a.max_alpha);
                         if (!(alpha < a.min_alpha)) {
                             const float c[3] = {rb.z, rb.w, rc.x};
                             backward_pair(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
                             contrib = true;
                         }
                     }
-                    if (__any(contrib)) {
+                    if (wave_any(contrib)) {
                         js[e] = __builtin_amdgcn_readfirstlane(jj);
                         break;
                     }

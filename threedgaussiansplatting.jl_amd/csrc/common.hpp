@@ -69,6 +69,9 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
     return (1ull << __lane_id()) - 1ull;
 }
 
+// Wavefront vote straight from the lane mask (a scalar test, no vector compare).
+__device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
+
 // Device-wide scan over n int32 items produced by a functor, with int64 running sums
 // (scan.hip). In(i) returns item i; Out(i, inclusive, item) consumes the result.
 size_t scan_temp_bytes_internal(int64_t n);

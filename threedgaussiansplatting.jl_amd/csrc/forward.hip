@@ -545,6 +545,7 @@ struct BlendArgs {
     int32_t W, H, TW, TH, ntx;
     float bg0, bg1, bg2, min_alpha, max_alpha, min_T;
     float e_cut;   // exp_f(e) < min_alpha for every exponent e < e_cut
+    int cut_low;   // e_cut < -87: live exponents may leave exp_f's polynomial range
     int64_t m;
     const int32_t* tiles_end;
     const int32_t* sorted_f;
@@ -589,6 +590,7 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     for (int64_t base = beg; base < end; base += NT) {
         if (__syncthreads_count(done ? 0 : 1) == 0) break;
         const int64_t s = base + t;
+        bool big = false;   // opacity above 1e38: exponents may pass 88
         if (s < end) {
             const int64_t f = (int64_t)a.sorted_f[s] - 1;
             const float* r = a.f2d + 9 * f;
@@ -599,8 +601,11 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
             rec.b = make_float4(p[4], p[5], RGB ? r[6] : 0.0f, RGB ? r[7] : 0.0f);
             rec.c = make_float4(RGB ? r[8] : 0.0f, DEPTH ? a.depths[f] : 0.0f, 0.0f, 0.0f);
             s_rec[t] = rec;
+            big = !(r[2] <= 1e38f);
         }
-        __syncthreads();
+        // A live exponent lies in [e_cut, log a]; unless e_cut < -87 or an opacity in the
+        // batch is huge (or NaN), that is inside [-87, 88], where exp_f is its polynomial core.
+        const bool checked = __syncthreads_or(big) || a.cut_low;
         const int nb = (int)((end - base) < NT ? (end - base) : NT);
         if (!done) {
             for (int j = 0; j < nb; ++j) {
@@ -609,11 +614,15 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
                 const float4 rb = s_rec[j].b;
                 const float e = fmaf(ra.x, uu, fmaf(ra.y, vv, fmaf(ra.z, uv, fmaf(ra.w, cu, fmaf(rb.x, cv, rb.y)))));
                 const bool live = !done && !(e < a.e_cut);
-                if (!__any(live)) continue;
-                // exp_f(e): polynomial core unless a live lane is outside [-87, 88] (or NaN)
-                const float ex = __any(live && !(e >= -87.0f && e <= 88.0f)) ? exp_f_sel(e) : exp_f_core(e);
-                const float alpha = ex < a.max_alpha ? ex : a.max_alpha;   // fminf for a non-NaN max_alpha
-                const bool contrib = !done && !(alpha < a.min_alpha);
+                if (!wave_any(live)) continue;
+                // exp_f(e) for the live lanes: the polynomial core unless a live lane is outside
+                // [-87, 88] or NaN (the other lanes' values are not used)
+                const float ex = (checked && wave_any(live && !(e >= -87.0f && e <= 88.0f))) ? exp_f_sel(e)
+                                                                                            : exp_f_core(e);
+                // min(ex, max_alpha); equal to the select ex < max_alpha ? ex : max_alpha for a
+                // non-NaN max_alpha, NaN ex included
+                const float alpha = __builtin_fminf(ex, a.max_alpha);
+                const bool contrib = live && !(alpha < a.min_alpha);
                 const float Tn = T * (1.0f - alpha);
                 const bool stop = contrib && Tn < a.min_T;
                 if (contrib && !stop) {
@@ -630,9 +639,9 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
                     T = Tn;
                     last = (int32_t)(base + j + 1);
                 }
-                if (__any(stop)) {
+                if (wave_any(stop)) {
                     done = done || stop;
-                    if (!__any(!done)) break;
+                    if (!wave_any(!done)) break;
                 }
             }
         }
@@ -689,6 +698,7 @@ static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs
     a.bg0 = o->background[0]; a.bg1 = o->background[1]; a.bg2 = o->background[2];
     a.min_alpha = o->min_alpha; a.max_alpha = o->max_alpha; a.min_T = o->min_transmittance;
     a.e_cut = exponent_cut(o->min_alpha);
+    a.cut_low = !(a.e_cut >= -87.0f);
     a.m = m; a.tiles_end = tiles_end; a.sorted_f = sorted_f; a.f2d = f2d; a.depths = depths;
     a.rgb = out->rgb; a.T = out->T; a.depth = out->depth; a.last = out->last;
     a.evaluations = evaluations;
