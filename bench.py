@@ -131,6 +131,34 @@ def train_bench(core, w, cams, tiling, deg, steps, warmup):
     return steps / (t1 - t0), (t1 - t0) * 1000.0 / steps, stage, tr.current_loss()
 
 
+def train_host_images(core, w, tiling, deg, steps=60, warmup=5, ncams=16):
+    """Training steps of the main workload with the ground truth on the host (pinned,
+    uploaded one step ahead on a copy stream) beside the same steps with it on the device:
+    the difference is what the host-to-device traffic costs once overlapped."""
+    import torch
+    from tdgs_amd import host, training
+    cams = w.cameras[:ncams]
+    rng = np.random.Generator(np.random.PCG64(0x3D6501))
+    host_imgs = [rng.random((c.width, c.height, 3), dtype=np.float32) for c in cams]
+    out = {"cameras": ncams, "steps": steps, "image_MB": round(host_imgs[0].nbytes / 1e6, 2)}
+    for name, images in (("device", [torch.from_numpy(im).cuda() for im in host_imgs]), ("host", host_imgs)):
+        g = core.TrainableGaussiansVector.from_host(w.gaussians, 0)
+        opts = host.RenderOptions.for_camera(cams[0], deg)
+        to = training.TrainingOptions.for_scene(host.scene_radius(w.cameras), sh_degree_increase_interval=10**9)
+        tr = training.Trainer(g, cams, images, opts, tiling, to, seed=1)
+        for _ in range(warmup):
+            tr.training_step_()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tr.training_step_()
+        torch.cuda.synchronize()
+        out[f"{name}_images_it_per_s"] = round(steps / (time.perf_counter() - t0), 2)
+        del tr, g
+        torch.cuda.empty_cache()
+    return out
+
+
 def train_cfg1(core, steps=100, warmup=5):
     """Config 1: one training step (200k Gaussians, 800x800, SH3, L1 + 0.2 DSSIM against a seeded
     uniform target) repeated `steps` times on its single camera."""
@@ -387,7 +415,9 @@ def main():
     extra = None
     if not args.no_extra_configs:
         torch.cuda.empty_cache()
-        extra = {"train_cfg1": train_cfg1(core)}
+        extra = {"train_cfg2_host_images": train_host_images(core, w, tiling, deg)}
+        torch.cuda.empty_cache()
+        extra["train_cfg1"] = train_cfg1(core)
         torch.cuda.empty_cache()
         extra["train_cfg3"] = train_cfg3(core, args.cfg3_iterations)
         torch.cuda.empty_cache()

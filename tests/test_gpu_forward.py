@@ -119,6 +119,24 @@ def test_render_large_footprints_bit_exact(gpu, oracle):
     _assert_forward_equal(r, out, buf)
 
 
+def test_render_needle_gaussians_without_dilation(gpu, oracle):
+    """Needle-thin Gaussians with no dilation: within one wavefront's 8x8 pixels the exponent
+    falls from above the cut to below -1000, where the branch-free exponential core is not
+    exp_f; such lanes must neither contribute nor stop."""
+    w = synthetic.config(0, n=4000)
+    g = w.gaussians
+    g.scaling[:, 0] = np.float32(-7.0)   # sub-pixel width along one axis
+    g.scaling[:, 1] = np.float32(-1.0)
+    g.means_opacity[:, 3] = np.float32(4.0)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 0, dilation_x_px=0.0, dilation_y_px=0.0)
+    r = oracle.render(g, cam, t, opts)
+    out, buf = _gpu_render(gpu, g, cam, t, opts)
+    assert r["nb_keys"] > 1000
+    _assert_forward_equal(r, out, buf)
+
+
 def test_render_filter_mode_and_antialiasing(gpu, oracle):
     w = synthetic.config(0, n=5000)
     cam = w.cameras[0]

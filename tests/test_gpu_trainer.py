@@ -41,3 +41,54 @@ def test_training_steps_exercise_every_branch(gpu):
         assert torch.isfinite(t).all()
     assert len(tr.optimizer.moments) == len(tr.gaussians)
     assert tr.optimizer.moments.sh.shape[2] == 16
+
+
+def test_host_images_upload_ahead(gpu):
+    """GroundTruthImages with host images: uploads run one step ahead on the copy stream and
+    every acquire sees exactly its image, also when a camera repeats at once."""
+    from tdgs_amd import training
+    rng = np.random.default_rng(4)
+    imgs = [rng.random((64, 48, 3), dtype=np.float32) for _ in range(3)]
+    ref = [torch.from_numpy(im).cuda() for im in imgs]
+    gt = training.GroundTruthImages(imgs, torch.device("cuda", 0))
+    assert not gt.on_device
+    seq = [0, 1, 2, 2, 1, 0, 0, 0, 1, 2, 1]
+    scratch = torch.empty((2048, 2048), device="cuda")
+    for i, k in enumerate(seq):
+        gt.prefetch(k)
+        if i + 1 < len(seq):
+            gt.prefetch(seq[i + 1])
+        scratch.normal_()          # unrelated work on the compute stream
+        img = gt.acquire(k)
+        assert torch.equal(img, ref[k])
+        gt.release(k)
+
+
+def test_host_images_match_device_images(gpu):
+    """Training on host images (pinned, uploaded one step ahead) follows training on the same
+    images on the device: the same camera order across permutation boundaries and the same
+    losses (up to the order of the gradient atomics, which differs from run to run)."""
+    from tdgs_amd import training
+    w = synthetic.config(1, n=20_000)
+    cams = synthetic.orbit_cameras(np.random.default_rng(0), 3, 320, 240, 4.0, 60.0)
+    rng = np.random.default_rng(5)
+    host_imgs = [rng.random((320, 240, 3), dtype=np.float32) for _ in cams]
+    opts = host.RenderOptions.for_camera(cams[0], 3)
+    tiling = host.Tiling.for_camera(cams[0], 16, 16)
+    to = training.TrainingOptions.for_scene(host.scene_radius(cams), nb_iterations=100)
+    runs = []
+    for images in (host_imgs, [torch.from_numpy(im).cuda() for im in host_imgs]):
+        g = gpu.TrainableGaussiansVector.from_host(w.gaussians, 0)
+        tr = training.Trainer(g, cams, images, opts, tiling, to, seed=7)
+        assert tr.images.on_device == (images is not host_imgs)
+        order, losses = [], []
+        for _ in range(10):
+            tr.training_step_()
+            order.append(next(i for i, c in enumerate(tr.cameras) if c is tr.last_camera))
+            losses.append(tr.current_loss())
+        torch.cuda.synchronize()
+        runs.append((order, losses))
+    (o1, l1), (o2, l2) = runs
+    assert o1 == o2 and sorted(o1[:3]) == [0, 1, 2] and sorted(o1[3:6]) == [0, 1, 2]
+    assert l1[0] == l2[0]
+    np.testing.assert_allclose(l1, l2, rtol=1e-5)

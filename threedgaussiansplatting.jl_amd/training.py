@@ -249,12 +249,83 @@ def loss_grad_(rendered, gt, grad_out, dssim_weight, sums, temp):
                                C.c_size_t(temp.numel())))
 
 
+class GroundTruthImages:
+    """The ground-truth images of a trainer, on the device or on the host.
+
+    Device images (torch tensors on the GPU) are used in place. Host images (numpy arrays or
+    CPU tensors) are copied once into pinned memory; each step's image is then uploaded on a
+    copy stream of its own into one of two device buffers, one step ahead, so the transfer
+    overlaps the previous step's kernels instead of stalling the step as the blocking
+    copyto! of training.jl:196-201 does. Events order the copy after the last read of the
+    buffer it overwrites and the loss after the copy it reads."""
+
+    def __init__(self, images, device):
+        self.device = device
+        imgs = list(images)
+        self.on_device = all(isinstance(im, torch.Tensor) and im.is_cuda for im in imgs)
+        if self.on_device:
+            self.images = imgs
+            return
+        self.pinned = []
+        for im in imgs:
+            t = im if isinstance(im, torch.Tensor) else torch.from_numpy(np.asarray(im))
+            if t.is_cuda:
+                raise ValueError("images must be all on the device or all on the host")
+            if t.dtype != torch.float32 or t.dim() != 3 or t.shape[2] != 3:
+                raise ValueError(f"host images must be float32 (w, h, 3), got {tuple(t.shape)} {t.dtype}")
+            self.pinned.append(t.contiguous().pin_memory())
+        shapes = {tuple(t.shape) for t in self.pinned}
+        if len(shapes) != 1:
+            raise ValueError(f"host images of different sizes: {sorted(shapes)}")
+        shape = shapes.pop()
+        self.buffers = [torch.empty(shape, dtype=torch.float32, device=device) for _ in range(2)]
+        self.copy_stream = torch.cuda.Stream(device=device)   # default priority
+        self.uploaded = [torch.cuda.Event() for _ in range(2)]
+        self.released = [torch.cuda.Event() for _ in range(2)]
+        for e in self.released:
+            e.record(torch.cuda.current_stream(device))
+        self.slot_image = [None, None]
+        self.next_slot = 0
+
+    def prefetch(self, k):
+        """Start the upload of image k into the next buffer (host images only)."""
+        if self.on_device or k in self.slot_image:
+            return
+        slot = self.next_slot
+        self.next_slot ^= 1
+        with torch.cuda.stream(self.copy_stream):
+            self.copy_stream.wait_event(self.released[slot])
+            self.buffers[slot].copy_(self.pinned[k], non_blocking=True)
+            self.uploaded[slot].record(self.copy_stream)
+        self.slot_image[slot] = k
+
+    def acquire(self, k):
+        """Image k on the device, ordered on the current stream; pair with release(k)."""
+        if self.on_device:
+            return self.images[k]
+        if k not in self.slot_image:
+            self.prefetch(k)
+        slot = self.slot_image.index(k)
+        torch.cuda.current_stream(self.device).wait_event(self.uploaded[slot])
+        return self.buffers[slot]
+
+    def release(self, k):
+        """The current stream has issued its last read of image k's buffer."""
+        if self.on_device:
+            return
+        slot = self.slot_image.index(k)
+        self.released[slot].record(torch.cuda.current_stream(self.device))
+        self.slot_image[slot] = None
+
+
 class Trainer:
     """Trainer (training.jl:40-151) with training_step_ = training_step! (:173-244).
 
-    images[k] is the ground-truth image of cameras[k] as a (w, h, 3) float32 device tensor
-    (the reference's 3 x h x w layout). The camera order is a seeded permutation, redrawn
-    after every pass over the cameras (the reference uses an unseeded randperm!)."""
+    images[k] is the ground-truth image of cameras[k], (w, h, 3) float32 (the reference's
+    3 x h x w layout), either all device tensors or all host arrays (GroundTruthImages). The
+    camera order is a seeded permutation, redrawn after every pass over the cameras (the
+    reference uses an unseeded randperm!); the next step's camera is known one step ahead,
+    so its host image uploads while the current step runs."""
 
     def __init__(self, gaussians: TrainableGaussiansVector, cameras, images, render_options: RenderOptions,
                  tiling: Tiling, training_options: TrainingOptions, optimizer: AdamOptimizer | None = None,
@@ -262,7 +333,7 @@ class Trainer:
         self.device = _dev(device)
         self.gaussians = gaussians
         self.cameras = list(cameras)
-        self.images = list(images)
+        self.images = GroundTruthImages(images, self.device)
         self.render_options = render_options
         self.tiling = tiling
         self.options = training_options
@@ -272,6 +343,7 @@ class Trainer:
         self.iteration_nb = 0
         self.cameras_order = self.rng.permutation(len(self.cameras))
         self.cameras_order_idx = -1
+        self.next_order = None   # the permutation after cameras_order, once drawn
         cam0 = self.cameras[0]
         self.render_outputs = RenderOutputs.for_camera(cam0, device, include_rgb=True, include_transmittance=True,
                                                        include_depth=False, include_last_contributing_indices=True)
@@ -296,16 +368,22 @@ class Trainer:
         self.iteration_nb += 1
         self.cameras_order_idx += 1
         if self.cameras_order_idx >= len(self.cameras_order):
-            self.cameras_order = self.rng.permutation(len(self.cameras))
+            self.cameras_order = self.next_order if self.next_order is not None else \
+                self.rng.permutation(len(self.cameras))
+            self.next_order = None
             self.cameras_order_idx = 0
         self.maybe_increase_sh_degree_()
         k = int(self.cameras_order[self.cameras_order_idx])
+        self.images.prefetch(k)
+        self.images.prefetch(self.peek_next_camera())
         cam = self.cameras[k]
         self.last_camera = cam
         render_(self.render_outputs, self.gaussians, cam, self.tiling, self.render_options, self.render_buffers)
         self.loss_sums.zero_()
-        loss_grad_(self.render_outputs.rgb, self.images[k], self.rgb_image_grad,
+        gt = self.images.acquire(k)
+        loss_grad_(self.render_outputs.rgb, gt, self.rgb_image_grad,
                    self.options.loss_dssim_vs_L1_weight, self.loss_sums, self.loss_temp)
+        self.images.release(k)
         backward_(self.fgradients, self.rgb_image_grad, self.render_outputs, self.gaussians, cam, self.tiling,
                   self.render_options, self.render_buffers)
         in_adc = self.maybe_densify_and_prune_()
@@ -315,6 +393,16 @@ class Trainer:
         if in_adc:
             self.complete_adc_step_()
         self.maybe_opacity_reset_()
+
+    def peek_next_camera(self):
+        """Camera index of the next step (draws the next permutation early if needed; the
+        sequence of permutations is the same as drawing it when it is reached)."""
+        i = self.cameras_order_idx + 1
+        if i < len(self.cameras_order):
+            return int(self.cameras_order[i])
+        if self.next_order is None:
+            self.next_order = self.rng.permutation(len(self.cameras))
+        return int(self.next_order[0])
 
     def maybe_increase_sh_degree_(self):
         """maybe_increase_sh_degree! (training.jl:253-263)."""
