@@ -311,13 +311,13 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
 // Key duplication
 // ------------------------------------------------------------------------------------
 
-// Overlap counts of the Gaussians in depth order (entries past N_f count 0).
+// Overlap counts of the non-empty Gaussians in depth order (entries past N_b count 0).
 struct SortedCounts {
     const int32_t* sorted_f;
     const int32_t* counts;
-    const int64_t* d_nbf;
+    const int64_t* d_nb;
     __device__ int32_t operator()(int64_t j) const {
-        return j < *d_nbf ? counts[sorted_f[j] - 1] : 0;
+        return j < *d_nb ? counts[sorted_f[j] - 1] : 0;
     }
 };
 
@@ -331,7 +331,7 @@ constexpr int kEmitThreads = 256;
 constexpr int kEmitItems = 16;
 constexpr int kEmitTile = kEmitThreads * kEmitItems;
 static_assert((kKeepSub & (kKeepSub - 1)) == 0, "power of two");
-static_assert(kEmitTile == kRsTile, "one emission workgroup fills one radix count tile");
+static_assert(kEmitTile == RsTile<uint64_t>::kTile, "one emission workgroup fills one radix count tile");
 
 __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, int64_t x) {
     int64_t lo = 0, hi = n;  // first index with a[i] > x
@@ -342,10 +342,11 @@ __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, 
     return lo;
 }
 
-// It also counts the digit of the first tile-sort pass (key bits [32, 32 + nbits0)) of its
-// keys, which form one radix count tile: counts0[d][blockIdx.x].
+// sorted_f holds the nb non-empty Gaussians in depth order and cs the inclusive scan of
+// their tile counts. The kernel also counts the digit of the first tile-sort pass (key bits
+// [32, 32 + nbits0)) of its keys, which form one radix count tile: counts0[d][blockIdx.x].
 __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
-    int64_t nbf, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
+    int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
     const float* __restrict__ depths, const int32_t* __restrict__ ranges, int32_t ntx,
     int64_t* __restrict__ keys, int32_t* __restrict__ vals, int nbits0, uint32_t* __restrict__ counts0,
     int64_t count_tiles) {
@@ -355,10 +356,10 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     s_h[threadIdx.x] = 0;
     const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
     const int64_t d1 = (d0 + kEmitTile < m ? d0 + kEmitTile : m) - 1;  // last key of the block
-    if (threadIdx.x < 2) s_range[threadIdx.x] = upper_bound_i32(cs, nbf, threadIdx.x == 0 ? d0 : d1);
+    if (threadIdx.x < 2) s_range[threadIdx.x] = upper_bound_i32(cs, nb, threadIdx.x == 0 ? d0 : d1);
     __syncthreads();
     const int64_t j_lo = s_range[0];
-    const int64_t j_hi = s_range[1] < nbf ? s_range[1] : nbf - 1;
+    const int64_t j_hi = s_range[1] < nb ? s_range[1] : nb - 1;
     const int64_t cnt = j_hi - j_lo + 1;  // Gaussians spanned (each owns >= 1 key here)
     const bool staged = cnt <= kEmitTile;
     if (staged) {
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
             j = j_lo + lo;
             start = s_cs[lo];
         } else {
-            j = upper_bound_i32(cs, nbf, d);
+            j = upper_bound_i32(cs, nb, d);
             start = j == 0 ? 0 : cs[j - 1];
         }
         const int32_t f = sorted_f[j];
@@ -957,22 +958,25 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
             k_project<TDGS_RENDER_ONLY><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
         TDGS_LAUNCHED();
     }
-    // 4: Gaussians by (depth bits, fgidx)
+    // 4: the N_b non-empty Gaussians by (depth bits, fgidx); empty and culled ones (all-ones
+    // depth key) are dropped by the first pass, the later passes sort N_b pairs
+    int64_t* d_nb = ctx->d_counters + 4;
     {
         StageScope sc(TDGS_STAGE_DEPTH_SORT, s);
         TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
-                                            rtemp, rbytes, s));
+                                            rtemp, rbytes, s, nullptr, nullptr, d_nb));
     }
     // 5: tile counts in depth order -> M
     {
         StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
-        TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nbf},
-                             SortedCounts{sorted_f, buf->counts, d_nbf}, WriteInclusiveI32{cs}, n, stemp, sbytes,
+        TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nb},
+                             SortedCounts{sorted_f, buf->counts, d_nb}, WriteInclusiveI32{cs}, n, stemp, sbytes,
                              d_m, s));
     }
-    TDGS_TRY(read_counters(ctx, s, 2));
+    TDGS_TRY(read_counters(ctx, s, 5));
     const int64_t nbf = ctx->h_counters[0];
     const int64_t m = ctx->h_counters[1];
+    const int64_t nb = ctx->h_counters[4];   // non-empty Gaussians: the sorted depth order's length
     *nb_fgaussians_out = (int32_t)nbf;
     *nb_keys_out = m;
     if (nbf == 0 || m == 0) return launch_render_void(s, cam, opt, out);
@@ -993,10 +997,10 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     int32_t* ev2 = emit_into_sorted ? buf->sorted_values : buf->values;
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
-        const int nbits0 = eb - 32 < 8 ? eb - 32 : 8;
+        const int nbits0 = radix_digit_bits(32, eb);   // digit of the first tile-sort pass
         k_emit_depth_order<<<(unsigned)ceil_div(m, kEmitTile), kEmitThreads, 0, s>>>(
-            nbf, m, sorted_f, cs, buf->depths, buf->tile_ranges, tiling->nb_tiles_x, ek, ev2, nbits0,
-            radix_count_table(rtemp), radix_tiles(m));
+            nb, m, sorted_f, cs, buf->depths, buf->tile_ranges, tiling->nb_tiles_x, ek, ev2, nbits0,
+            radix_count_table(rtemp), radix_tiles<uint64_t>(m));
         TDGS_LAUNCHED();
     }
     {

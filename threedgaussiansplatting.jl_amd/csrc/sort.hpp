@@ -1,5 +1,5 @@
 // sort.hpp — stable LSD radix sort of (key, int32 value) pairs on a key bit range
-// [begin_bit, end_bit), 8-bit digits; replaces CUB DeviceRadixSort::SortPairs
+// [begin_bit, end_bit), digits of at most 8 bits; replaces CUB DeviceRadixSort::SortPairs
 // (deps/cub_sort_pairs/cub_sort_pairs_wrapper.cu:31-43).
 //
 // Each pass is three launches over tiles of kRsTile consecutive keys:
@@ -24,10 +24,17 @@
 
 namespace tdgs {
 
-constexpr int kRsThreads = 512;   // scatter / count: threads and keys per thread
-constexpr int kRsItems = 8;
-constexpr int kRsTile = kRsThreads * kRsItems;
+constexpr int kRsThreads = 512;   // scatter / count: threads per workgroup
 constexpr int kRsBins = 256;
+// Keys per thread and per tile (4096-key tiles). 8192-key tiles for the 64-bit keys (twice
+// the keys per digit per tile, so twice-as-long output runs) measured 6% faster on 751M keys
+// but 35% slower on 6M keys (half the workgroups, at 151 VGPRs and 74 KB of LDS each).
+template <class K>
+struct RsTile {
+    static constexpr int kItems = 8;
+    static constexpr int kTile = kRsThreads * kItems;
+};
+constexpr int kRsMinTile = kRsThreads * 8;
 constexpr int kRsWaves = kRsThreads / kWave;
 static_assert(kRsThreads >= kRsBins && kRsThreads % kRsBins == 0, "digit owners");
 
@@ -62,12 +69,13 @@ __device__ __forceinline__ uint32_t digit_excl_scan(uint32_t a, uint32_t* s_tmp)
 // block barrier with s_h complete.
 template <class K>
 __device__ __forceinline__ void tile_digit_histogram(const K* __restrict__ keys, int64_t n, int64_t tile, int shift,
-                                                     int nbits, uint32_t* s_h) {
+                                                     int nbits, uint32_t* s_h, bool drop_max = false) {
+    constexpr int kRsItems = RsTile<K>::kItems;
     const int t = threadIdx.x;
     for (int i = t; i < kRsBins; i += kRsThreads) s_h[i] = 0;
     __syncthreads();
     const uint32_t mask = (1u << nbits) - 1u;
-    const int64_t base = tile * kRsTile + t;
+    const int64_t base = tile * RsTile<K>::kTile + t;
     K key[kRsItems];
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
@@ -76,7 +84,7 @@ __device__ __forceinline__ void tile_digit_histogram(const K* __restrict__ keys,
     }
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        const bool valid = base + (int64_t)k * kRsThreads < n;
+        const bool valid = base + (int64_t)k * kRsThreads < n && !(drop_max && key[k] == ~(K)0);
         const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
         const uint64_t peers = match_digit(d, nbits, valid);
         if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&s_h[d], (uint32_t)__popcll(peers));
@@ -84,11 +92,14 @@ __device__ __forceinline__ void tile_digit_histogram(const K* __restrict__ keys,
     __syncthreads();
 }
 
+// d_n, when not null, replaces n by a count computed on the device (the grid still covers n);
+// drop_max leaves keys equal to the all-ones key out of the count (and of the sort).
 template <class K>
 __global__ __launch_bounds__(kRsThreads) void k_rs_count(const K* __restrict__ keys, int64_t n, int shift,
-                                                         int nbits, uint32_t* __restrict__ counts, int64_t tiles) {
+                                                         int nbits, uint32_t* __restrict__ counts, int64_t tiles,
+                                                         const int64_t* d_n, int drop_max) {
     __shared__ uint32_t s_h[kRsBins];
-    tile_digit_histogram(keys, n, blockIdx.x, shift, nbits, s_h);
+    tile_digit_histogram(keys, d_n ? *d_n : n, blockIdx.x, shift, nbits, s_h, drop_max != 0);
     if (threadIdx.x < kRsBins) counts[(int64_t)threadIdx.x * tiles + blockIdx.x] = s_h[threadIdx.x];
 }
 
@@ -137,16 +148,21 @@ template <class K>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_rs_scatter(
     const K* __restrict__ kin, const int32_t* __restrict__ vin, K* __restrict__ kout,
     int32_t* __restrict__ vout, int64_t n, int shift, int nbits, const uint32_t* __restrict__ offsets,
-    const uint32_t* __restrict__ totals, int64_t tiles, uint32_t* err) {
+    const uint32_t* __restrict__ totals, int64_t tiles, uint32_t* err, const int64_t* d_n, int drop_max,
+    int64_t* d_kept) {
+    constexpr int kRsItems = RsTile<K>::kItems;
+    constexpr int kRsTile = RsTile<K>::kTile;
     __shared__ K s_buf[kRsTile];                 // the tile in digit order: keys, then values
     __shared__ uint32_t s_wh[kRsWaves][kRsBins];  // per-wave digit counts -> offsets
     __shared__ uint32_t s_local[kRsBins];         // start of each digit inside the tile
     __shared__ int32_t s_delta[kRsBins];          // output index - tile-local index
     __shared__ uint32_t s_tmp[kRsWaves];
 
+    __shared__ uint32_t s_tile_n;                 // keys of the tile that are sorted
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const bool owner = t < kRsBins;
     const int64_t tile = blockIdx.x;
+    if (d_n) n = *d_n;
     const uint32_t total_t = owner ? totals[t] : 0u;
     const uint32_t off_t = owner ? offsets[(int64_t)t * tiles + tile] : 0u;
     for (int i = t; i < kRsWaves * kRsBins; i += kRsThreads) (&s_wh[0][0])[i] = 0;
@@ -167,15 +183,16 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     }
     // Rank inside the wavefront, items in index order: the first lane of each group of equal
     // digits advances the wave's counter for that digit after every lane has read it.
+    bool keep[kRsItems];
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        const bool valid = wbase + k * kWave < nn;
+        keep[k] = wbase + k * kWave < nn && !(drop_max && key[k] == ~(K)0);
         const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
-        const uint64_t peers = match_digit(d, nbits, valid);
+        const uint64_t peers = match_digit(d, nbits, keep[k]);
         const uint64_t below = peers & lanemask_lt();
         const uint32_t cnt = s_wh[w][d];
         pos[k] = cnt + (uint32_t)__popcll(below);
-        if (valid && below == 0) s_wh[w][d] = cnt + (uint32_t)__popcll(peers);
+        if (keep[k] && below == 0) s_wh[w][d] = cnt + (uint32_t)__popcll(peers);
     }
     __syncthreads();
 
@@ -195,20 +212,24 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     if (owner) {
         s_local[t] = local;
         s_delta[t] = (int32_t)(bin + off_t) - (int32_t)local;
+        if (t == kRsBins - 1) {
+            s_tile_n = local + tot;
+            if (d_kept && tile == 0) *d_kept = (int64_t)bin + total_t;   // keys sorted in all
+        }
     }
     __syncthreads();
 
     // Stage keys in digit order, then write contiguous runs per digit.
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        if (wbase + k * kWave < nn) {
+        if (keep[k]) {
             const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
             pos[k] += s_local[d] + s_wh[w][d];
             if (pos[k] < (uint32_t)kRsTile) s_buf[pos[k]] = key[k];
         }
     }
     __syncthreads();
-    const int tile_n = nn - base < kRsTile ? nn - base : kRsTile;
+    const int tile_n = (int)s_tile_n;
     int32_t opos[kRsItems];
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
@@ -230,8 +251,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     int32_t* s_val = reinterpret_cast<int32_t*>(s_buf);
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        const int32_t i = wbase + k * kWave;
-        if (i < nn && pos[k] < (uint32_t)kRsTile) s_val[pos[k]] = val[k];
+        if (keep[k] && pos[k] < (uint32_t)kRsTile) s_val[pos[k]] = val[k];
     }
     __syncthreads();
 #pragma unroll
@@ -245,7 +265,16 @@ inline int radix_passes(int begin_bit, int end_bit) {
     return end_bit > begin_bit ? (end_bit - begin_bit + 7) / 8 : 0;
 }
 
-inline int64_t radix_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, kRsTile); }
+// Digit width of every pass but possibly the last: the bits spread evenly over the passes
+// (14 bits sort as 7 + 7, not 8 + 6), so no pass scatters into more bins than it needs; more
+// keys per bin per tile means longer contiguous output runs.
+inline int radix_digit_bits(int begin_bit, int end_bit) {
+    const int passes = radix_passes(begin_bit, end_bit);
+    return passes > 0 ? (end_bit - begin_bit + passes - 1) / passes : 0;
+}
+
+template <class K>
+inline int64_t radix_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, RsTile<K>::kTile); }
 
 // The count table inside radix_sort_pairs' scratch, for producers that fill the first
 // pass's counts themselves.
@@ -253,29 +282,42 @@ inline uint32_t* radix_count_table(void* temp) { return (uint32_t*)temp; }
 
 // Scratch for radix_sort_pairs, excluding the ping-pong buffers: the digit-major count
 // table, the digit totals and an error word.
+// (Sized for the smallest tile, so it serves both key widths.)
 inline size_t radix_temp_bytes(int64_t n) {
-    return align_up((size_t)radix_tiles(n) * kRsBins * sizeof(uint32_t)) + align_up((kRsBins + 64) * 4);
+    return align_up((size_t)ceil_div(n > 0 ? n : 1, kRsMinTile) * kRsBins * sizeof(uint32_t)) +
+           align_up((kRsBins + 64) * 4);
 }
 
 // Sort n pairs from (kin, vin) into (kout, vout) on key bits [begin_bit, end_bit).
 // (alt_k, alt_v) is the ping-pong buffer. The first pass writes (kout) when the pass count is
 // odd and (alt) when it is even, so kin may alias whichever of the two the first pass does
 // not write (and it is never written otherwise). first_counts, when not null, is the count
-// table of the first pass ([256][radix_tiles(n)] digit-major, from the producer of the
+// table of the first pass ([256][radix_tiles<K>(n)] digit-major, from the producer of the
 // keys); it is consumed (scanned in place). `err` (device word, may be null) is set nonzero
 // if the counts disagree with the keys (the affected keys are not written).
+//
+// kept_out (device word, may be null) asks for the pairs whose key is all ones to be left
+// out: they are not counted or written by the first pass, the later passes sort only the
+// kept pairs (their count read on the device, so the host needs no synchronisation), and the
+// count of kept pairs is written to *kept_out. The output then holds the kept pairs, stably
+// sorted, in its first *kept_out entries.
 template <class K>
 int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K* alt_k,
                      int32_t* alt_v, int64_t n, int begin_bit, int end_bit, void* temp,
                      size_t temp_bytes, hipStream_t stream, uint32_t* first_counts = nullptr,
-                     uint32_t* err = nullptr) {
+                     uint32_t* err = nullptr, int64_t* kept_out = nullptr) {
     const int passes = radix_passes(begin_bit, end_bit);
+    const int width = radix_digit_bits(begin_bit, end_bit);
     if (n <= 0) return TDGS_OK;
     if (n > (int64_t)INT32_MAX) {
         set_error("radix sort of %lld keys exceeds the int32 index range", (long long)n);
         return TDGS_ERR_INVALID;
     }
     if (passes == 0) {
+        if (kept_out) {
+            set_error("radix sort: dropping keys needs at least one pass");
+            return TDGS_ERR_INVALID;
+        }
         if (kout != kin) TDGS_HIP(hipMemcpyAsync(kout, kin, n * sizeof(K), hipMemcpyDeviceToDevice, stream));
         if (vout != vin) TDGS_HIP(hipMemcpyAsync(vout, vin, n * sizeof(int32_t), hipMemcpyDeviceToDevice, stream));
         return TDGS_OK;
@@ -284,29 +326,36 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
         set_error("radix sort scratch too small (%zu bytes for %lld keys)", temp_bytes, (long long)n);
         return TDGS_ERR_CAPACITY;
     }
-    const int64_t tiles = radix_tiles(n);
+    const int64_t tiles = radix_tiles<K>(n);
     uint32_t* counts = (uint32_t*)temp;
-    uint32_t* totals = (uint32_t*)((char*)temp + align_up((size_t)tiles * kRsBins * sizeof(uint32_t)));
+    uint32_t* totals = (uint32_t*)((char*)temp + align_up((size_t)ceil_div(n, kRsMinTile) * kRsBins * sizeof(uint32_t)));
     if (!err) err = totals + kRsBins;
     const K* src_k = kin;
     const int32_t* src_v = vin;
     for (int p = 0; p < passes; ++p) {
-        const int shift = begin_bit + 8 * p;
-        const int nbits = end_bit - shift < 8 ? end_bit - shift : 8;
+        const int shift = begin_bit + width * p;
+        const int nbits = end_bit - shift < width ? end_bit - shift : width;
         const bool to_out = ((passes - 1 - p) % 2) == 0;
         K* dk = to_out ? kout : alt_k;
         int32_t* dv = to_out ? vout : alt_v;
         uint32_t* table = counts;
+        const int64_t* d_n = (kept_out && p > 0) ? kept_out : nullptr;
+        const int drop = (kept_out && p == 0) ? 1 : 0;
         if (p == 0 && first_counts) {
+            if (kept_out) {
+                set_error("radix sort: dropping keys with producer counts is not supported");
+                return TDGS_ERR_INVALID;
+            }
             table = first_counts;
         } else {
-            k_rs_count<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, n, shift, nbits, table, tiles);
+            k_rs_count<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, n, shift, nbits, table, tiles, d_n, drop);
             TDGS_LAUNCHED();
         }
         k_rs_scan_rows<<<kRsBins, 256, 0, stream>>>(table, tiles, totals);
         TDGS_LAUNCHED();
         k_rs_scatter<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, src_v, dk, dv, n, shift, nbits, table,
-                                                                     totals, tiles, err);
+                                                                     totals, tiles, err, d_n, drop,
+                                                                     drop ? kept_out : nullptr);
         TDGS_LAUNCHED();
         src_k = dk;
         src_v = dv;
