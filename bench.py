@@ -32,9 +32,11 @@ __graft_entry__.load_package()
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3       # MI355X vector FP32 (published)
 
-# FLOP of one (pixel, sorted entry) evaluation of the blending loop: exponent 5 FMA (10),
-# exp 19, min/1-alpha/T(1-alpha)/weight 4, colour 3 FMA (6) (contributing evaluations).
-BLEND_FLOP_PER_EVALUATION = 39
+# FLOP of the blending loop per (pixel, sorted entry) evaluation: the exponent, 5 FMA (10),
+# for every evaluation; for one that passes the exponent cut also the exponential (1 mul,
+# 2 + 8 FMA, 1 mul: 22) and 1 - alpha, T (1 - alpha) (2); for a contributing one also the
+# weight T alpha (1) and the colour, 3 FMA (6).
+BLEND_FLOP_EVAL, BLEND_FLOP_LIVE, BLEND_FLOP_CONTRIB = 10, 24, 7
 
 STAGES = ["cull_compact", "project", "depth_sort", "count_scan", "emit", "tile_sort", "tile_ranges",
           "blend", "backward_blend", "backward_project", "adam", "adc", "loss"]
@@ -86,7 +88,7 @@ def frame_stats(core, g, cams, tiling, opts, outputs, buffers, idx):
     """N_f, N_b, M and blending evaluations E for the given cameras (untimed pass)."""
     import torch
     L = core.lib()
-    ev = torch.zeros(1, dtype=torch.int64, device="cuda")
+    ev = torch.zeros(3, dtype=torch.int64, device="cuda")
     st = []
     for k in idx:
         core.render_(outputs, g, cams[k], tiling, opts, buffers)
@@ -96,7 +98,8 @@ def frame_stats(core, g, cams, tiling, opts, outputs, buffers, idx):
         core.check(L.tdgs_blend_evaluations(core.stream_ptr(0), C.byref(cams[k].to_c()), C.byref(tiling.to_c()),
                                             C.byref(opts.to_c()), C.byref(buffers.struct()),
                                             C.c_int64(buffers.nb_keys), C.c_void_p(ev.data_ptr())))
-        st.append((nf, nb, buffers.nb_keys, int(ev.item())))
+        e = ev.cpu().tolist()
+        st.append((nf, nb, buffers.nb_keys, e[0], e[1], e[2]))
     torch.cuda.synchronize()
     return np.array(st, dtype=np.float64)
 
@@ -369,7 +372,7 @@ def main():
     used = sorted({k % ncam for k in range(args.steps)})
     st = frame_stats(core, g, cams, tiling, opts, out, buf, used)
     n = len(g)
-    nf, nb, m, evals = st.mean(axis=0)
+    nf, nb, m, evals, evals_live, evals_contrib = st.mean(axis=0)
     npx = cam0.width * cam0.height
     h = (deg + 1) ** 2
     stage_ms = {STAGES[i]: ms[i] / cnt[i] for i in range(13) if cnt[i] > 0}
@@ -385,7 +388,7 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
                 "algorithmic_bytes_per_launch": int(b_dom), "mean_launch_ms": round(stage_ms[dom], 4)}
     if dom == "blend":
-        flop = BLEND_FLOP_PER_EVALUATION * evals
+        flop = BLEND_FLOP_EVAL * evals + BLEND_FLOP_LIVE * evals_live + BLEND_FLOP_CONTRIB * evals_contrib
         tflops = flop / (stage_ms[dom] * 1e-3) / 1e12
         if tflops / FP32_PEAK_TFLOPS > roofline["frac"]:
             roofline.update({"bound": "valu", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS,
@@ -433,7 +436,8 @@ def main():
         "frame_ms_p50": round(float(np.percentile(frame_ms, 50)), 4),
         "frame_ms_p99": round(float(np.percentile(frame_ms, 99)), 4),
         "mean_counts": {"filtered": round(nf), "nonempty": round(nb), "keys": round(m),
-                        "blend_evaluations": round(evals)},
+                        "blend_evaluations": round(evals), "blend_evaluations_live": round(evals_live),
+                        "blend_evaluations_contributing": round(evals_contrib)},
         "train": train,
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
         "stage_algorithmic_GBs": {k: round(v, 1) for k, v in stage_gbs.items()},

@@ -259,9 +259,10 @@ int tdgs_render_tiles(void* stream, const tdgs_camera* cam, const tdgs_tiling* t
                       const tdgs_render_outputs* out);
 
 /* Instrumentation: replays the blending of the last tdgs_render (same buffers, nb_keys keys)
- * without writing images and adds the number of (pixel, sorted entry) evaluations made
- * before each pixel's early exit to *evaluations_dev (device). No reference counterpart:
- * it sizes the FLOP count of the blending kernel for roofline reporting. */
+ * without writing images and adds to evaluations_dev[0..2] (device) the number of (pixel,
+ * sorted entry) evaluations made before each pixel's early exit, how many of them passed
+ * the exponent cut (exponential evaluated), and how many contributed. No reference
+ * counterpart: it sizes the FLOP count of the blending kernel for roofline reporting. */
 int tdgs_blend_evaluations(void* stream, const tdgs_camera* cam, const tdgs_tiling* tiling,
                            const tdgs_render_options* opt, const tdgs_render_buffers* buf,
                            int64_t nb_keys, uint64_t* evaluations_dev);

@@ -161,3 +161,21 @@ def test_render_void_when_nothing_visible(gpu, oracle):
     np.testing.assert_array_equal(rgb[..., 2], 0.75)
     assert np.all(out.T.cpu().numpy() == 1) and np.all(out.last.cpu().numpy() == 0)
     assert np.all(np.isinf(out.depth.cpu().numpy()))
+
+
+def test_blend_evaluation_counts(gpu):
+    """The instrumentation replay (roofline FLOP counts) on the cfg0 scene: evaluations >=
+    those past the exponent cut >= contributing ones >= pixels with a last contributor."""
+    import ctypes as C
+    w = synthetic.config(0, n=5000)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 0)
+    out, buf = _gpu_render(gpu, w.gaussians, cam, t, opts)
+    ev = torch.zeros(3, dtype=torch.int64, device="cuda")
+    gpu.check(gpu.lib().tdgs_blend_evaluations(gpu.stream_ptr(0), C.byref(cam.to_c()), C.byref(t.to_c()),
+                                               C.byref(opts.to_c()), C.byref(buf.struct()),
+                                               C.c_int64(buf.nb_keys), C.c_void_p(ev.data_ptr())))
+    e, live, contrib = ev.cpu().tolist()
+    covered = int((out.last.cpu().numpy() > 0).sum())
+    assert e >= live >= contrib >= covered > 0

@@ -556,7 +556,7 @@ struct BlendArgs {
     float* T;
     float* depth;
     int32_t* last;
-    unsigned long long* evaluations;  // COUNT variant: number of pixel x entry evaluations
+    unsigned long long* evaluations;  // COUNT variant: [evaluations, live, contributing]
 };
 
 // One workgroup per tile, one thread per pixel (tile_pixel). Each batch of TW*TH sorted
@@ -587,7 +587,7 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f, D = 0.0f;
     int32_t last = 0;
     bool done = !on;
-    unsigned long long evals = 0;
+    unsigned long long evals = 0, live_n = 0, contrib_n = 0;
     for (int64_t base = beg; base < end; base += NT) {
         if (__syncthreads_count(done ? 0 : 1) == 0) break;
         const int64_t s = base + t;
@@ -624,6 +624,10 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
                 // non-NaN max_alpha, NaN ex included
                 const float alpha = __builtin_fminf(ex, a.max_alpha);
                 const bool contrib = live && !(alpha < a.min_alpha);
+                if (COUNT) {
+                    live_n += live ? 1 : 0;
+                    contrib_n += contrib ? 1 : 0;
+                }
                 const float Tn = T * (1.0f - alpha);
                 const bool stop = contrib && Tn < a.min_T;
                 if (contrib && !stop) {
@@ -648,8 +652,16 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
         }
     }
     if (COUNT) {
-        for (int d = 32; d >= 1; d >>= 1) evals += __shfl_xor(evals, d, kWave);
-        if (__lane_id() == 0) atomicAdd(a.evaluations, evals);
+        for (int d = 32; d >= 1; d >>= 1) {
+            evals += __shfl_xor(evals, d, kWave);
+            live_n += __shfl_xor(live_n, d, kWave);
+            contrib_n += __shfl_xor(contrib_n, d, kWave);
+        }
+        if (__lane_id() == 0) {
+            atomicAdd(a.evaluations, evals);
+            atomicAdd(a.evaluations + 1, live_n);
+            atomicAdd(a.evaluations + 2, contrib_n);
+        }
         return;
     }
     if (!on) return;
