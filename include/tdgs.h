@@ -376,6 +376,23 @@ int tdgs_opacity_reset(void* stream, tdgs_gaussians* g, float max_logit,
 int tdgs_sh_resize(void* stream, const float* src, int32_t h_src, float* dst, int32_t h_dst,
                    int64_t n, int32_t interleave);
 
+/* ---- viewer output ---------------------------------------------------------------------- */
+
+enum { TDGS_IMAGE_RGB = 0, TDGS_IMAGE_TRANSMITTANCE = 1, TDGS_IMAGE_DEPTH = 2 };
+
+/* One rendered image to the UInt8 3 x width x height (channel fastest, then x, then y)
+ * buffer an OpenGL RGB texture takes, as convert_rgb_to_gl_img_kernel!,
+ * convert_transmittance_to_gl_img_kernel! and convert_depth_to_gl_img_kernel!
+ * (gui.jl:958-1067) write it into the viewer's pixel buffer:
+ *   RGB (3 x h x w, values >= 0):  v <= 1 ? round(v * 255) : 255 per channel;
+ *   transmittance (h x w, [0, 1]): round(T * 255) in all three channels;
+ *   depth (h x w):                 round((1 - clamp01((d - min_depth) / (max_depth -
+ *                                   min_depth))) * 255) in all three channels
+ * (round = to nearest, ties to even; products in float). dst holds 3 * width * height bytes;
+ * min_depth < max_depth is required for TDGS_IMAGE_DEPTH. */
+int tdgs_image_to_rgb8(void* stream, int32_t kind, const float* src, int32_t width, int32_t height,
+                       float min_depth, float max_depth, uint8_t* dst);
+
 #ifdef __cplusplus
 }
 #endif

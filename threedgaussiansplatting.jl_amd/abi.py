@@ -16,6 +16,9 @@ TDGS_RENDER_ONLY = 1
 TDGS_CLIP_CLAMP = 0
 TDGS_CLIP_FILTER = 1
 TDGS_FLAG_EXACT_SH_JACOBIAN = 0x1
+TDGS_IMAGE_RGB = 0
+TDGS_IMAGE_TRANSMITTANCE = 1
+TDGS_IMAGE_DEPTH = 2
 
 fp = C.POINTER(C.c_float)
 i32p = C.POINTER(C.c_int32)

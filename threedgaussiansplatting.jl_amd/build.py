@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(HERE, "..", "include")
 LIB = os.path.join(HERE, "libtdgs.so")
 OBJDIR = os.path.join(HERE, "_build")
-SOURCES = ["context.hip", "forward.hip", "backward.hip", "train.hip", "loss.hip"]
+SOURCES = ["context.hip", "forward.hip", "backward.hip", "train.hip", "loss.hip", "image.hip"]
 ARCH = os.environ.get("TDGS_OFFLOAD_ARCH", "gfx950")
 
 

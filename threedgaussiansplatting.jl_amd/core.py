@@ -354,6 +354,22 @@ def tile_ranges(sorted_keys: torch.Tensor, nb_tiles: int):
     return te
 
 
+def image_to_rgb8(image: torch.Tensor, kind=abi.TDGS_IMAGE_RGB, min_depth=0.0, max_depth=1.0,
+                  out: torch.Tensor | None = None):
+    """The viewer's UInt8 image (gui.jl:958-1067) of a rendered rgb (w, h, 3), T or depth
+    (w, h) image: a (h, w, 3) uint8 tensor, i.e. Julia's 3 x w x h."""
+    w, h = int(image.shape[0]), int(image.shape[1])
+    expect = (w, h, 3) if kind == abi.TDGS_IMAGE_RGB else (w, h)
+    if tuple(image.shape) != expect or image.dtype != torch.float32 or not image.is_contiguous():
+        raise ValueError(f"image must be contiguous float32 {expect}, got {tuple(image.shape)} {image.dtype}")
+    if out is None:
+        out = torch.empty((h, w, 3), dtype=torch.uint8, device=image.device)
+    check(lib().tdgs_image_to_rgb8(stream_ptr(image.device.index), C.c_int32(kind), C.c_void_p(dptr(image)),
+                                   C.c_int32(w), C.c_int32(h), C.c_float(min_depth), C.c_float(max_depth),
+                                   C.c_void_p(dptr(out))))
+    return out
+
+
 # ------------------------------------------------------------------------------------
 # backward!
 # ------------------------------------------------------------------------------------
