@@ -104,6 +104,22 @@ struct BackBlendArgs {
     float* grads2d;
 };
 
+// Tile of this workgroup. Workgroups go to the 8 XCDs round-robin, and neighbouring tiles
+// share most of their Gaussians, so a row-major order has the workgroups running at any
+// moment flush their per-(tile, Gaussian) gradient atomics onto the same addresses. The
+// workgroups are instead dealt over kBwdBands contiguous bands of the tile grid (workgroup l
+// takes the next tile of band l mod kBwdBands), so concurrent workgroups work in different
+// parts of the image; a bijection for any tile count. Measured at cfg2: 0.66 ms instead of
+// 0.76 ms (8 bands: 0.68 ms, 2048: 0.69 ms).
+constexpr int kBwdBands = 256;
+__device__ __forceinline__ void backward_tile(int ntx, int nty, int* tx, int* ty) {
+    const int lin = blockIdx.x + blockIdx.y * gridDim.x, T = ntx * nty;
+    const int b = lin % kBwdBands, q = T / kBwdBands, r = T % kBwdBands;
+    const int l = b * q + (b < r ? b : r) + lin / kBwdBands;
+    *tx = l % ntx + 1;
+    *ty = l / ntx + 1;
+}
+
 __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
     extern __shared__ float4 s_raw4[];
     const int NT = a.TW * a.TH;
@@ -112,7 +128,8 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
     __shared__ int s_max_last;
     const int t = threadIdx.x;
     const int lane = __lane_id();
-    const int tx = blockIdx.x + 1, ty = blockIdx.y + 1;
+    int tx, ty;
+    backward_tile(a.ntx, (int)gridDim.y, &tx, &ty);
     const int tile = tx + (ty - 1) * a.ntx;
     int u_in, v_in;
     tile_pixel(t, a.TW, a.TH, &u_in, &v_in);
