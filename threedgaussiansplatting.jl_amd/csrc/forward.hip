@@ -36,10 +36,7 @@ struct KeepEval {
     tdgs_camera cam;
     tdgs_render_options opt;
     uint8_t* keep;             // optional keep flags
-    int32_t* zero = nullptr;   // optional array zeroed on the side (first zero_n entries)
-    int64_t zero_n = 0;
     __device__ bool test(int64_t i, float4 m) const {
-        if (i < zero_n) zero[i] = 0;
         const bool k = keep_gaussian(cam, opt, m.x, m.y, m.z, opacity_of(kind, m.w));
         if (keep) keep[i] = k ? 1 : 0;
         return k;
@@ -945,13 +942,6 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     {
         StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
         KeepEval ev{g->means_opacity, g->kind, *cam, *opt, buf->keep};
-        if (n >= kRectCopies * ndiff) {
-            ev.zero = rect_diff;   // zeroed on the side of the keep pass
-            ev.zero_n = kRectCopies * ndiff;
-        } else {
-            k_fill_i32<<<(unsigned)ceil_div(kRectCopies * ndiff, 256), 256, 0, s>>>(rect_diff, kRectCopies * ndiff, 0);
-            TDGS_LAUNCHED();
-        }
         k_keep_counts<<<(unsigned)ngroups, 256, 0, s>>>(ev, n, block_counts, group_counts, nblocks);
         TDGS_LAUNCHED();
     }
@@ -1026,6 +1016,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     {
         StageScope sc(TDGS_STAGE_TILE_RANGES, s);
         if (m > kRectKeysPerGaussian * nbf) {
+            k_fill_i32<<<(unsigned)ceil_div(kRectCopies * ndiff, 256), 256, 0, s>>>(rect_diff, kRectCopies * ndiff, 0);
+            TDGS_LAUNCHED();
             k_rect_diff<<<(unsigned)ceil_div(nbf, 256), 256, 0, s>>>(nbf, buf->counts, buf->tile_ranges,
                                                                     tiling->nb_tiles_x, rect_diff, ndiff);
             TDGS_LAUNCHED();
