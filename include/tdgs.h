@@ -116,8 +116,8 @@ typedef struct tdgs_render_buffers {
     float* f2d;              /* 9 x capacity: [mu_x, mu_y, a, M11, M21, M22, r, g, b]; 16-byte aligned */
     int32_t* tile_ranges;    /* 4 x capacity: [tx_min, ty_min, tx_max, ty_max] */
     int32_t* counts;         /* capacity; overlapped tiles per filtered Gaussian */
-    int64_t* keys;           /* key_capacity; emitted keys (depth order) */
-    int32_t* values;         /* key_capacity */
+    int64_t* keys;           /* key_capacity; scratch of the tile sort */
+    int32_t* values;         /* key_capacity; scratch of the tile sort */
     int64_t* sorted_keys;    /* key_capacity */
     int32_t* sorted_values;  /* key_capacity; sdfgidx_to_fgidx, 1-based */
     int32_t* tiles_end;      /* nb_tiles; tiles_end_sdfgidx */
@@ -275,11 +275,20 @@ size_t tdgs_render_temp_bytes(int32_t capacity, int64_t key_capacity, const tdgs
 /* render! GPU (forward_core.jl:196-314): cull, compact, project, duplicate, sort, ranges,
  * raster. Synchronises once to learn the filtered count and the key count. When the key
  * count exceeds buf->key_capacity it returns TDGS_ERR_CAPACITY with *nb_keys_out set and
- * leaves the outputs untouched; grow the key arrays (and temp) and call again. */
+ * leaves the outputs untouched; grow the key arrays (and temp) and call again.
+ * With at most 65535 tiles the sort by tile moves 16-bit tile ids, not the 64-bit keys, and
+ * buf->sorted_keys is not written: tdgs_render_sorted_keys assembles it on request. */
 int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
                 const tdgs_tiling* tiling, const tdgs_render_options* opt,
                 tdgs_render_buffers* buf, const tdgs_render_outputs* out,
                 int32_t* nb_fgaussians_out, int64_t* nb_keys_out);
+
+/* The sorted keys of the last tdgs_render with these buffers and tiling (nb_keys keys), as
+ * the reference's RenderBuffers hold them after sort_keys_and_sdfgidx!
+ * (forward_core.jl:641-659): (tile << 32) | depth bits, ascending, into buf->sorted_keys.
+ * Nothing to do when the render sorted 64-bit keys (more than 65535 tiles). */
+int tdgs_render_sorted_keys(void* stream, const tdgs_tiling* tiling, const tdgs_render_buffers* buf,
+                            int64_t nb_keys);
 
 /* ---- backward: backward! -------------------------------------------------------------- */
 

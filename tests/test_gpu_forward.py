@@ -104,6 +104,23 @@ def test_render_synthetic_bit_exact(gpu, oracle, cfg, n, tile):
     _assert_forward_equal(r, out, buf)
 
 
+@pytest.mark.parametrize("width", [2040, 2048])
+def test_render_tile_id_width_boundary(gpu, oracle, width):
+    """8x8 tiles on width x 2056 pixels: 255 x 257 = 65535 tiles (the largest tiling whose
+    tile ids the sort moves as 16-bit values, keys assembled on request) and 256 x 257 = 65792
+    (64-bit keys sorted). Both must give the oracle's keys, lists, tile ranges and images."""
+    from tdgs_amd.host import look_at_camera
+    w = synthetic.config(0, n=4000)
+    cam = look_at_camera(width, 2056, 60.0, (0.0, 0.0, -4.0))
+    t = host.Tiling.for_camera(cam, 8, 8)
+    assert (t.nb_tiles <= 65535) == (width == 2040)
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.1, 0.2, 0.3))
+    r = oracle.render(w.gaussians, cam, t, opts)
+    out, buf = _gpu_render(gpu, w.gaussians, cam, t, opts, depth=False)
+    assert r["nb_keys"] > 10_000 and r["sorted_keys"].max() >> 32 > 60_000
+    _assert_forward_equal(r, out, buf)
+
+
 def test_render_large_footprints_bit_exact(gpu, oracle):
     """Gaussians covering tens of tiles each (M > 32 N_f): tiles_end then comes from the tile
     rectangles (difference array) instead of the sorted keys; it must be the same."""

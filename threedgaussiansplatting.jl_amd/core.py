@@ -56,6 +56,7 @@ def lib():
         L.tdgs_sort_pairs.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_void_p, C.c_int32, C.c_int32, C.c_void_p]
         L.tdgs_tile_ranges.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_int32, C.c_void_p]
+        L.tdgs_render_sorted_keys.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64]
         L.tdgs_fill_fgidx_to_gidx.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
                                               C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
         L.tdgs_scan_counts.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
@@ -230,8 +231,20 @@ class RenderBuffers:
         self.nb_fgaussians = 0
         self.nb_keys = 0
         self.key_capacity = 0
-        self.keys = self.values = self.sorted_keys = self.sorted_values = None
+        self.keys = self.values = self._sorted_keys = self.sorted_values = None
+        self._keys_pending = None   # the C tiling of a render whose keys are not assembled yet
         self._alloc_keys(key_capacity if key_capacity is not None else 8 * cap)
+
+    @property
+    def sorted_keys(self):
+        """The sorted 64-bit keys of the last render (int64, key_capacity entries, the first
+        nb_keys valid). The render sorts 16-bit tile ids when the tiling has at most 65535 tiles;
+        the keys are then assembled here on first access (on the current stream)."""
+        if self._keys_pending:
+            check(lib().tdgs_render_sorted_keys(stream_ptr(self.device.index), C.byref(self._keys_pending),
+                                                C.byref(self.struct()), self.nb_keys))
+            self._keys_pending = None
+        return self._sorted_keys
 
     def _alloc_keys(self, key_capacity):
         d = self.device
@@ -239,7 +252,7 @@ class RenderBuffers:
         self.key_capacity = kc
         self.keys = torch.empty(kc, dtype=torch.int64, device=d)
         self.values = torch.empty(kc, dtype=torch.int32, device=d)
-        self.sorted_keys = torch.empty(kc, dtype=torch.int64, device=d)
+        self._sorted_keys = torch.empty(kc, dtype=torch.int64, device=d)
         self.sorted_values = torch.empty(kc, dtype=torch.int32, device=d)
         tb = lib().tdgs_render_temp_bytes(self.capacity, kc, C.byref(self.tiling.to_c()))
         self.temp = torch.empty(int(tb), dtype=torch.uint8, device=d)
@@ -260,7 +273,7 @@ class RenderBuffers:
         b.counts = dptr(self.counts)
         b.keys = dptr(self.keys)
         b.values = dptr(self.values)
-        b.sorted_keys = dptr(self.sorted_keys)
+        b.sorted_keys = dptr(self._sorted_keys)
         b.sorted_values = dptr(self.sorted_values)
         b.tiles_end = dptr(self.tiles_end)
         b.temp = dptr(self.temp)
@@ -293,6 +306,7 @@ def render_(outputs: RenderOutputs, gaussians, camera: PinholeCamera, tiling: Ti
         break
     buffers.nb_fgaussians = int(nbf.value)
     buffers.nb_keys = int(m.value)
+    buffers._keys_pending = t if buffers.nb_keys > 0 else None
     return outputs
 
 

@@ -11,15 +11,20 @@
 //                                                 depth key
 //   4. stable sort of (depth bits, fgidx)         radix, bits [0, 32)
 //   5. scan of tile counts in depth order -> M    scan (SortedCounts)
-//   6. key emission in depth order                k_emit_depth_order
-//   7. stable sort by tile                        radix, key bits [32, end_bit)
+//   6. key emission in depth order                k_emit_depth_order (16-bit tile ids when
+//                                                 the tiling has at most 65535 tiles, else
+//                                                 64-bit keys)
+//   7. stable sort by tile                        radix on the tile bits
 //   8. tile ranges                                k_tile_ranges
 //   9. blending                                   k_render_tiles
 // Steps 4-7 give exactly CUB's result on the reference's emission order: a Gaussian emits at
 // most one key per tile, so the reference's stable sort by (tile, depth bits) breaks ties by
 // ascending fgidx, i.e. it orders keys by (tile, depth bits, fgidx). Sorting the Gaussians by
 // (depth bits, fgidx) first and then stably by tile yields that same total order while
-// sorting only the tile bits of the M duplicated keys (2 passes instead of 6).
+// sorting only the tile bits of the M duplicated keys (2 passes instead of 6). Since the
+// depth order is already in place, the tile sort needs only the tile ids: it moves 6 bytes
+// per key instead of 12, and the 64-bit keys are assembled only on request
+// (tdgs_render_sorted_keys).
 #include "internal.hpp"
 #include "scan.hpp"
 #include "sort.hpp"
@@ -328,7 +333,8 @@ constexpr int kEmitThreads = 256;
 constexpr int kEmitItems = 16;
 constexpr int kEmitTile = kEmitThreads * kEmitItems;
 static_assert((kKeepSub & (kKeepSub - 1)) == 0, "power of two");
-static_assert(kEmitTile == RsTile<uint64_t>::kTile, "one emission workgroup fills one radix count tile");
+static_assert(kEmitTile == RsTile<uint64_t>::kTile && kEmitTile == RsTile<uint16_t>::kTile,
+              "one emission workgroup fills one radix count tile");
 
 __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, int64_t x) {
     int64_t lo = 0, hi = n;  // first index with a[i] > x
@@ -340,12 +346,16 @@ __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, 
 }
 
 // sorted_f holds the nb non-empty Gaussians in depth order and cs the inclusive scan of
-// their tile counts. The kernel also counts the digit of the first tile-sort pass (key bits
-// [32, 32 + nbits0)) of its keys, which form one radix count tile: counts0[d][blockIdx.x].
+// their tile counts. The kernel also counts the digit of the first tile-sort pass (the low
+// nbits0 bits of the tile id) of its keys, which form one radix count tile:
+// counts0[d][blockIdx.x]. TILE16 writes only the tile id of each key (uint16_t): the keys
+// already are in depth order, so the stable sort by tile needs no depth bits, and the full
+// keys are assembled on request (k_assemble_keys).
+template <bool TILE16>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
     const float* __restrict__ depths, const int32_t* __restrict__ ranges, int32_t ntx,
-    int64_t* __restrict__ keys, int32_t* __restrict__ vals, int nbits0, uint32_t* __restrict__ counts0,
+    void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0, uint32_t* __restrict__ counts0,
     int64_t count_tiles) {
     __shared__ int32_t s_cs[kEmitTile + 1];
     __shared__ int64_t s_range[2];
@@ -393,7 +403,10 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
         const int32_t ty = r.y + local / wx;
         const int32_t tx = r.x + local % wx;
         const int32_t tile = tx + (ty - 1) * ntx;
-        keys[d] = ((int64_t)tile << 32) | (int64_t)float_bits(depths[f - 1]);
+        if (TILE16)
+            static_cast<uint16_t*>(keys_out)[d] = (uint16_t)tile;
+        else
+            static_cast<int64_t*>(keys_out)[d] = ((int64_t)tile << 32) | (int64_t)float_bits(depths[f - 1]);
         vals[d] = f;
         digit = (uint32_t)tile & mask0;
         }
@@ -428,25 +441,41 @@ __global__ __launch_bounds__(256) void k_emit_keys(int64_t nbf, const float* __r
     }
 }
 
+// Tile id of sorted entry i: the high word of a 64-bit key, or a 16-bit tile id.
+__device__ __forceinline__ int32_t tile_of(const int64_t* sk, int64_t i) { return (int32_t)(sk[i] >> 32); }
+__device__ __forceinline__ int32_t tile_of(const uint16_t* st, int64_t i) { return st[i]; }
+
 // fill_tiles_end_sdfgidx_kernel! (forward_core.jl:676-734). Tile ids are clamped to
 // [1, nb_tiles] so that a malformed key cannot write out of bounds.
-__global__ __launch_bounds__(256) void k_tile_ranges(int64_t m, const int64_t* __restrict__ sk,
-                                                     int32_t nb_tiles, int32_t* __restrict__ te) {
+template <class K>
+__global__ __launch_bounds__(256) void k_tile_ranges(int64_t m, const K* __restrict__ sk, int32_t nb_tiles,
+                                                     int32_t* __restrict__ te) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= m) return;
-    const int32_t cur = (int32_t)(sk[i] >> 32);
+    const int32_t cur = tile_of(sk, i);
     if (i == 0) {
         const int32_t stop = cur < nb_tiles + 1 ? cur : nb_tiles + 1;
         for (int32_t t = 1; t < stop; ++t) te[t - 1] = 0;
     }
     int32_t lo = cur < 1 ? 1 : cur;
     if (i + 1 < m) {
-        int32_t nxt = (int32_t)(sk[i + 1] >> 32);
+        int32_t nxt = tile_of(sk, i + 1);
         if (nxt > nb_tiles + 1) nxt = nb_tiles + 1;
         for (int32_t t = lo; t < nxt; ++t) te[t - 1] = (int32_t)(i + 1);
     } else {
         for (int32_t t = lo; t <= nb_tiles; ++t) te[t - 1] = (int32_t)m;
     }
+}
+
+// The 64-bit sorted keys (tile << 32 | depth bits of the Gaussian) from the 16-bit sorted
+// tile ids and the sorted values.
+__global__ __launch_bounds__(256) void k_assemble_keys(int64_t m, const uint16_t* __restrict__ st,
+                                                       const int32_t* __restrict__ sv,
+                                                       const float* __restrict__ depths,
+                                                       int64_t* __restrict__ sk) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    sk[i] = ((int64_t)st[i] << 32) | (int64_t)float_bits(depths[sv[i] - 1]);
 }
 
 // tiles_end from the tile-coverage difference array D ((ntx+1) x (nty+1), 0-based corners).
@@ -852,8 +881,20 @@ int tdgs_tile_ranges(void* stream, int64_t nb_keys, const int64_t* sorted_keys, 
     TDGS_REQUIRE(nb_keys >= 0 && nb_tiles > 0 && tiles_end, "bad arguments");
     if (nb_keys == 0) return TDGS_OK;
     TDGS_REQUIRE(sorted_keys, "null keys");
-    k_tile_ranges<<<(unsigned)ceil_div(nb_keys, 256), 256, 0, (hipStream_t)stream>>>(nb_keys, sorted_keys,
-                                                                                      nb_tiles, tiles_end);
+    k_tile_ranges<int64_t><<<(unsigned)ceil_div(nb_keys, 256), 256, 0, (hipStream_t)stream>>>(nb_keys, sorted_keys,
+                                                                                               nb_tiles, tiles_end);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+int tdgs_render_sorted_keys(void* stream, const tdgs_tiling* tiling, const tdgs_render_buffers* buf,
+                            int64_t nb_keys) {
+    TDGS_REQUIRE(tiling && tiling->nb_tiles_x > 0 && tiling->nb_tiles_y > 0, "bad tiling");
+    TDGS_REQUIRE(buf && nb_keys >= 0 && nb_keys <= buf->key_capacity, "bad buffers or key count");
+    if (nb_keys == 0 || (int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y > 65535) return TDGS_OK;
+    TDGS_REQUIRE(buf->keys && buf->sorted_values && buf->sorted_keys && buf->depths, "null buffers");
+    k_assemble_keys<<<(unsigned)ceil_div(nb_keys, 256), 256, 0, (hipStream_t)stream>>>(
+        nb_keys, reinterpret_cast<const uint16_t*>(buf->keys), buf->sorted_values, buf->depths, buf->sorted_keys);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
@@ -990,32 +1031,53 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         set_error("key buffers hold %lld keys, %lld needed", (long long)buf->key_capacity, (long long)m);
         return TDGS_ERR_CAPACITY;
     }
-    // 6-7: emit in depth order, then stable sort on the tile bits. The first radix pass
-    // writes sorted_* when the pass count is odd, keys/values when even; emit into the other.
+    // 6-7: emit in depth order, then stable sort on the tile bits. With at most 65535 tiles
+    // the sort moves 16-bit tile ids (two arrays carved from buf->keys) and the values; the
+    // 64-bit keys are assembled after it. The first radix pass writes the output arrays when
+    // the pass count is odd and the alternate ones when even; emit into the other.
     const int eb = end_bit_of(tiling);
-    const int passes = radix_passes(32, eb);
-    const bool emit_into_sorted = (passes % 2) == 0;
-    int64_t* ek = emit_into_sorted ? buf->sorted_keys : buf->keys;
-    int32_t* ev2 = emit_into_sorted ? buf->sorted_values : buf->values;
+    const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
+    const bool tile16 = nb_tiles <= 65535;
+    const int tb = tile16 ? 0 : 32;   // first tile bit of the sorted key
+    const int te_bit = tile16 ? eb - 32 : eb;
+    const int passes = radix_passes(tb, te_bit);
+    const bool emit_into_out = (passes % 2) == 0;
+    uint16_t* t16_out = reinterpret_cast<uint16_t*>(buf->keys);
+    uint16_t* t16_alt = t16_out + buf->key_capacity;
+    void* ek = tile16 ? (void*)(emit_into_out ? t16_out : t16_alt)
+                      : (void*)(emit_into_out ? buf->sorted_keys : buf->keys);
+    int32_t* ev2 = emit_into_out ? buf->sorted_values : buf->values;
+    const int64_t count_tiles = tile16 ? radix_tiles<uint16_t>(m) : radix_tiles<uint64_t>(m);
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
-        const int nbits0 = radix_digit_bits(32, eb);   // digit of the first tile-sort pass
-        k_emit_depth_order<<<(unsigned)ceil_div(m, kEmitTile), kEmitThreads, 0, s>>>(
-            nb, m, sorted_f, cs, buf->depths, buf->tile_ranges, tiling->nb_tiles_x, ek, ev2, nbits0,
-            radix_count_table(rtemp), radix_tiles<uint64_t>(m));
+        const int nbits0 = radix_digit_bits(tb, te_bit);   // digit of the first tile-sort pass
+        const unsigned grid = (unsigned)ceil_div(m, kEmitTile);
+        if (tile16)
+            k_emit_depth_order<true><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, buf->depths, buf->tile_ranges,
+                                                                  tiling->nb_tiles_x, ek, ev2, nbits0,
+                                                                  radix_count_table(rtemp), count_tiles);
+        else
+            k_emit_depth_order<false><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, buf->depths, buf->tile_ranges,
+                                                                   tiling->nb_tiles_x, ek, ev2, nbits0,
+                                                                   radix_count_table(rtemp), count_tiles);
         TDGS_LAUNCHED();
     }
     {
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
-        TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
-                                            buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, 32, eb,
-                                            rtemp, rbytes, s, radix_count_table(rtemp)));
+        if (tile16)
+            TDGS_TRY(radix_sort_pairs<uint16_t>((const uint16_t*)ek, t16_out, ev2, buf->sorted_values, t16_alt,
+                                                buf->values, m, tb, te_bit, rtemp, rbytes, s,
+                                                radix_count_table(rtemp)));
+        else
+            TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
+                                                buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, tb,
+                                                te_bit, rtemp, rbytes, s, radix_count_table(rtemp)));
     }
     // 8: tile ranges
-    const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
     {
         StageScope sc(TDGS_STAGE_TILE_RANGES, s);
-        if (m > kRectKeysPerGaussian * nbf) {
+        const bool rects = m > kRectKeysPerGaussian * nbf;
+        if (rects) {
             k_fill_i32<<<(unsigned)ceil_div(kRectCopies * ndiff, 256), 256, 0, s>>>(rect_diff, kRectCopies * ndiff, 0);
             TDGS_LAUNCHED();
             k_rect_diff<<<(unsigned)ceil_div(nbf, 256), 256, 0, s>>>(nbf, buf->counts, buf->tile_ranges,
@@ -1025,9 +1087,11 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
             TDGS_LAUNCHED();
             k_tiles_end_from_rects<<<(unsigned)tiling->nb_tiles_y, kTeThreads, 0, s>>>(
                 rect_diff, tiling->nb_tiles_x, buf->tiles_end);
-        } else {
-            k_tile_ranges<<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles, buf->tiles_end);
-        }
+        } else if (tile16)
+            k_tile_ranges<uint16_t><<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, t16_out, nb_tiles, buf->tiles_end);
+        else
+            k_tile_ranges<int64_t><<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles,
+                                                                             buf->tiles_end);
         TDGS_LAUNCHED();
     }
     // 9: blending

@@ -84,7 +84,7 @@ __device__ __forceinline__ void tile_digit_histogram(const K* __restrict__ keys,
     }
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        const bool valid = base + (int64_t)k * kRsThreads < n && !(drop_max && key[k] == ~(K)0);
+        const bool valid = base + (int64_t)k * kRsThreads < n && !(drop_max && key[k] == (K)~(K)0);
         const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
         const uint64_t peers = match_digit(d, nbits, valid);
         if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&s_h[d], (uint32_t)__popcll(peers));
@@ -152,7 +152,10 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     int64_t* d_kept) {
     constexpr int kRsItems = RsTile<K>::kItems;
     constexpr int kRsTile = RsTile<K>::kTile;
-    __shared__ K s_buf[kRsTile];                 // the tile in digit order: keys, then values
+    // the tile in digit order: keys, then values (room for whichever is wider)
+    constexpr int kBufWords = kRsTile * (sizeof(K) > 4 ? (int)sizeof(K) : 4) / 4;
+    __shared__ uint32_t s_raw[kBufWords];
+    K* s_buf = reinterpret_cast<K*>(s_raw);
     __shared__ uint32_t s_wh[kRsWaves][kRsBins];  // per-wave digit counts -> offsets
     __shared__ uint32_t s_local[kRsBins];         // start of each digit inside the tile
     __shared__ int32_t s_delta[kRsBins];          // output index - tile-local index
@@ -186,7 +189,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     bool keep[kRsItems];
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        keep[k] = wbase + k * kWave < nn && !(drop_max && key[k] == ~(K)0);
+        keep[k] = wbase + k * kWave < nn && !(drop_max && key[k] == (K)~(K)0);
         const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
         const uint64_t peers = match_digit(d, nbits, keep[k]);
         const uint64_t below = peers & lanemask_lt();
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
         }
     }
     __syncthreads();
-    int32_t* s_val = reinterpret_cast<int32_t*>(s_buf);
+    int32_t* s_val = reinterpret_cast<int32_t*>(s_raw);
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
         if (keep[k] && pos[k] < (uint32_t)kRsTile) s_val[pos[k]] = val[k];
