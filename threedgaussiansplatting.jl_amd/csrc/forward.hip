@@ -585,6 +585,101 @@ struct BlendArgs {
     unsigned long long* evaluations;  // COUNT variant: [evaluations, live, contributing]
 };
 
+// The blending steps of one batch of nb staged records, written out instruction by instruction.
+// Per record it performs exactly the single-precision operations of the C++ loop in
+// k_render_tiles below (same operands, same order: the exponent's five fused multiply-adds,
+// exp_f_core's sequence, min with max_alpha, 1 - alpha, the products and the colour fused
+// multiply-adds), so every result is bit for bit the compiled loop's. What differs is the
+// bookkeeping: the lanes still blending (act), live, contributing and stopping lanes are
+// 64-bit lane masks combined with scalar instructions, the exponential is skipped (scalar
+// branch) when no lane is live, and the state update runs under exec = contributing and not
+// stopping lanes; the compiled loop needed about 30 scalar and 39 vector instructions per
+// live record against 10 and 32 here. Valid only when every live exponent lies in
+// [-87, 88] (the batch is not `checked`). v48-v62 are its scratch registers. Returns the
+// mask of the lanes that did not stop.
+template <bool DEPTH>
+__device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0, int32_t idx_end, float uu,
+                                                float vv, float uv, float cu, float cv, float e_cut,
+                                                float max_alpha, float min_alpha, float min_T, float& T,
+                                                float& C0, float& C1, float& C2, float& D, int32_t& last) {
+    const float c6 = 1.38888888888889e-3f;   // exp_f_core's coefficient of r^6 (a VGPR operand)
+    uint64_t act, live, ctb, stp, sav;
+    int32_t idx;
+#define TDGS_BLEND_ASM(DEPTH_FMA)                                                                  \
+    asm volatile(                                                                                  \
+        "s_and_b64 %[act], exec, exec\n"                                                           \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                \
+        "s_mov_b32 %[idx], %[i0]\n"                                                                \
+        "v_mov_b32 v62, %[addr]\n"                                                                 \
+        ".Lstep_%=:\n"                                                                             \
+        "ds_read_b128 v[48:51], v62\n"                                                             \
+        "ds_read_b128 v[52:55], v62 offset:16\n"                                                   \
+        "s_waitcnt lgkmcnt(0)\n"                                                                   \
+        "v_fma_f32 v58, v52, %[cv], v53\n"                                                         \
+        "v_fmac_f32 v58, v51, %[cu]\n"                                                             \
+        "v_fmac_f32 v58, v50, %[uv]\n"                                                             \
+        "v_fmac_f32 v58, v49, %[vv]\n"                                                             \
+        "v_fmac_f32 v58, v48, %[uu]\n"                                                             \
+        "v_cmp_ngt_f32 vcc, %[cut], v58\n"                                                         \
+        "s_and_b64 %[live], vcc, %[act]\n"                                                         \
+        "s_cbranch_scc0 .Lnext_%=\n"                                                               \
+        "v_mul_f32 v59, 0x3fb8aa3b, v58\n"                                                         \
+        "v_rndne_f32 v59, v59\n"                                                                   \
+        "v_fmac_f32 v58, 0xbf317200, v59\n"                                                        \
+        "v_fmac_f32 v58, 0xb5bfbe8e, v59\n"                                                        \
+        "v_fmamk_f32 v60, v58, 0x39500d01, %[c6]\n"                                                \
+        "v_fmaak_f32 v60, v60, v58, 0x3c088889\n"                                                  \
+        "v_fmaak_f32 v60, v60, v58, 0x3d2aaaab\n"                                                  \
+        "v_fmaak_f32 v60, v60, v58, 0x3e2aaaab\n"                                                  \
+        "v_fma_f32 v60, v60, v58, 0.5\n"                                                           \
+        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
+        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
+        "v_cvt_i32_f32 v59, v59\n"                                                                 \
+        "v_lshl_add_u32 v59, v59, 23, 1.0\n"                                                       \
+        "v_mul_f32 v60, v60, v59\n"                                                                \
+        "v_min_f32 v60, %[maxa], v60\n"                                                            \
+        "v_cmp_ngt_f32 vcc, %[mina], v60\n"                                                        \
+        "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
+        "v_sub_f32 v61, 1.0, v60\n"                                                                \
+        "v_mul_f32 v61, %[T], v61\n"                                                               \
+        "v_cmp_gt_f32 vcc, %[minT], v61\n"                                                         \
+        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                          \
+        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                     \
+        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                      \
+        "ds_read_b64 v[56:57], v62 offset:32\n"                                                    \
+        "v_mul_f32 v59, %[T], v60\n"                                                               \
+        "v_fmac_f32 %[C0], v59, v54\n"                                                             \
+        "v_fmac_f32 %[C1], v59, v55\n"                                                             \
+        "s_waitcnt lgkmcnt(0)\n"                                                                   \
+        "v_fmac_f32 %[C2], v59, v56\n"                                                             \
+        DEPTH_FMA                                                                                  \
+        "v_mov_b32 %[T], v61\n"                                                                    \
+        "v_mov_b32 %[last], %[idx]\n"                                                              \
+        "s_mov_b64 exec, %[sav]\n"                                                                 \
+        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                \
+        ".Lnext_%=:\n"                                                                             \
+        "v_add_u32 v62, 48, v62\n"                                                                 \
+        "s_add_u32 %[idx], %[idx], 1\n"                                                            \
+        "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
+        "s_cbranch_scc1 .Lstep_%=\n"                                                               \
+        ".Lend_%=:\n"                                                                              \
+        : [act] "=&s"(act), [live] "=&s"(live), [ctb] "=&s"(ctb), [stp] "=&s"(stp), [sav] "=&s"(sav), \
+          [idx] "=&s"(idx), [T] "+v"(T), [C0] "+v"(C0), [C1] "+v"(C1), [C2] "+v"(C2), [D] "+v"(D),   \
+          [last] "+v"(last)                                                                         \
+        : [addr] "v"(lds_addr), [i0] "s"(idx0), [iend] "s"(idx_end), [uu] "v"(uu), [vv] "v"(vv),     \
+          [uv] "v"(uv), [cu] "v"(cu), [cv] "v"(cv), [c6] "v"(c6), [cut] "s"(e_cut),                  \
+          [maxa] "s"(max_alpha), [mina] "s"(min_alpha), [minT] "s"(min_T)                           \
+        : "v48", "v49", "v50", "v51", "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60",  \
+          "v61", "v62", "vcc", "scc", "memory")
+    if constexpr (DEPTH)
+        TDGS_BLEND_ASM("v_fmac_f32 %[D], v59, v57\n");
+    else
+        TDGS_BLEND_ASM("");
+#undef TDGS_BLEND_ASM
+    return act;
+}
+
 // One workgroup per tile, one thread per pixel (tile_pixel). Each batch of TW*TH sorted
 // entries is converted to blending parameters once per tile and staged in LDS, where every
 // lane reads the same record (broadcast). A wavefront skips an entry when no pixel it still
@@ -634,7 +729,15 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
         // batch is huge (or NaN), that is inside [-87, 88], where exp_f is its polynomial core.
         const bool checked = __syncthreads_or(big) || a.cut_low;
         const int nb = (int)((end - base) < NT ? (end - base) : NT);
-        if (!done) {
+        if (!COUNT && !checked) {
+            if (!done) {
+                const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) BlendRec*)s_rec;
+                const uint64_t act = blend_batch<DEPTH>(lds, (int32_t)(base + 1), (int32_t)(base + nb + 1), uu,
+                                                        vv, uv, cu, cv, a.e_cut, a.max_alpha, a.min_alpha,
+                                                        a.min_T, T, C0, C1, C2, D, last);
+                done = ((act >> __lane_id()) & 1ull) == 0;
+            }
+        } else if (!done) {
             for (int j = 0; j < nb; ++j) {
                 if (COUNT && !done) ++evals;
                 const float4 ra = s_rec[j].a;
