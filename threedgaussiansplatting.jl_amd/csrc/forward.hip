@@ -323,12 +323,25 @@ struct SortedCounts {
     }
 };
 
-// Load-balanced key emission in depth order: one thread per output key. Each workgroup owns
-// kEmitTile consecutive keys; it finds the Gaussians (depth order) that produce them by two
-// binary searches on the inclusive count scan, stages their scan values in LDS, and every
-// key then finds its Gaussian by a binary search in LDS. Writes are fully coalesced. Within
-// a Gaussian, key number `local` is tile (x0 + local % wx, y0 + local / wx): tiles row-major,
-// x fastest, as the reference emits them (forward_core.jl:577-597).
+// The inclusive scan of the tile counts in depth order, and for every emission block (keys
+// [b kEmitTile, (b + 1) kEmitTile)) the Gaussian that owns its first key: the one whose keys
+// [incl - count, incl) contain b kEmitTile.
+struct WriteScanAndBlocks {
+    int32_t* cs;
+    int32_t* blk_first;
+    int64_t nblk;   // entries of blk_first (blocks past it, for keys beyond the key capacity, are not recorded)
+    __device__ void operator()(int64_t j, int64_t incl, int32_t count) const;
+};
+
+// Key emission in depth order. Each workgroup owns kEmitTile consecutive keys; the count scan
+// recorded the Gaussian (depth order) that owns the first key of every block, which bounds
+// the span of Gaussians producing them, and the workgroup stages their scan values in LDS.
+// Thread t then produces the kEmitItems consecutive keys d0 + kEmitItems t, ...: one binary
+// search in LDS for the first, then a walk that moves to the next Gaussian when the key
+// passes its end and steps the tile (x fastest) without a division. Within a Gaussian, key
+// number `local` is tile (x0 + local % wx, y0 + local / wx): tiles row-major, x fastest, as
+// the reference emits them (forward_core.jl:577-597). The keys go through LDS (a rotated
+// layout without bank conflicts) to fully coalesced stores.
 constexpr int kEmitThreads = 256;
 constexpr int kEmitItems = 16;
 constexpr int kEmitTile = kEmitThreads * kEmitItems;
@@ -336,13 +349,10 @@ static_assert((kKeepSub & (kKeepSub - 1)) == 0, "power of two");
 static_assert(kEmitTile == RsTile<uint64_t>::kTile && kEmitTile == RsTile<uint16_t>::kTile,
               "one emission workgroup fills one radix count tile");
 
-__device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, int64_t x) {
-    int64_t lo = 0, hi = n;  // first index with a[i] > x
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        if ((int64_t)a[mid] > x) hi = mid; else lo = mid + 1;
-    }
-    return lo;
+__device__ void WriteScanAndBlocks::operator()(int64_t j, int64_t incl, int32_t count) const {
+    cs[j] = (int32_t)incl;
+    for (int64_t b = (incl - count + kEmitTile - 1) / kEmitTile; b * kEmitTile < incl && b < nblk; ++b)
+        blk_first[b] = (int32_t)j;
 }
 
 // sorted_f holds the nb non-empty Gaussians in depth order and cs the inclusive scan of
@@ -351,70 +361,157 @@ __device__ __forceinline__ int64_t upper_bound_i32(const int32_t* a, int64_t n, 
 // counts0[d][blockIdx.x]. TILE16 writes only the tile id of each key (uint16_t): the keys
 // already are in depth order, so the stable sort by tile needs no depth bits, and the full
 // keys are assembled on request (k_assemble_keys).
+//
+// When the block's keys come from at most kEmitStage Gaussians, their fgidx, first tile id
+// and rectangle width are staged in LDS too (in the part of the scan buffer that a span of
+// that size leaves free); otherwise the walk reads them from global memory.
+constexpr int kEmitStage = 1024;
+static_assert(kEmitStage + 1 + 3 * kEmitStage <= kEmitTile + 1, "staging fits the scan buffer");
+
+// Slot of key k (0 <= k < kEmitTile) of the block in the LDS transpose: thread k / kEmitItems
+// writes its item k % kEmitItems rotated by the thread index, so that the 64 lanes of a
+// wavefront writing item i, and the 64 lanes reading consecutive keys, spread over the banks.
+__device__ __forceinline__ int emit_slot(int k) {
+    const int t = k / kEmitItems, i = k % kEmitItems;
+    return t * kEmitItems + ((i + t) & (kEmitItems - 1));
+}
+
 template <bool TILE16>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
-    const float* __restrict__ depths, const int32_t* __restrict__ ranges, int32_t ntx,
-    void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0, uint32_t* __restrict__ counts0,
-    int64_t count_tiles) {
-    __shared__ int32_t s_cs[kEmitTile + 1];
+    const int32_t* __restrict__ blk_first, const float* __restrict__ depths, const int32_t* __restrict__ ranges,
+    int32_t ntx, void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0,
+    uint32_t* __restrict__ counts0, int64_t count_tiles) {
+    __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
     __shared__ uint32_t s_h[kRsBins];
-    s_h[threadIdx.x] = 0;
+    int32_t* const s_cs = s_buf;                      // [0, cnt]: scan values of the span
+    int32_t* const s_f = s_buf + kEmitStage + 1;      // staged Gaussians: fgidx,
+    int32_t* const s_t0 = s_f + kEmitStage;           // tile id of the rectangle's first tile,
+    int32_t* const s_wx = s_t0 + kEmitStage;          // rectangle width in tiles
+    const int t = threadIdx.x;
+    s_h[t] = 0;
     const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
-    const int64_t d1 = (d0 + kEmitTile < m ? d0 + kEmitTile : m) - 1;  // last key of the block
-    if (threadIdx.x < 2) s_range[threadIdx.x] = upper_bound_i32(cs, nb, threadIdx.x == 0 ? d0 : d1);
+    // Gaussians owning the block's first and last keys: from the block table of the count scan
+    // (the next block's first Gaussian, or the one before it when that one starts exactly at
+    // the next block), clamped to [0, nb)
+    if (t == 0) s_range[0] = blk_first[blockIdx.x];
+    if (t == 1) {
+        const int64_t dn = d0 + kEmitTile;
+        int64_t jh = nb - 1;
+        if (dn < m) {
+            const int64_t jn = blk_first[blockIdx.x + 1];
+            const int64_t sn = jn <= 0 ? 0 : cs[jn - 1];
+            jh = sn < dn ? jn : jn - 1;
+        }
+        s_range[1] = jh;
+    }
     __syncthreads();
-    const int64_t j_lo = s_range[0];
-    const int64_t j_hi = s_range[1] < nb ? s_range[1] : nb - 1;
+    int64_t j_lo = s_range[0];
+    int64_t j_hi = s_range[1];
+    if (j_hi > nb - 1) j_hi = nb - 1;
+    if (j_lo < 0) j_lo = 0;
+    if (j_lo > j_hi) j_lo = j_hi;
     const int64_t cnt = j_hi - j_lo + 1;  // Gaussians spanned (each owns >= 1 key here)
-    const bool staged = cnt <= kEmitTile;
+    const bool staged = cnt <= kEmitTile; // always, with consistent counts
+    const bool full = cnt <= kEmitStage;
     if (staged) {
-        for (int64_t k = threadIdx.x; k <= cnt; k += kEmitThreads) {
+        for (int64_t k = t; k <= cnt; k += kEmitThreads) {
             const int64_t j = j_lo + k - 1;
             s_cs[k] = j < 0 ? 0 : cs[j];
-        }
-    }
-    __syncthreads();
-    const uint32_t mask0 = (1u << nbits0) - 1u;
-#pragma unroll 2
-    for (int it = 0; it < kEmitItems; ++it) {
-        const int64_t d = d0 + (int64_t)it * kEmitThreads + threadIdx.x;
-        const bool valid = d < m;
-        uint32_t digit = 0;
-        if (valid) {
-        int64_t j, start;
-        if (staged) {
-            int lo = 0, hi = (int)cnt;  // largest jj in [0, cnt) with s_cs[jj] <= d
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if ((int64_t)s_cs[mid] <= d) lo = mid; else hi = mid;
+            if (full && k < cnt) {
+                const int32_t f = sorted_f[j + 1];
+                const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
+                s_f[k] = f;
+                s_t0[k] = r.x + (r.y - 1) * ntx;
+                s_wx[k] = r.z - r.x + 1;
             }
-            j = j_lo + lo;
-            start = s_cs[lo];
-        } else {
-            j = upper_bound_i32(cs, nb, d);
-            start = j == 0 ? 0 : cs[j - 1];
         }
-        const int32_t f = sorted_f[j];
-        const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
-        const int32_t wx = r.z - r.x + 1;
-        const int32_t local = (int32_t)(d - start);
-        const int32_t ty = r.y + local / wx;
-        const int32_t tx = r.x + local % wx;
-        const int32_t tile = tx + (ty - 1) * ntx;
-        if (TILE16)
-            static_cast<uint16_t*>(keys_out)[d] = (uint16_t)tile;
-        else
-            static_cast<int64_t*>(keys_out)[d] = ((int64_t)tile << 32) | (int64_t)float_bits(depths[f - 1]);
-        vals[d] = f;
-        digit = (uint32_t)tile & mask0;
-        }
-        const uint64_t peers = match_digit(digit, nbits0, valid);
-        if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&s_h[digit], (uint32_t)__popcll(peers));
     }
     __syncthreads();
-    counts0[(int64_t)threadIdx.x * count_tiles + blockIdx.x] = s_h[threadIdx.x];
+    // scan value before span entry k (k <= cnt): the first key of Gaussian j_lo + k
+    auto start_of = [&](int64_t k) -> int64_t {
+        if (staged) return s_cs[k];
+        const int64_t j = j_lo + k - 1;
+        return j < 0 ? 0 : cs[j];
+    };
+    int32_t tile[kEmitItems], val[kEmitItems];
+    const int64_t first = d0 + (int64_t)t * kEmitItems;
+    if (first < m) {
+        int64_t lo = 0, hi = cnt;   // largest k in [0, cnt) with start_of(k) <= first
+        while (hi - lo > 1) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (start_of(mid) <= first) lo = mid; else hi = mid;
+        }
+        int64_t nxt = start_of(lo + 1);
+        int32_t f, t0, wx;
+        auto load = [&](int64_t k) {
+            if (full) {
+                f = s_f[k]; t0 = s_t0[k]; wx = s_wx[k];
+            } else {
+                f = sorted_f[j_lo + k];
+                const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
+                t0 = r.x + (r.y - 1) * ntx;
+                wx = r.z - r.x + 1;
+            }
+        };
+        load(lo);
+        const int32_t local = (int32_t)(first - start_of(lo));
+        int32_t q = local / wx, rx = local - q * wx;
+#pragma unroll
+        for (int i = 0; i < kEmitItems; ++i) {
+            const int64_t d = first + i;
+            if (d >= nxt && lo + 1 < cnt) {   // next Gaussian (each owns >= 1 key)
+                ++lo;
+                nxt = start_of(lo + 1);
+                load(lo);
+                q = 0;
+                rx = 0;
+            }
+            tile[i] = t0 + q * ntx + rx;
+            val[i] = f;
+            if (++rx == wx) {
+                rx = 0;
+                ++q;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kEmitItems; ++i) tile[i] = val[i] = 0;
+    }
+    // values, then tile ids (or keys), through LDS to coalesced stores
+    const int64_t nk = m - d0 < kEmitTile ? m - d0 : kEmitTile;
+    const uint32_t mask0 = (1u << nbits0) - 1u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kEmitItems; ++i) s_buf[t * kEmitItems + ((i + t) & (kEmitItems - 1))] = val[i];
+    __syncthreads();
+    int32_t fv[kEmitItems];   // the value of key t + kEmitThreads i (the 64-bit keys need it)
+#pragma unroll
+    for (int i = 0; i < kEmitItems; ++i) {
+        const int k = t + kEmitThreads * i;
+        fv[i] = s_buf[emit_slot(k)];
+        if (k < nk) vals[d0 + k] = fv[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kEmitItems; ++i) s_buf[t * kEmitItems + ((i + t) & (kEmitItems - 1))] = tile[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kEmitItems; ++i) {
+        const int k = t + kEmitThreads * i;
+        if (k < nk) {
+            const int32_t tl = s_buf[emit_slot(k)];
+            if (TILE16)
+                static_cast<uint16_t*>(keys_out)[d0 + k] = (uint16_t)tl;
+            else
+                static_cast<int64_t*>(keys_out)[d0 + k] = ((int64_t)tl << 32) |
+                                                          (int64_t)float_bits(depths[fv[i] - 1]);
+            atomicAdd(&s_h[(uint32_t)tl & mask0], 1u);
+        }
+    }
+    __syncthreads();
+    counts0[(int64_t)t * count_tiles + blockIdx.x] = s_h[t];
 }
 
 // fill_df2dgs_codes_and_dfgidx_to_fgidx_kernel! (forward_core.jl:531-603): reference
@@ -889,6 +986,7 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     const int64_t big = cap > key_cap ? cap : key_cap;
     ar.template take<char>((int64_t)radix_temp_bytes(big));
     ar.template take<int32_t>(kRectCopies * rect_diff_size(t));   // tile-coverage difference arrays
+    ar.template take<int32_t>(ceil_div(key_cap, kEmitTile) + 2);  // first Gaussian of each emission block
 }
 
 }  // namespace tdgs
@@ -1076,6 +1174,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     void* rtemp = ar.take<char>((int64_t)rbytes);
     const int64_t ndiff = rect_diff_size(tiling);
     int32_t* rect_diff = ar.take<int32_t>(kRectCopies * ndiff);
+    const int64_t nblk = ceil_div(buf->key_capacity, kEmitTile) + 2;
+    int32_t* blk_first = ar.take<int32_t>(nblk);
     int64_t* d_nbf = ctx->d_counters;
     int64_t* d_m = ctx->d_counters + 1;
 
@@ -1116,8 +1216,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     {
         StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
         TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nb},
-                             SortedCounts{sorted_f, buf->counts, d_nb}, WriteInclusiveI32{cs}, n, stemp, sbytes,
-                             d_m, s));
+                             SortedCounts{sorted_f, buf->counts, d_nb}, WriteScanAndBlocks{cs, blk_first, nblk}, n, stemp,
+                             sbytes, d_m, s));
     }
     TDGS_TRY(read_counters(ctx, s, 5));
     const int64_t nbf = ctx->h_counters[0];
@@ -1156,13 +1256,13 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         const int nbits0 = radix_digit_bits(tb, te_bit);   // digit of the first tile-sort pass
         const unsigned grid = (unsigned)ceil_div(m, kEmitTile);
         if (tile16)
-            k_emit_depth_order<true><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, buf->depths, buf->tile_ranges,
-                                                                  tiling->nb_tiles_x, ek, ev2, nbits0,
-                                                                  radix_count_table(rtemp), count_tiles);
+            k_emit_depth_order<true><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->depths,
+                                                                  buf->tile_ranges, tiling->nb_tiles_x, ek, ev2,
+                                                                  nbits0, radix_count_table(rtemp), count_tiles);
         else
-            k_emit_depth_order<false><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, buf->depths, buf->tile_ranges,
-                                                                   tiling->nb_tiles_x, ek, ev2, nbits0,
-                                                                   radix_count_table(rtemp), count_tiles);
+            k_emit_depth_order<false><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->depths,
+                                                                   buf->tile_ranges, tiling->nb_tiles_x, ek, ev2,
+                                                                   nbits0, radix_count_table(rtemp), count_tiles);
         TDGS_LAUNCHED();
     }
     {
