@@ -691,9 +691,12 @@ struct BlendArgs {
 // 64-bit lane masks combined with scalar instructions, the exponential is skipped (scalar
 // branch) when no lane is live, and the state update runs under exec = contributing and not
 // stopping lanes; the compiled loop needed about 30 scalar and 39 vector instructions per
-// live record against 10 and 32 here. Valid only when every live exponent lies in
-// [-87, 88] (the batch is not `checked`). v48-v62 are its scratch registers. Returns the
-// mask of the lanes that did not stop.
+// live record against 10 and 32 here. The next record's parameters are read from LDS into a
+// second register set while the current one is processed (the loop is unrolled twice), so the
+// read latency is hidden; the LDS array holds one record more than a batch for the read past
+// the last record. Valid only when every live exponent lies in [-87, 88] (the batch is not
+// `checked`). v48-v62 and v64-v71 are its scratch registers. Returns the mask of the lanes that
+// did not stop.
 template <bool DEPTH>
 __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0, int32_t idx_end, float uu,
                                                 float vv, float uv, float cu, float cv, float e_cut,
@@ -708,10 +711,12 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         "s_mov_b32 %[idx], %[i0]\n"                                                                \
         "v_mov_b32 v62, %[addr]\n"                                                                 \
-        ".Lstep_%=:\n"                                                                             \
         "ds_read_b128 v[48:51], v62\n"                                                             \
         "ds_read_b128 v[52:55], v62 offset:16\n"                                                   \
+        ".Lstep_%=:\n"                                                                             \
         "s_waitcnt lgkmcnt(0)\n"                                                                   \
+        "ds_read_b128 v[64:67], v62 offset:48\n"                                                   \
+        "ds_read_b128 v[68:71], v62 offset:64\n"                                                   \
         "v_fma_f32 v58, v52, %[cv], v53\n"                                                         \
         "v_fmac_f32 v58, v51, %[cu]\n"                                                             \
         "v_fmac_f32 v58, v50, %[uv]\n"                                                             \
@@ -719,7 +724,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 v58, v48, %[uu]\n"                                                             \
         "v_cmp_ngt_f32 vcc, %[cut], v58\n"                                                         \
         "s_and_b64 %[live], vcc, %[act]\n"                                                         \
-        "s_cbranch_scc0 .Lnext_%=\n"                                                               \
+        "s_cbranch_scc0 .Lnexta_%=\n"                                                              \
         "v_mul_f32 v59, 0x3fb8aa3b, v58\n"                                                         \
         "v_rndne_f32 v59, v59\n"                                                                   \
         "v_fmac_f32 v58, 0xbf317200, v59\n"                                                        \
@@ -749,18 +754,70 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 %[C1], v59, v55\n"                                                             \
         "s_waitcnt lgkmcnt(0)\n"                                                                   \
         "v_fmac_f32 %[C2], v59, v56\n"                                                             \
-        DEPTH_FMA                                                                                  \
+        DEPTH_FMA                                                                                   \
         "v_mov_b32 %[T], v61\n"                                                                    \
         "v_mov_b32 %[last], %[idx]\n"                                                              \
         "s_mov_b64 exec, %[sav]\n"                                                                 \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
-        ".Lnext_%=:\n"                                                                             \
+        ".Lnexta_%=:\n"                                                                            \
+        "v_add_u32 v62, 48, v62\n"                                                                 \
+        "s_add_u32 %[idx], %[idx], 1\n"                                                            \
+        "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                \
+        "s_waitcnt lgkmcnt(0)\n"                                                                   \
+        "ds_read_b128 v[48:51], v62 offset:48\n"                                                   \
+        "ds_read_b128 v[52:55], v62 offset:64\n"                                                   \
+        "v_fma_f32 v58, v68, %[cv], v69\n"                                                         \
+        "v_fmac_f32 v58, v67, %[cu]\n"                                                             \
+        "v_fmac_f32 v58, v66, %[uv]\n"                                                             \
+        "v_fmac_f32 v58, v65, %[vv]\n"                                                             \
+        "v_fmac_f32 v58, v64, %[uu]\n"                                                             \
+        "v_cmp_ngt_f32 vcc, %[cut], v58\n"                                                         \
+        "s_and_b64 %[live], vcc, %[act]\n"                                                         \
+        "s_cbranch_scc0 .Lnextb_%=\n"                                                              \
+        "v_mul_f32 v59, 0x3fb8aa3b, v58\n"                                                         \
+        "v_rndne_f32 v59, v59\n"                                                                   \
+        "v_fmac_f32 v58, 0xbf317200, v59\n"                                                        \
+        "v_fmac_f32 v58, 0xb5bfbe8e, v59\n"                                                        \
+        "v_fmamk_f32 v60, v58, 0x39500d01, %[c6]\n"                                                \
+        "v_fmaak_f32 v60, v60, v58, 0x3c088889\n"                                                  \
+        "v_fmaak_f32 v60, v60, v58, 0x3d2aaaab\n"                                                  \
+        "v_fmaak_f32 v60, v60, v58, 0x3e2aaaab\n"                                                  \
+        "v_fma_f32 v60, v60, v58, 0.5\n"                                                           \
+        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
+        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
+        "v_cvt_i32_f32 v59, v59\n"                                                                 \
+        "v_lshl_add_u32 v59, v59, 23, 1.0\n"                                                       \
+        "v_mul_f32 v60, v60, v59\n"                                                                \
+        "v_min_f32 v60, %[maxa], v60\n"                                                            \
+        "v_cmp_ngt_f32 vcc, %[mina], v60\n"                                                        \
+        "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
+        "v_sub_f32 v61, 1.0, v60\n"                                                                \
+        "v_mul_f32 v61, %[T], v61\n"                                                               \
+        "v_cmp_gt_f32 vcc, %[minT], v61\n"                                                         \
+        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                          \
+        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                     \
+        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                      \
+        "ds_read_b64 v[56:57], v62 offset:32\n"                                                    \
+        "v_mul_f32 v59, %[T], v60\n"                                                               \
+        "v_fmac_f32 %[C0], v59, v70\n"                                                             \
+        "v_fmac_f32 %[C1], v59, v71\n"                                                             \
+        "s_waitcnt lgkmcnt(0)\n"                                                                   \
+        "v_fmac_f32 %[C2], v59, v56\n"                                                             \
+        DEPTH_FMA                                                                                   \
+        "v_mov_b32 %[T], v61\n"                                                                    \
+        "v_mov_b32 %[last], %[idx]\n"                                                              \
+        "s_mov_b64 exec, %[sav]\n"                                                                 \
+        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                \
+        ".Lnextb_%=:\n"                                                                            \
         "v_add_u32 v62, 48, v62\n"                                                                 \
         "s_add_u32 %[idx], %[idx], 1\n"                                                            \
         "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
         "s_cbranch_scc1 .Lstep_%=\n"                                                               \
         ".Lend_%=:\n"                                                                              \
+        "s_waitcnt lgkmcnt(0)\n"                                                                   \
         : [act] "=&s"(act), [live] "=&s"(live), [ctb] "=&s"(ctb), [stp] "=&s"(stp), [sav] "=&s"(sav), \
           [idx] "=&s"(idx), [T] "+v"(T), [C0] "+v"(C0), [C1] "+v"(C1), [C2] "+v"(C2), [D] "+v"(D),   \
           [last] "+v"(last)                                                                         \
@@ -768,7 +825,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
           [uv] "v"(uv), [cu] "v"(cu), [cv] "v"(cv), [c6] "v"(c6), [cut] "s"(e_cut),                  \
           [maxa] "s"(max_alpha), [mina] "s"(min_alpha), [minT] "s"(min_T)                           \
         : "v48", "v49", "v50", "v51", "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60",  \
-          "v61", "v62", "vcc", "scc", "memory")
+          "v61", "v62", "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "vcc", "scc", "memory")
     if constexpr (DEPTH)
         TDGS_BLEND_ASM("v_fmac_f32 %[D], v59, v57\n");
     else
@@ -943,7 +1000,7 @@ static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs
     a.evaluations = evaluations;
     const int nt = t->tile_width * t->tile_height;
     const dim3 grid(t->nb_tiles_x, t->nb_tiles_y);
-    const size_t lds = (size_t)nt * sizeof(BlendRec);
+    const size_t lds = (size_t)(nt + 1) * sizeof(BlendRec);   // + the record blend_batch prefetches past a batch
     if (evaluations) {
         k_render_tiles<false, false, true><<<grid, nt, lds, s>>>(a);
         TDGS_LAUNCHED();
