@@ -691,12 +691,12 @@ struct BlendArgs {
 // 64-bit lane masks combined with scalar instructions, the exponential is skipped (scalar
 // branch) when no lane is live, and the state update runs under exec = contributing and not
 // stopping lanes; the compiled loop needed about 30 scalar and 39 vector instructions per
-// live record against 10 and 32 here. The next record's parameters are read from LDS into a
-// second register set while the current one is processed (the loop is unrolled twice), so the
-// read latency is hidden; the LDS array holds one record more than a batch for the read past
-// the last record. Valid only when every live exponent lies in [-87, 88] (the batch is not
-// `checked`). v48-v62 and v64-v71 are its scratch registers. Returns the mask of the lanes that
-// did not stop.
+// live record against 10 and 32 here. The next record (all ten floats) is read from LDS into
+// a second register set while the current one is processed (the loop is unrolled twice), so
+// no step waits on LDS; the LDS array holds one record more than a batch for the read past the
+// last record. Valid only when every live exponent lies in [-87, 88] (the batch is not
+// `checked`). v39-v63 are its scratch registers (the kernel stays within 64 VGPRs, 8
+// wavefronts per SIMD). Returns the mask of the lanes that did not stop.
 template <bool DEPTH>
 __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0, int32_t idx_end, float uu,
                                                 float vv, float uv, float cu, float cv, float e_cut,
@@ -710,109 +710,108 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "s_and_b64 %[act], exec, exec\n"                                                           \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         "s_mov_b32 %[idx], %[i0]\n"                                                                \
-        "v_mov_b32 v62, %[addr]\n"                                                                 \
-        "ds_read_b128 v[48:51], v62\n"                                                             \
-        "ds_read_b128 v[52:55], v62 offset:16\n"                                                   \
+        "v_mov_b32 v39, %[addr]\n"                                                                 \
+        "ds_read_b128 v[40:43], v39\n"                                                             \
+        "ds_read_b128 v[44:47], v39 offset:16\n"                                                   \
+        "ds_read_b64 v[48:49], v39 offset:32\n"                                                    \
         ".Lstep_%=:\n"                                                                             \
         "s_waitcnt lgkmcnt(0)\n"                                                                   \
-        "ds_read_b128 v[64:67], v62 offset:48\n"                                                   \
-        "ds_read_b128 v[68:71], v62 offset:64\n"                                                   \
-        "v_fma_f32 v58, v52, %[cv], v53\n"                                                         \
-        "v_fmac_f32 v58, v51, %[cu]\n"                                                             \
-        "v_fmac_f32 v58, v50, %[uv]\n"                                                             \
-        "v_fmac_f32 v58, v49, %[vv]\n"                                                             \
-        "v_fmac_f32 v58, v48, %[uu]\n"                                                             \
-        "v_cmp_ngt_f32 vcc, %[cut], v58\n"                                                         \
+        "ds_read_b128 v[50:53], v39 offset:48\n"                                                   \
+        "ds_read_b128 v[54:57], v39 offset:64\n"                                                   \
+        "ds_read_b64 v[58:59], v39 offset:80\n"                                                    \
+        "v_fma_f32 v60, v44, %[cv], v45\n"                                                         \
+        "v_fmac_f32 v60, v43, %[cu]\n"                                                             \
+        "v_fmac_f32 v60, v42, %[uv]\n"                                                             \
+        "v_fmac_f32 v60, v41, %[vv]\n"                                                             \
+        "v_fmac_f32 v60, v40, %[uu]\n"                                                             \
+        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                         \
         "s_and_b64 %[live], vcc, %[act]\n"                                                         \
         "s_cbranch_scc0 .Lnexta_%=\n"                                                              \
-        "v_mul_f32 v59, 0x3fb8aa3b, v58\n"                                                         \
-        "v_rndne_f32 v59, v59\n"                                                                   \
-        "v_fmac_f32 v58, 0xbf317200, v59\n"                                                        \
-        "v_fmac_f32 v58, 0xb5bfbe8e, v59\n"                                                        \
-        "v_fmamk_f32 v60, v58, 0x39500d01, %[c6]\n"                                                \
-        "v_fmaak_f32 v60, v60, v58, 0x3c088889\n"                                                  \
-        "v_fmaak_f32 v60, v60, v58, 0x3d2aaaab\n"                                                  \
-        "v_fmaak_f32 v60, v60, v58, 0x3e2aaaab\n"                                                  \
-        "v_fma_f32 v60, v60, v58, 0.5\n"                                                           \
-        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
-        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
-        "v_cvt_i32_f32 v59, v59\n"                                                                 \
-        "v_lshl_add_u32 v59, v59, 23, 1.0\n"                                                       \
-        "v_mul_f32 v60, v60, v59\n"                                                                \
-        "v_min_f32 v60, %[maxa], v60\n"                                                            \
-        "v_cmp_ngt_f32 vcc, %[mina], v60\n"                                                        \
+        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                         \
+        "v_rndne_f32 v61, v61\n"                                                                   \
+        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                        \
+        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                        \
+        "v_fmamk_f32 v62, v60, 0x39500d01, %[c6]\n"                                                \
+        "v_fmaak_f32 v62, v62, v60, 0x3c088889\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aaaab\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaaab\n"                                                  \
+        "v_fma_f32 v62, v62, v60, 0.5\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
+        "v_cvt_i32_f32 v61, v61\n"                                                                 \
+        "v_lshl_add_u32 v61, v61, 23, 1.0\n"                                                       \
+        "v_mul_f32 v62, v62, v61\n"                                                                \
+        "v_min_f32 v62, %[maxa], v62\n"                                                            \
+        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                        \
         "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
-        "v_sub_f32 v61, 1.0, v60\n"                                                                \
-        "v_mul_f32 v61, %[T], v61\n"                                                               \
-        "v_cmp_gt_f32 vcc, %[minT], v61\n"                                                         \
+        "v_sub_f32 v63, 1.0, v62\n"                                                                \
+        "v_mul_f32 v63, %[T], v63\n"                                                               \
+        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                         \
         "s_and_b64 %[stp], vcc, %[ctb]\n"                                                          \
         "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                     \
         "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                      \
-        "ds_read_b64 v[56:57], v62 offset:32\n"                                                    \
-        "v_mul_f32 v59, %[T], v60\n"                                                               \
-        "v_fmac_f32 %[C0], v59, v54\n"                                                             \
-        "v_fmac_f32 %[C1], v59, v55\n"                                                             \
-        "s_waitcnt lgkmcnt(0)\n"                                                                   \
-        "v_fmac_f32 %[C2], v59, v56\n"                                                             \
-        DEPTH_FMA                                                                                   \
-        "v_mov_b32 %[T], v61\n"                                                                    \
+        "v_mul_f32 v61, %[T], v62\n"                                                               \
+        "v_fmac_f32 %[C0], v61, v46\n"                                                             \
+        "v_fmac_f32 %[C1], v61, v47\n"                                                             \
+        "v_fmac_f32 %[C2], v61, v48\n"                                                             \
+        DEPTH_FMA("v49")                                                                           \
+        "v_mov_b32 %[T], v63\n"                                                                    \
         "v_mov_b32 %[last], %[idx]\n"                                                              \
         "s_mov_b64 exec, %[sav]\n"                                                                 \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         ".Lnexta_%=:\n"                                                                            \
-        "v_add_u32 v62, 48, v62\n"                                                                 \
+        "v_add_u32 v39, 48, v39\n"                                                                 \
         "s_add_u32 %[idx], %[idx], 1\n"                                                            \
         "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         "s_waitcnt lgkmcnt(0)\n"                                                                   \
-        "ds_read_b128 v[48:51], v62 offset:48\n"                                                   \
-        "ds_read_b128 v[52:55], v62 offset:64\n"                                                   \
-        "v_fma_f32 v58, v68, %[cv], v69\n"                                                         \
-        "v_fmac_f32 v58, v67, %[cu]\n"                                                             \
-        "v_fmac_f32 v58, v66, %[uv]\n"                                                             \
-        "v_fmac_f32 v58, v65, %[vv]\n"                                                             \
-        "v_fmac_f32 v58, v64, %[uu]\n"                                                             \
-        "v_cmp_ngt_f32 vcc, %[cut], v58\n"                                                         \
+        "ds_read_b128 v[40:43], v39 offset:48\n"                                                   \
+        "ds_read_b128 v[44:47], v39 offset:64\n"                                                   \
+        "ds_read_b64 v[48:49], v39 offset:80\n"                                                    \
+        "v_fma_f32 v60, v54, %[cv], v55\n"                                                         \
+        "v_fmac_f32 v60, v53, %[cu]\n"                                                             \
+        "v_fmac_f32 v60, v52, %[uv]\n"                                                             \
+        "v_fmac_f32 v60, v51, %[vv]\n"                                                             \
+        "v_fmac_f32 v60, v50, %[uu]\n"                                                             \
+        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                         \
         "s_and_b64 %[live], vcc, %[act]\n"                                                         \
         "s_cbranch_scc0 .Lnextb_%=\n"                                                              \
-        "v_mul_f32 v59, 0x3fb8aa3b, v58\n"                                                         \
-        "v_rndne_f32 v59, v59\n"                                                                   \
-        "v_fmac_f32 v58, 0xbf317200, v59\n"                                                        \
-        "v_fmac_f32 v58, 0xb5bfbe8e, v59\n"                                                        \
-        "v_fmamk_f32 v60, v58, 0x39500d01, %[c6]\n"                                                \
-        "v_fmaak_f32 v60, v60, v58, 0x3c088889\n"                                                  \
-        "v_fmaak_f32 v60, v60, v58, 0x3d2aaaab\n"                                                  \
-        "v_fmaak_f32 v60, v60, v58, 0x3e2aaaab\n"                                                  \
-        "v_fma_f32 v60, v60, v58, 0.5\n"                                                           \
-        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
-        "v_fma_f32 v60, v60, v58, 1.0\n"                                                           \
-        "v_cvt_i32_f32 v59, v59\n"                                                                 \
-        "v_lshl_add_u32 v59, v59, 23, 1.0\n"                                                       \
-        "v_mul_f32 v60, v60, v59\n"                                                                \
-        "v_min_f32 v60, %[maxa], v60\n"                                                            \
-        "v_cmp_ngt_f32 vcc, %[mina], v60\n"                                                        \
+        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                         \
+        "v_rndne_f32 v61, v61\n"                                                                   \
+        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                        \
+        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                        \
+        "v_fmamk_f32 v62, v60, 0x39500d01, %[c6]\n"                                                \
+        "v_fmaak_f32 v62, v62, v60, 0x3c088889\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aaaab\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaaab\n"                                                  \
+        "v_fma_f32 v62, v62, v60, 0.5\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
+        "v_cvt_i32_f32 v61, v61\n"                                                                 \
+        "v_lshl_add_u32 v61, v61, 23, 1.0\n"                                                       \
+        "v_mul_f32 v62, v62, v61\n"                                                                \
+        "v_min_f32 v62, %[maxa], v62\n"                                                            \
+        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                        \
         "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
-        "v_sub_f32 v61, 1.0, v60\n"                                                                \
-        "v_mul_f32 v61, %[T], v61\n"                                                               \
-        "v_cmp_gt_f32 vcc, %[minT], v61\n"                                                         \
+        "v_sub_f32 v63, 1.0, v62\n"                                                                \
+        "v_mul_f32 v63, %[T], v63\n"                                                               \
+        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                         \
         "s_and_b64 %[stp], vcc, %[ctb]\n"                                                          \
         "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                     \
         "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                      \
-        "ds_read_b64 v[56:57], v62 offset:32\n"                                                    \
-        "v_mul_f32 v59, %[T], v60\n"                                                               \
-        "v_fmac_f32 %[C0], v59, v70\n"                                                             \
-        "v_fmac_f32 %[C1], v59, v71\n"                                                             \
-        "s_waitcnt lgkmcnt(0)\n"                                                                   \
-        "v_fmac_f32 %[C2], v59, v56\n"                                                             \
-        DEPTH_FMA                                                                                   \
-        "v_mov_b32 %[T], v61\n"                                                                    \
+        "v_mul_f32 v61, %[T], v62\n"                                                               \
+        "v_fmac_f32 %[C0], v61, v56\n"                                                             \
+        "v_fmac_f32 %[C1], v61, v57\n"                                                             \
+        "v_fmac_f32 %[C2], v61, v58\n"                                                             \
+        DEPTH_FMA("v59")                                                                           \
+        "v_mov_b32 %[T], v63\n"                                                                    \
         "v_mov_b32 %[last], %[idx]\n"                                                              \
         "s_mov_b64 exec, %[sav]\n"                                                                 \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         ".Lnextb_%=:\n"                                                                            \
-        "v_add_u32 v62, 48, v62\n"                                                                 \
+        "v_add_u32 v39, 48, v39\n"                                                                 \
         "s_add_u32 %[idx], %[idx], 1\n"                                                            \
         "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
         "s_cbranch_scc1 .Lstep_%=\n"                                                               \
@@ -824,13 +823,18 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         : [addr] "v"(lds_addr), [i0] "s"(idx0), [iend] "s"(idx_end), [uu] "v"(uu), [vv] "v"(vv),     \
           [uv] "v"(uv), [cu] "v"(cu), [cv] "v"(cv), [c6] "v"(c6), [cut] "s"(e_cut),                  \
           [maxa] "s"(max_alpha), [mina] "s"(min_alpha), [minT] "s"(min_T)                           \
-        : "v48", "v49", "v50", "v51", "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60",  \
-          "v61", "v62", "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "vcc", "scc", "memory")
+        : "v39", "v40", "v41", "v42", "v43", "v44", "v45", "v46", "v47", "v48", "v49", "v50", "v51",  \
+          "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60", "v61", "v62", "v63", "vcc",    \
+          "scc", "memory")
+#define TDGS_DEPTH_ON(R) "v_fmac_f32 %[D], v61, " R "\n"
+#define TDGS_DEPTH_OFF(R) ""
     if constexpr (DEPTH)
-        TDGS_BLEND_ASM("v_fmac_f32 %[D], v59, v57\n");
+        TDGS_BLEND_ASM(TDGS_DEPTH_ON);
     else
-        TDGS_BLEND_ASM("");
+        TDGS_BLEND_ASM(TDGS_DEPTH_OFF);
 #undef TDGS_BLEND_ASM
+#undef TDGS_DEPTH_ON
+#undef TDGS_DEPTH_OFF
     return act;
 }
 
