@@ -26,16 +26,17 @@ constexpr int kSsimIn = kSsimT + 2 * kSsimR;
 constexpr float kC1 = 0.01f * 0.01f;
 constexpr float kC2 = 0.03f * 0.03f;
 
-// LDS layouts: a pixel's values are an odd number of words apart and a tile column starts at
-// a word offset = 16 (mod 32). A half-wavefront reads 16 consecutive rows of two adjacent
-// columns, so its 32 words fall on 32 distinct banks.
-constexpr int kInF = 7;                // forward input: x, y (3 channels each) + 1 pad
-constexpr int kPitchF = 208;           // >= kSsimIn * kInF, = 16 (mod 32)
-constexpr int kInB = 9;                // backward input: D1, D2, D3 (3 channels each)
-constexpr int kPitchB = 240;           // >= kSsimIn * kInB, = 16 (mod 32)
-static_assert(kPitchF >= kSsimIn * kInF && kPitchF % 32 == 16, "forward pitch");
-static_assert(kPitchB >= kSsimIn * kInB && kPitchB % 32 == 16, "backward pitch");
-static_assert((kSsimT * 15) % 32 == 16 && (kSsimT * 9) % 32 == 16, "filtered column pitch");
+// Both kernels filter with sliding windows held in registers. Pass 1 (along v, the contiguous
+// image axis): a thread takes one input column of the 26 x 26 tile and one quantity (or one
+// colour channel), loads the 26 (or 18 for half a column) inputs once and produces 16 (or 8)
+// outputs. Pass 2 (along u): a thread takes one output row and one filtered quantity, loads its
+// 26 pass-1 values and produces the 16 outputs. Each LDS value is read about once per pass
+// instead of once per window tap. LDS rows have 27 entries (odd), so lanes reading the same
+// entry of consecutive rows fall on distinct banks.
+constexpr int kRow = kSsimIn + 1;      // 27: LDS row length of a column / filtered row
+constexpr int kQF = 15;                // forward filtered quantities: 5 per channel
+constexpr int kQB = 9;                 // backward filtered quantities: D1, D2, D3 per channel
+constexpr int kOutPitch = 17;          // pass-2 output: value q of pixel (ou, ov) at (ou*16+ov)*17+q
 
 // XCD-aware tile order: workgroups are handed to the 8 XCDs round-robin by linear id, so the
 // workgroups with id = x (mod 8) all run on XCD x. They get one contiguous band of tiles (v
@@ -54,14 +55,17 @@ struct SsimWindow {
     float w[2 * kSsimR + 1];
 };
 
-// k_ssim_forward LDS layout: input x/y (3 channels each) for the 26 x 26 input tile, then the
-// v-filtered values of 5 quantities x 3 channels for 26 columns x 16 rows.
+// k_ssim_forward LDS: the input (x, y) pairs of the 26 x 26 tile per (column, channel), then
+// the pass-1 values of the 15 quantities per (quantity, output row), columns contiguous; the
+// pass-2 output (15 values per pixel) reuses the latter's space.
 __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ x, const float* __restrict__ y,
                                                       int W, int H, SsimWindow win, float* __restrict__ dmap,
                                                       double* __restrict__ partials) {
-    __shared__ float s_in[kSsimIn * kPitchF];      // (column iu, row iv, value) at iu*kPitchF + iv*kInF
-    __shared__ float s_v[kSsimIn][kSsimT][15];
+    __shared__ float2 s_in[kSsimIn * 3 * kRow];        // (iu, c, iv) at (iu*3 + c)*kRow + iv
+    __shared__ float s_v[kQF * kSsimT * kRow];         // (q, ov, iu) at (q*16 + ov)*kRow + iu
     __shared__ double s_red[2][256 / kWave];
+    float* const s_out = s_v;                          // (ou, ov, q) at (ou*16 + ov)*kOutPitch + q
+    static_assert(kSsimT * kSsimT * kOutPitch <= kQF * kSsimT * kRow, "pass-2 output fits");
     const int t = threadIdx.x;
     int tv, tu;
     ssim_tile((H + kSsimT - 1) / kSsimT, gridDim.x, &tv, &tu);
@@ -71,50 +75,70 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
         const int v = v0 + iv, u = u0 + iu;
         const bool in = v >= 0 && v < H && u >= 0 && u < W;
         const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
-        float* d = s_in + iu * kPitchF + iv * kInF;
 #pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            d[c] = in ? x[p + c] : 0.0f;
-            d[3 + c] = in ? y[p + c] : 0.0f;
+        for (int c = 0; c < 3; ++c)
+            s_in[(iu * 3 + c) * kRow + iv] = in ? make_float2(x[p + c], y[p + c]) : make_float2(0.0f, 0.0f);
+    }
+    __syncthreads();
+    // pass 1: thread (iu, c, half) filters rows ov = 8 half .. 8 half + 7 of column iu, channel c
+    if (t < kSsimIn * 3 * 2) {
+        const int iu = t % kSsimIn, c = (t / kSsimIn) % 3, half = t / (3 * kSsimIn);
+        const float2* src = s_in + (iu * 3 + c) * kRow + 8 * half;
+        float a[18], b[18];
+#pragma unroll
+        for (int k = 0; k < 18; ++k) {
+            const float2 ab = src[k];
+            a[k] = ab.x;
+            b[k] = ab.y;
+        }
+#pragma unroll
+        for (int o = 0; o < 8; ++o) {
+            float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f, m4 = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 2 * kSsimR + 1; ++d) {
+                const float wd = win.w[d], av = a[o + d], bv = b[o + d];
+                m0 = fmaf(wd, av, m0);
+                m1 = fmaf(wd, bv, m1);
+                m2 = fmaf(wd, av * av, m2);
+                m3 = fmaf(wd, bv * bv, m3);
+                m4 = fmaf(wd, av * bv, m4);
+            }
+            const int ov = 8 * half + o;
+            float* dst = s_v + ((5 * c) * kSsimT + ov) * kRow + iu;
+            dst[0] = m0;
+            dst[kSsimT * kRow] = m1;
+            dst[2 * kSsimT * kRow] = m2;
+            dst[3 * kSsimT * kRow] = m3;
+            dst[4 * kSsimT * kRow] = m4;
         }
     }
     __syncthreads();
-    // filter along v (the contiguous image axis)
-    for (int k = t; k < kSsimIn * kSsimT; k += 256) {
-        const int ov = k % kSsimT, iu = k / kSsimT;
-        float acc[15];
+    // pass 2: thread (ov, q) filters row ov of quantity q along u
+    float f[kSsimIn];
+    const bool p2 = t < kSsimT * kQF;
+    const int p2_ov = t % kSsimT, p2_q = t / kSsimT;
+    if (p2) {
+        const float* src = s_v + (p2_q * kSsimT + p2_ov) * kRow;
 #pragma unroll
-        for (int q = 0; q < 15; ++q) acc[q] = 0.0f;
+        for (int k = 0; k < kSsimIn; ++k) f[k] = src[k];
+    }
+    __syncthreads();   // s_out overwrites s_v
+    if (p2) {
 #pragma unroll
-        for (int d = 0; d < 2 * kSsimR + 1; ++d) {
-            const float* s = s_in + iu * kPitchF + (ov + d) * kInF;
-            const float wd = win.w[d];
+        for (int ou = 0; ou < kSsimT; ++ou) {
+            float m = 0.0f;
 #pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                const float a = s[c], b = s[3 + c];
-                acc[5 * c] = fmaf(wd, a, acc[5 * c]);
-                acc[5 * c + 1] = fmaf(wd, b, acc[5 * c + 1]);
-                acc[5 * c + 2] = fmaf(wd, a * a, acc[5 * c + 2]);
-                acc[5 * c + 3] = fmaf(wd, b * b, acc[5 * c + 3]);
-                acc[5 * c + 4] = fmaf(wd, a * b, acc[5 * c + 4]);
-            }
+            for (int d = 0; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], f[ou + d], m);
+            s_out[(ou * kSsimT + p2_ov) * kOutPitch + p2_q] = m;
         }
-#pragma unroll
-        for (int q = 0; q < 15; ++q) s_v[iu][ov][q] = acc[q];
     }
     __syncthreads();
     const int ov = t % kSsimT, ou = t / kSsimT;
     const int v = v0 + kSsimR + ov, u = u0 + kSsimR + ou;
     const bool on = v < H && u < W;
-    float m[15];
+    float m[kQF];
 #pragma unroll
-    for (int q = 0; q < 15; ++q) m[q] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < 2 * kSsimR + 1; ++d) {
-        const float wd = win.w[d];
-#pragma unroll
-        for (int q = 0; q < 15; ++q) m[q] = fmaf(wd, s_v[ou + d][ov][q], m[q]);
-    }
+    for (int q = 0; q < kQF; ++q) m[q] = s_out[(ou * kSsimT + ov) * kOutPitch + q];
     double ssum = 0.0, l1 = 0.0;
     if (on) {
         const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
@@ -133,8 +157,8 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
             dmap[3 * p + 3 + c] = -S / b2;            // dS/dE[x^2]
             dmap[3 * p + 6 + c] = 2.0f * a1 / B;      // dS/dE[xy]
             ssum += (double)S;
-            const float* px = s_in + (ou + kSsimR) * kPitchF + (ov + kSsimR) * kInF;
-            l1 += fabs((double)px[c] - (double)px[3 + c]);
+            const float2 px = s_in[((ou + kSsimR) * 3 + c) * kRow + ov + kSsimR];
+            l1 += fabs((double)px.x - (double)px.y);
         }
     }
     for (int d = 32; d >= 1; d >>= 1) {
@@ -185,8 +209,10 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
                                                        int W, int H, SsimWindow win,
                                                        const float* __restrict__ dmap, float w_l1, float w_ssim,
                                                        float* __restrict__ grad) {
-    __shared__ float s_in[kSsimIn * kPitchB];      // (column iu, row iv, value) at iu*kPitchB + iv*kInB
-    __shared__ float s_v[kSsimIn][kSsimT][9];
+    __shared__ float s_in[kSsimIn * kQB * kRow];       // (iu, q, iv) at (iu*9 + q)*kRow + iv
+    __shared__ float s_v[kQB * kSsimT * kRow];         // (q, ov, iu) at (q*16 + ov)*kRow + iu
+    float* const s_out = s_in;                         // (ou, ov, q) at (ou*16 + ov)*kOutPitch + q
+    static_assert(kSsimT * kSsimT * kOutPitch <= kSsimIn * kQB * kRow, "pass-2 output fits");
     const int t = threadIdx.x;
     int tv, tu;
     ssim_tile((H + kSsimT - 1) / kSsimT, gridDim.x, &tv, &tu);
@@ -196,39 +222,48 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         const int v = v0 + iv, u = u0 + iu;
         const bool in = v >= 0 && v < H && u >= 0 && u < W;
         const int64_t p = 9 * ((int64_t)v + (int64_t)H * u);
-        float* d = s_in + iu * kPitchB + iv * kInB;
 #pragma unroll
-        for (int q = 0; q < 9; ++q) d[q] = in ? dmap[p + q] : 0.0f;
+        for (int q = 0; q < kQB; ++q) s_in[(iu * kQB + q) * kRow + iv] = in ? dmap[p + q] : 0.0f;
     }
     __syncthreads();
-    for (int k = t; k < kSsimIn * kSsimT; k += 256) {
-        const int ov = k % kSsimT, iu = k / kSsimT;
-        float acc[9];
+    // pass 1: thread (iu, q) filters the whole column iu of quantity q along v
+    if (t < kSsimIn * kQB) {
+        const float* src = s_in + t * kRow;   // t = iu * 9 + q
+        const int iu = t / kQB, q = t % kQB;
+        float a[kSsimIn];
 #pragma unroll
-        for (int q = 0; q < 9; ++q) acc[q] = 0.0f;
+        for (int k = 0; k < kSsimIn; ++k) a[k] = src[k];
 #pragma unroll
-        for (int d = 0; d < 2 * kSsimR + 1; ++d) {
-            const float* s = s_in + iu * kPitchB + (ov + d) * kInB;
-            const float wd = win.w[d];
+        for (int ov = 0; ov < kSsimT; ++ov) {
+            float m = 0.0f;
 #pragma unroll
-            for (int q = 0; q < 9; ++q) acc[q] = fmaf(wd, s[q], acc[q]);
+            for (int d = 0; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], a[ov + d], m);
+            s_v[(q * kSsimT + ov) * kRow + iu] = m;
         }
+    }
+    __syncthreads();
+    // pass 2: thread (ov, q) filters row ov of quantity q along u
+    if (t < kSsimT * kQB) {
+        const int ov = t % kSsimT, q = t / kSsimT;
+        const float* src = s_v + (q * kSsimT + ov) * kRow;
+        float b[kSsimIn];
 #pragma unroll
-        for (int q = 0; q < 9; ++q) s_v[iu][ov][q] = acc[q];
+        for (int k = 0; k < kSsimIn; ++k) b[k] = src[k];
+#pragma unroll
+        for (int ou = 0; ou < kSsimT; ++ou) {
+            float m = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], b[ou + d], m);
+            s_out[(ou * kSsimT + ov) * kOutPitch + q] = m;   // s_in is no longer read
+        }
     }
     __syncthreads();
     const int ov = t % kSsimT, ou = t / kSsimT;
     const int v = v0 + kSsimR + ov, u = u0 + kSsimR + ou;
     if (v >= H || u >= W) return;
-    float f[9];
+    float f[kQB];
 #pragma unroll
-    for (int q = 0; q < 9; ++q) f[q] = 0.0f;
-#pragma unroll
-    for (int d = 0; d < 2 * kSsimR + 1; ++d) {
-        const float wd = win.w[d];
-#pragma unroll
-        for (int q = 0; q < 9; ++q) f[q] = fmaf(wd, s_v[ou + d][ov][q], f[q]);
-    }
+    for (int q = 0; q < kQB; ++q) f[q] = s_out[(ou * kSsimT + ov) * kOutPitch + q];
     const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
