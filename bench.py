@@ -232,6 +232,38 @@ def train_cfg3(core, iterations):
             "loss_last": round(float(tr.current_loss()), 6)}
 
 
+def render_other_tiling(core, w, g, tile, frames=240, warmup=10):
+    """The headline render with another tile size (the reference's default at 1080p is 16x32,
+    forward_structs.jl:419-424): wall-clock frames/s and the blending stage time."""
+    import torch
+    from tdgs_amd import host
+    cams = w.cameras
+    t = host.Tiling.for_camera(cams[0], *tile)
+    opts = host.RenderOptions.for_camera(cams[0], w.gaussians.sh_degree)
+    out = core.RenderOutputs.for_camera(cams[0], 0, include_rgb=True, include_transmittance=True,
+                                        include_depth=False, include_last_contributing_indices=False)
+    buf = core.RenderBuffers(len(g), t, 0)
+    for k in range(warmup):
+        core.render_(out, g, cams[k % len(cams)], t, opts, buf)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(frames):
+        core.render_(out, g, cams[k % len(cams)], t, opts, buf)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    L = core.lib()
+    core.check(L.tdgs_profile_begin(C.c_int32(16 * len(cams) + 64)))
+    for k in range(len(cams)):
+        core.render_(out, g, cams[k], t, opts, buf)
+    torch.cuda.synchronize()
+    ms = (C.c_double * 13)()
+    cnt = (C.c_int64 * 13)()
+    core.check(L.tdgs_profile_end(ms, cnt))
+    return {"tile": list(tile), "tiles": t.nb_tiles, "frames": frames,
+            "frames_per_s": round(frames / (t1 - t0), 2),
+            "stage_ms": {STAGES[i]: round(ms[i] / cnt[i], 4) for i in range(13) if cnt[i] > 0}}
+
+
 def stress_cfg4(core, repeats=5):
     """Config 4: 3M Gaussians at 3840x2160 (SH3, 16x32 tiles), forward and backward of one
     camera against a seeded uniform target; more than 100M duplicated keys."""
@@ -437,7 +469,9 @@ def main():
     extra = None
     if not args.no_extra_configs:
         torch.cuda.empty_cache()
-        extra = {"train_cfg2_host_images": train_host_images(core, w, tiling, deg)}
+        extra = {"render_cfg2_tile16x32": render_other_tiling(core, w, g, (16, 32))}
+        torch.cuda.empty_cache()
+        extra["train_cfg2_host_images"] = train_host_images(core, w, tiling, deg)
         torch.cuda.empty_cache()
         extra["train_cfg1"] = train_cfg1(core)
         torch.cuda.empty_cache()
