@@ -1278,7 +1278,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
         TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nb},
                              SortedCounts{sorted_f, buf->counts, d_nb}, WriteScanAndBlocks{cs, blk_first, nblk}, n, stemp,
-                             sbytes, d_m, s));
+                             sbytes, d_m, s, d_nb));
     }
     TDGS_TRY(read_counters(ctx, s, 5));
     const int64_t nbf = ctx->h_counters[0];

@@ -40,8 +40,15 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* tota
     return wave_off + incl - v;
 }
 
+// d_limit, when not null, is a device count past which every item is zero: tiles that start
+// at or after it do no work (their sum is 0 and nothing is written for them).
 template <class In>
-__global__ __launch_bounds__(kScanThreads) void k_scan_reduce(In in, int64_t n, int64_t* tile_sums) {
+__global__ __launch_bounds__(kScanThreads) void k_scan_reduce(In in, int64_t n, int64_t* tile_sums,
+                                                              const int64_t* d_limit) {
+    if (d_limit && (int64_t)blockIdx.x * kScanTile >= *d_limit) {
+        if (threadIdx.x == 0) tile_sums[blockIdx.x] = 0;
+        return;
+    }
     const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
     int64_t acc = 0;
 #pragma unroll
@@ -81,7 +88,8 @@ static __global__ __launch_bounds__(kScanThreads) void k_scan_tiles(int64_t* til
 
 template <class In, class Out>
 __global__ __launch_bounds__(kScanThreads) void k_scan_apply(In in, Out out, int64_t n,
-                                                             const int64_t* tile_offsets) {
+                                                             const int64_t* tile_offsets, const int64_t* d_limit) {
+    if (d_limit && (int64_t)blockIdx.x * kScanTile >= *d_limit) return;
     const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
     int32_t v[kScanItems];
     int64_t acc = 0;
@@ -107,20 +115,22 @@ inline size_t scan_temp_bytes_for(int64_t n) {
 
 // In1 is used by the reduce pass, In2 by the apply pass (they may differ when the reduce
 // pass also materialises the items, e.g. writes keep flags that the apply pass re-reads).
+// d_limit (device count, may be null): items at or past it are zero and their results are
+// not needed; the tiles past it are skipped.
 template <class In1, class In2, class Out>
 int device_scan(In1 in_reduce, In2 in_apply, Out out, int64_t n, void* temp, size_t temp_bytes,
-                int64_t* d_total, hipStream_t stream) {
+                int64_t* d_total, hipStream_t stream, const int64_t* d_limit = nullptr) {
     const int64_t ntiles = ceil_div(n > 0 ? n : 1, kScanTile);
     if (temp_bytes < (size_t)ntiles * sizeof(int64_t) || temp == nullptr) {
         set_error("scan scratch too small: need %zu bytes, have %zu", (size_t)ntiles * 8, temp_bytes);
         return TDGS_ERR_CAPACITY;
     }
     int64_t* tile_sums = (int64_t*)temp;
-    k_scan_reduce<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_reduce, n, tile_sums);
+    k_scan_reduce<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_reduce, n, tile_sums, d_limit);
     TDGS_LAUNCHED();
     k_scan_tiles<<<1, kScanThreads, 0, stream>>>(tile_sums, ntiles, d_total);
     TDGS_LAUNCHED();
-    k_scan_apply<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_apply, out, n, tile_sums);
+    k_scan_apply<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_apply, out, n, tile_sums, d_limit);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
