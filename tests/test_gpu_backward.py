@@ -84,3 +84,20 @@ def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact):
     got, ref = _run(gpu, oracle, w.gaussians, cam, t, opts, rand_grad)
     for k in ["grads2d"] + ARRAYS:
         assert rel_l2(got[k], ref[k]) <= REL_L2, (k, rel_l2(got[k], ref[k]))
+
+
+def test_backward_tiny_min_alpha_takes_range_checked_path(gpu, oracle):
+    """min_alpha = 1e-38 gives per-record cuts below -87, so every batch of the backward
+    blending uses the range-checked loop."""
+    w = synthetic.config(0, n=3000)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 0, min_alpha=1e-38, background_color=(0.2, 0.1, 0.3))
+    gen = torch.Generator(device="cuda").manual_seed(11)
+
+    def rand_grad(rgb):
+        return (torch.rand(rgb.shape, generator=gen, device=rgb.device) - 0.5) * 1e-3
+
+    got, ref = _run(gpu, oracle, w.gaussians, cam, t, opts, rand_grad)
+    for k in ["grads2d"] + ARRAYS:
+        assert rel_l2(got[k], ref[k]) <= REL_L2, (k, rel_l2(got[k], ref[k]))

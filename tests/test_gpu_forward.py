@@ -154,6 +154,38 @@ def test_render_needle_gaussians_without_dilation(gpu, oracle):
     _assert_forward_equal(r, out, buf)
 
 
+def test_render_tiny_min_alpha_takes_range_checked_path(gpu, oracle):
+    """min_alpha = 1e-38 puts the exponent cut below -87: every batch then leaves the
+    hand-scheduled blending steps for the loop that evaluates exp_f with its range handling."""
+    w = synthetic.config(0, n=3000)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 0, min_alpha=1e-38, background_color=(0.1, 0.2, 0.3))
+    r = oracle.render(w.gaussians, cam, t, opts)
+    out, buf = _gpu_render(gpu, w.gaussians, cam, t, opts)
+    assert r["nb_keys"] > 1000
+    _assert_forward_equal(r, out, buf)
+
+
+def test_render_only_huge_opacities_take_range_checked_path(gpu, oracle):
+    """Render-only opacities above 1e38 make live exponents exceed 88 in their batches, which
+    then use the range-checked loop; the other batches the fast steps."""
+    from tdgs_amd import ply
+    w = synthetic.config(0, n=3000)
+    ro = ply.to_render_only(w.gaussians)
+    ro.means_opacity[::97, 3] = np.float32(3e38)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.1, 0.2, 0.3))
+    r = oracle.render(ro, cam, t, opts)
+    out = gpu.RenderOutputs.for_camera(cam, 0, include_depth=True)
+    buf = gpu.RenderBuffers(len(ro.means_opacity), t, 0, keep_flags=True)
+    gpu.render_(out, gpu.RenderOnlyGaussiansVector.from_host(ro, 0), cam, t, opts, buf)
+    torch.cuda.synchronize()
+    assert r["nb_keys"] > 1000
+    _assert_forward_equal(r, out, buf)
+
+
 def test_render_filter_mode_and_antialiasing(gpu, oracle):
     w = synthetic.config(0, n=5000)
     cam = w.cameras[0]
