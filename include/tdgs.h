@@ -311,6 +311,19 @@ int tdgs_backward_project(void* stream, tdgs_gradients* grads, const tdgs_gaussi
                           const tdgs_camera* cam, const tdgs_render_options* opt,
                           const tdgs_render_buffers* buf, int32_t nb_fgaussians);
 
+/* backward_project_fgaussians_kernel! (backward_core.jl:309-452) fused with update!
+ * (optimizer.jl:964-1009, sh_degree = opt->sh_degree): the 3D gradients of each filtered
+ * Gaussian are applied to its parameters and moments at once instead of being written to
+ * grads (whose 3D arrays are left untouched; grads2d is read). The result equals
+ * tdgs_backward_project followed by tdgs_adam_step bit for bit; increments st->update_count.
+ * No reference counterpart as one call: for trainers that run no density control between the
+ * backward pass and the optimiser step (training.jl:221-236 does so every adc_interval
+ * iterations; call the two functions separately then). */
+int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_gaussians* g,
+                               tdgs_adam_state* st, const tdgs_camera* cam,
+                               const tdgs_render_options* opt, const tdgs_render_buffers* buf,
+                               int32_t nb_fgaussians);
+
 /* ---- optimiser: update! -------------------------------------------------------------- */
 
 /* update!(opt, fgradients, Val(sh_degree)) (optimizer.jl:964-1009): sparse Adam over the

@@ -6,6 +6,7 @@ bit. The fused L1 + DSSIM loss is a floating-point reduction and is compared wit
 torch restatement of the textbook SSIM (Wang et al. 2004; conv2d, zero padding) and its
 autograd gradient.
 """
+import ctypes as C
 import math
 
 import numpy as np
@@ -234,3 +235,54 @@ def test_reference_adc_case_on_gpu(gpu):
     f2g = torch.tensor(gold["fgidx_to_gidx_before"], dtype=torch.int32, device=DEV)
     training.adc_remap_fgidx_(adc, f2g, 3)
     assert f2g.cpu().tolist() == gold["fgidx_to_gidx_after"]
+
+
+@pytest.mark.parametrize("cfg,render_deg", [(1, 3), (1, 1), (0, 0)])
+def test_backward_project_adam_equals_separate_steps(gpu, cfg, render_deg):
+    """tdgs_backward_project_adam (the trainer's fused step) against tdgs_backward_project
+    followed by tdgs_adam_step on the same 2D gradients: parameters and moments bit for bit
+    (SH3 float4 items, a render degree below the stored one, SH0)."""
+    from tdgs_amd import synthetic, training
+    w = synthetic.config(cfg, n=20_000 if cfg else None, cameras=2)
+    cam = w.cameras[-1]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, render_deg)
+    deg = w.gaussians.sh_degree
+    runs = []
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    grads2d = None
+    for fused in (False, True):
+        gd = gpu.TrainableGaussiansVector.from_host(w.gaussians, 0)
+        out = gpu.RenderOutputs.for_camera(cam, 0)
+        buf = gpu.RenderBuffers(len(gd), t, 0)
+        gpu.render_(out, gd, cam, t, opts, buf)
+        opt = training.AdamOptimizer(gd, training.TrainingOptions())
+        rng = np.random.default_rng(9)
+        m = opt.moments
+        for arr in (m.means, m.opacity, m.scaling, m.rotation, m.sh):
+            arr.copy_(torch.from_numpy((np.abs(rng.normal(size=tuple(arr.shape))) * 1e-3).astype(np.float32)))
+        opt.update_count = 7
+        fg = gpu.FilteredGaussiansGradientsVector(len(gd), deg, 0)
+        nbf = buf.nb_fgaussians
+        if grads2d is None:   # one set of 2D gradients for both (the blending atomics are unordered)
+            rgb_grad = (torch.rand(out.rgb.shape, generator=gen, device="cuda") - 0.5) * 1e-3
+            gpu.backward_render_tiles_(fg, rgb_grad.contiguous(), out, cam, t, opts, buf)
+            grads2d = fg.grads2d[:nbf].clone()
+        fg.grads2d[:nbf].copy_(grads2d)
+        if fused:
+            opt.backward_project_update_(fg, cam, opts, buf)
+        else:
+            gpu.check(gpu.lib().tdgs_backward_project(gpu.stream_ptr(0), C.byref(fg.struct()), C.byref(gd.struct()),
+                                                      C.byref(cam.to_c()), C.byref(opts.to_c()),
+                                                      C.byref(buf.struct()), C.c_int32(nbf)))
+            opt.update_(fg, buf.fgidx_to_gidx, nbf, render_deg)
+        torch.cuda.synchronize()
+        assert opt.update_count == 8
+        runs.append((gd.to_host(), [x.cpu().numpy() for x in (m.means, m.opacity, m.scaling, m.rotation, m.sh)]))
+    (ga, ma), (gb, mb) = runs
+    for x, y in ((ga.means_opacity, gb.means_opacity), (ga.scaling, gb.scaling), (ga.rotation, gb.rotation),
+                 (ga.sh, gb.sh)):
+        np.testing.assert_array_equal(x, y)
+    for x, y in zip(ma, mb):
+        np.testing.assert_array_equal(x, y)
+    assert not np.array_equal(ga.means_opacity, w.gaussians.means_opacity)

@@ -435,6 +435,24 @@ class FilteredGaussiansGradientsVector:
         return s
 
 
+def backward_render_tiles_(fgradients: FilteredGaussiansGradientsVector, rgb_image_grad: torch.Tensor,
+                           outputs: RenderOutputs, camera: PinholeCamera, tiling: Tiling, options: RenderOptions,
+                           buffers: RenderBuffers):
+    """zero_2d_grads! + backward_render_tiles_kernel! (backward_core.jl:37-58, 96-293): the 2D
+    gradients only, for a caller that runs the backward projection itself."""
+    dev = rgb_image_grad.device.index
+    assert rgb_image_grad.dtype == torch.float32 and rgb_image_grad.is_contiguous()
+    nbf = buffers.nb_fgaussians
+    if nbf <= 0:
+        return fgradients
+    fgradients.grads2d[:nbf].zero_()
+    check(lib().tdgs_backward_render_tiles(stream_ptr(dev), C.byref(fgradients.struct()),
+                                           C.c_void_p(dptr(rgb_image_grad)), C.byref(outputs.struct()),
+                                           C.byref(camera.to_c()), C.byref(tiling.to_c()), C.byref(options.to_c()),
+                                           C.byref(buffers.struct())))
+    return fgradients
+
+
 def backward_(fgradients: FilteredGaussiansGradientsVector, rgb_image_grad: torch.Tensor,
               outputs: RenderOutputs, gaussians: TrainableGaussiansVector, camera: PinholeCamera,
               tiling: Tiling, options: RenderOptions, buffers: RenderBuffers):

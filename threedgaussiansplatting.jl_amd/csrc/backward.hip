@@ -254,6 +254,18 @@ __global__ void k_zero_f32(float* p, int64_t n) {
     if (i < n) p[i] = 0.0f;
 }
 
+// Adam applied in place of writing the 3D gradients (k_backward_project<true>): the moments,
+// the six learning rates and the step constants of update! (optimizer.jl:941-1009).
+struct AdamInPlace {
+    float* m_means;
+    float* m_op;
+    float* m_sc;
+    float* m_rot;
+    float* m_sh;
+    float lr[6];        // means, opacity, scaling, rotation, sh dc, sh rest
+    float beta1, beta2, omb1, omb2, bc1, bc2, eps;
+};
+
 struct BackProjectArgs {
     tdgs_gaussians g;
     tdgs_camera cam;
@@ -263,7 +275,49 @@ struct BackProjectArgs {
     const float* f2d;
     const int32_t* counts;
     tdgs_gradients gr;
+    AdamInPlace adam;
 };
+
+__device__ __forceinline__ void adam_in_place(const AdamInPlace& d, float& p, float g, float& m1, float& m2, float lr) {
+    adam_scalar(p, g, m1, m2, lr, d.beta1, d.beta2, d.omb1, d.omb2, d.bc1, d.bc2, d.eps);
+}
+
+// The geometry part of update! for Gaussian gi (0-based) with its 11 gradient components, in
+// the operation order of k_adam's geometry items.
+__device__ __forceinline__ void adam_geometry(const BackProjectArgs& a, int64_t gi, const float dm[3], float dlogit,
+                                              const float dlogs[3], const float dq[4]) {
+    const AdamInPlace& d = a.adam;
+    float4 mo = reinterpret_cast<float4*>(a.g.means_opacity)[gi];
+    float2* mm = reinterpret_cast<float2*>(d.m_means) + 3 * gi;
+    float2 m0 = mm[0], m1 = mm[1], m2 = mm[2];
+    adam_in_place(d, mo.x, dm[0], m0.x, m0.y, d.lr[0]);
+    adam_in_place(d, mo.y, dm[1], m1.x, m1.y, d.lr[0]);
+    adam_in_place(d, mo.z, dm[2], m2.x, m2.y, d.lr[0]);
+    float2 mop = reinterpret_cast<float2*>(d.m_op)[gi];
+    adam_in_place(d, mo.w, dlogit, mop.x, mop.y, d.lr[1]);
+    reinterpret_cast<float4*>(a.g.means_opacity)[gi] = mo;
+    mm[0] = m0; mm[1] = m1; mm[2] = m2;
+    reinterpret_cast<float2*>(d.m_op)[gi] = mop;
+    float2* ms = reinterpret_cast<float2*>(d.m_sc) + 3 * gi;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        float p = a.g.scaling[3 * gi + k];
+        float2 m = ms[k];
+        adam_in_place(d, p, dlogs[k], m.x, m.y, d.lr[2]);
+        a.g.scaling[3 * gi + k] = p;
+        ms[k] = m;
+    }
+    float4 r = reinterpret_cast<float4*>(a.g.rotation)[gi];
+    float4* mr = reinterpret_cast<float4*>(d.m_rot) + 2 * gi;
+    float4 ma = mr[0], mb = mr[1];
+    adam_in_place(d, r.x, dq[0], ma.x, ma.y, d.lr[3]);
+    adam_in_place(d, r.y, dq[1], ma.z, ma.w, d.lr[3]);
+    adam_in_place(d, r.z, dq[2], mb.x, mb.y, d.lr[3]);
+    adam_in_place(d, r.w, dq[3], mb.z, mb.w, d.lr[3]);
+    reinterpret_cast<float4*>(a.g.rotation)[gi] = r;
+    mr[0] = ma;
+    mr[1] = mb;
+}
 
 // backward_project_fgaussians_kernel! (backward_core.jl:309-452) + compute_sh_coeffs_grad!
 // A workgroup takes kBpThreads consecutive filtered Gaussians. Its non-empty ones (count > 0)
@@ -275,9 +329,16 @@ constexpr int kBpThreads = 256;
 constexpr int kShRow = 49;   // >= 48 coefficients, odd: rows of consecutive lanes hit distinct banks
 constexpr int kBpUnroll = 16;
 
+//
+// ADAM: instead of writing the 3D gradients, the kernel applies update! (k_adam's arithmetic)
+// to each filtered Gaussian's parameters and moments (empty ones with zero gradients), so the
+// 236 bytes per Gaussian of SH3 gradients are neither written nor read back. Used by the
+// trainer when no density control runs between the backward pass and the optimiser.
+template <bool ADAM>
 __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs a) {
     __shared__ float s_sh[kBpThreads * kShRow];   // row = local index of the Gaussian
     __shared__ int32_t s_gi[kBpThreads];          // gidx (0-based) of active Gaussians, else -1
+    __shared__ int32_t s_gall[ADAM ? kBpThreads : 1];   // gidx (0-based) of every valid row, else -1
     __shared__ int16_t s_list[kBpThreads];        // local indices of the active Gaussians
     __shared__ int32_t s_wcnt[kBpThreads / kWave];
     const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
@@ -285,10 +346,16 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
     const int64_t fz = f0 + t;
     const bool valid = fz < a.nbf;
     const bool active = valid && a.counts[fz] != 0;
-    s_gi[t] = active ? a.fgidx_to_gidx[fz] - 1 : -1;
+    const int32_t gz = valid ? a.fgidx_to_gidx[fz] - 1 : -1;
+    s_gi[t] = active ? gz : -1;
+    if (ADAM) s_gall[t] = gz;
     const uint64_t act = __ballot(active);
     if (lane == 0) s_wcnt[wave] = __popcll(act);
-    if (valid && !active) {
+    if (ADAM && valid && !active && gz >= 0) {
+        const float z[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        adam_geometry(a, gz, z, 0.0f, z, z);
+    }
+    if (!ADAM && valid && !active) {
         a.gr.mean3d[3 * fz] = 0.0f; a.gr.mean3d[3 * fz + 1] = 0.0f; a.gr.mean3d[3 * fz + 2] = 0.0f;
         a.gr.opacity_feature[fz] = 0.0f;
         a.gr.scaling_features[3 * fz] = 0.0f; a.gr.scaling_features[3 * fz + 1] = 0.0f;
@@ -377,10 +444,14 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
 #pragma unroll
         for (int k = 0; k < 9; ++k) in.g2[k] = g2[k];
         const BackwardProjectOut o = backward_project(in, a.cam, a.opt);
-        for (int k = 0; k < 3; ++k) a.gr.mean3d[3 * f + k] = o.dm[k];
-        a.gr.opacity_feature[f] = o.dlogit;
-        for (int k = 0; k < 3; ++k) a.gr.scaling_features[3 * f + k] = o.dlogs[k];
-        reinterpret_cast<float4*>(a.gr.rotation_features)[f] = make_float4(o.dq[0], o.dq[1], o.dq[2], o.dq[3]);
+        if (ADAM) {
+            adam_geometry(a, gi, o.dm, o.dlogit, o.dlogs, o.dq);
+        } else {
+            for (int k = 0; k < 3; ++k) a.gr.mean3d[3 * f + k] = o.dm[k];
+            a.gr.opacity_feature[f] = o.dlogit;
+            for (int k = 0; k < 3; ++k) a.gr.scaling_features[3 * f + k] = o.dlogs[k];
+            reinterpret_cast<float4*>(a.gr.rotation_features)[f] = make_float4(o.dq[0], o.dq[1], o.dq[2], o.dq[3]);
+        }
         sh_grad_basis(a.cam, a.opt.sh_degree, in.m, b);
         dcol[0] = in.g2[6]; dcol[1] = in.g2[7]; dcol[2] = in.g2[8];
     }
@@ -394,8 +465,46 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
         for (int c = 0; c < 3; ++c)
             for (int k = 0; k < hr; ++k) s_sh[t * kShRow + c * hg + k] = 0.0f;
     __syncthreads();
-    float* dsh = a.gr.sh + (int64_t)3 * hg * f0;
     const int nrows = (int)(a.nbf - f0 < kBpThreads ? a.nbf - f0 : kBpThreads);
+    if constexpr (ADAM) {
+        // update! on the SH coefficients k < hr of every row (k_adam's SH items)
+        const AdamInPlace& d = a.adam;
+        if (hs == hg && hg == hr && (3 * hr) % 4 == 0) {
+            const int q4 = 3 * hr / 4;
+            for (int i = t; i < nrows * q4; i += kBpThreads) {
+                const int j = i / q4, q = i - j * q4;
+                const int64_t gi = s_gall[j];
+                if (gi < 0) continue;
+                const int k0 = (4 * q) % hr;
+                const float* sv = s_sh + j * kShRow + 4 * q;
+                float4* pp = reinterpret_cast<float4*>(a.g.sh + (int64_t)3 * hs * gi) + q;
+                float4* mp = reinterpret_cast<float4*>(d.m_sh + (int64_t)6 * hs * gi) + 2 * q;
+                float4 p = *pp, m0 = mp[0], m1 = mp[1];
+                adam_in_place(d, p.x, sv[0], m0.x, m0.y, k0 == 0 ? d.lr[4] : d.lr[5]);
+                adam_in_place(d, p.y, sv[1], m0.z, m0.w, d.lr[5]);
+                adam_in_place(d, p.z, sv[2], m1.x, m1.y, d.lr[5]);
+                adam_in_place(d, p.w, sv[3], m1.z, m1.w, d.lr[5]);
+                *pp = p;
+                mp[0] = m0;
+                mp[1] = m1;
+            }
+        } else {
+            const int per = 3 * hr;
+            for (int i = t; i < nrows * per; i += kBpThreads) {
+                const int j = i / per, e = i - j * per, c = e / hr, k = e - c * hr;
+                const int64_t gi = s_gall[j];
+                if (gi < 0) continue;
+                const int64_t pi = (int64_t)3 * hs * gi + (int64_t)c * hs + k;
+                float p = a.g.sh[pi];
+                float2 m = reinterpret_cast<float2*>(d.m_sh)[pi];
+                adam_in_place(d, p, s_sh[j * kShRow + c * hg + k], m.x, m.y, k == 0 ? d.lr[4] : d.lr[5]);
+                a.g.sh[pi] = p;
+                reinterpret_cast<float2*>(d.m_sh)[pi] = m;
+            }
+        }
+        return;
+    }
+    float* dsh = a.gr.sh + (int64_t)3 * hg * f0;
     if (hg == 16 && hr == 16) {
         // every column written: float4 stores of 12 items per thread
 #pragma unroll
@@ -490,8 +599,44 @@ int tdgs_backward_project(void* stream, tdgs_gradients* grads, const tdgs_gaussi
     BackProjectArgs a;
     a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nb_fgaussians;
     a.fgidx_to_gidx = buf->fgidx_to_gidx; a.f2d = buf->f2d; a.counts = buf->counts; a.gr = *grads;
-    k_backward_project<<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(a);
+    k_backward_project<false><<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(a);
     TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_gaussians* g, tdgs_adam_state* st,
+                               const tdgs_camera* cam, const tdgs_render_options* opt,
+                               const tdgs_render_buffers* buf, int32_t nb_fgaussians) {
+    TDGS_TRY(check_gaussians(g, true));
+    TDGS_TRY(check_options(opt, g->sh_degree));
+    TDGS_REQUIRE(grads && grads->capacity >= nb_fgaussians && grads->sh_degree >= 0 && grads->sh_degree <= 3,
+                 "bad gradient buffers");
+    TDGS_REQUIRE(grads->sh_degree >= opt->sh_degree, "gradient SH storage below the render degree");
+    TDGS_REQUIRE(st && cam && buf && buf->fgidx_to_gidx && buf->f2d && buf->counts, "null arguments");
+    if (nb_fgaussians > 0) {
+        TDGS_REQUIRE(grads->grads2d && st->means_moments && st->opacity_moments && st->scaling_moments &&
+                         st->rotation_moments && st->sh_moments,
+                     "null arrays");
+        hipStream_t s = (hipStream_t)stream;
+        StageScope sc(TDGS_STAGE_BACKWARD_PROJECT, s);
+        BackProjectArgs a;
+        a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nb_fgaussians;
+        a.fgidx_to_gidx = buf->fgidx_to_gidx; a.f2d = buf->f2d; a.counts = buf->counts; a.gr = *grads;
+        AdamInPlace& d = a.adam;
+        d.m_means = st->means_moments; d.m_op = st->opacity_moments; d.m_sc = st->scaling_moments;
+        d.m_rot = st->rotation_moments; d.m_sh = st->sh_moments;
+        d.lr[0] = st->lr_means; d.lr[1] = st->lr_opacity; d.lr[2] = st->lr_scaling;
+        d.lr[3] = st->lr_rotation; d.lr[4] = st->lr_sh_dc; d.lr[5] = st->lr_sh_rest;
+        d.beta1 = st->beta1; d.beta2 = st->beta2;
+        d.omb1 = 1.0f - st->beta1; d.omb2 = 1.0f - st->beta2;
+        const double tt = (double)st->update_count + 1.0;
+        d.bc1 = (float)(1.0 - pow((double)st->beta1, tt));
+        d.bc2 = (float)(1.0 - pow((double)st->beta2, tt));
+        d.eps = st->epsilon;
+        k_backward_project<true><<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(a);
+        TDGS_LAUNCHED();
+    }
+    st->update_count += 1;
     return TDGS_OK;
 }
 

@@ -16,7 +16,7 @@ import torch
 
 from . import abi
 from .core import (FilteredGaussiansGradientsVector, RenderBuffers, RenderOutputs, TrainableGaussiansVector,
-                   _dev, backward_, check, context, dptr, lib, render_, stream_ptr)
+                   _dev, backward_, backward_render_tiles_, check, context, dptr, lib, render_, stream_ptr)
 from .host import PinholeCamera, RenderOptions, Tiling, logit32
 
 f32 = np.float32
@@ -118,6 +118,20 @@ class AdamOptimizer:
         s.beta1, s.beta2, s.epsilon = self.beta1, self.beta2, self.epsilon
         s.update_count = self.update_count
         return s
+
+    def backward_project_update_(self, fgradients: FilteredGaussiansGradientsVector, camera, options,
+                                 buffers):
+        """The backward projection with update! applied in place of the 3D gradients
+        (tdgs_backward_project_adam); the same parameters and moments as backward_project
+        followed by update_, bit for bit. fgradients.grads2d must hold the 2D gradients."""
+        g = self.gaussians
+        st = self.struct()
+        check(lib().tdgs_backward_project_adam(stream_ptr(g.device.index), C.byref(fgradients.struct()),
+                                               C.byref(g.struct()), C.byref(st), C.byref(camera.to_c()),
+                                               C.byref(options.to_c()), C.byref(buffers.struct()),
+                                               C.c_int32(buffers.nb_fgaussians)))
+        self.update_count = st.update_count
+        return g
 
     def update_(self, fgradients: FilteredGaussiansGradientsVector, fgidx_to_gidx: torch.Tensor,
                 nb_fgaussians: int, sh_degree: int):
@@ -329,8 +343,10 @@ class Trainer:
 
     def __init__(self, gaussians: TrainableGaussiansVector, cameras, images, render_options: RenderOptions,
                  tiling: Tiling, training_options: TrainingOptions, optimizer: AdamOptimizer | None = None,
-                 seed: int = 0, device=0):
+                 seed: int = 0, device=0, fuse_optimizer: bool = True):
         self.device = _dev(device)
+        # apply update! inside the backward projection when no density control intervenes
+        self.fuse_optimizer = fuse_optimizer
         self.gaussians = gaussians
         self.cameras = list(cameras)
         self.images = GroundTruthImages(images, self.device)
@@ -384,15 +400,30 @@ class Trainer:
         loss_grad_(self.render_outputs.rgb, gt, self.rgb_image_grad,
                    self.options.loss_dssim_vs_L1_weight, self.loss_sums, self.loss_temp)
         self.images.release(k)
-        backward_(self.fgradients, self.rgb_image_grad, self.render_outputs, self.gaussians, cam, self.tiling,
-                  self.render_options, self.render_buffers)
-        in_adc = self.maybe_densify_and_prune_()
-        self.update_learning_rates_()
-        self.optimizer.update_(self.fgradients, self.render_buffers.fgidx_to_gidx, self.render_buffers.nb_fgaussians,
-                               self.render_options.sh_degree)
+        if self.fuse_optimizer and not self.adc_step_due():
+            # no density control between the backward pass and update!: the backward
+            # projection applies the optimiser step itself (the 3D gradients are not stored)
+            backward_render_tiles_(self.fgradients, self.rgb_image_grad, self.render_outputs, cam, self.tiling,
+                                   self.render_options, self.render_buffers)
+            in_adc = self.maybe_densify_and_prune_()
+            self.update_learning_rates_()
+            self.optimizer.backward_project_update_(self.fgradients, cam, self.render_options, self.render_buffers)
+        else:
+            backward_(self.fgradients, self.rgb_image_grad, self.render_outputs, self.gaussians, cam, self.tiling,
+                      self.render_options, self.render_buffers)
+            in_adc = self.maybe_densify_and_prune_()
+            self.update_learning_rates_()
+            self.optimizer.update_(self.fgradients, self.render_buffers.fgidx_to_gidx,
+                                   self.render_buffers.nb_fgaussians, self.render_options.sh_degree)
         if in_adc:
             self.complete_adc_step_()
         self.maybe_opacity_reset_()
+
+    def adc_step_due(self):
+        """Whether maybe_densify_and_prune! densifies and prunes at this iteration."""
+        o = self.options
+        it = self.iteration_nb
+        return it <= o.adc_final_iteration_nb and it >= o.adc_start_iteration_nb and it % o.adc_interval == 0
 
     def peek_next_camera(self):
         """Camera index of the next step (draws the next permutation early if needed; the
