@@ -138,8 +138,21 @@ def train_bench(core, w, cams, tiling, deg, steps, warmup):
     ms = (C.c_double * 13)()
     cnt = (C.c_int64 * 13)()
     core.check(L.tdgs_profile_end(ms, cnt))
-    assert tr.iteration_nb < to.adc_start_iteration_nb
     stage = {STAGES[i]: round(ms[i] / psteps, 4) for i in range(13) if cnt[i] > 0}
+    # the backward projection and Adam as separate launches (what the trainer runs at density
+    # control iterations), for their per-kernel times
+    tr.fuse_optimizer = False
+    core.check(L.tdgs_profile_begin(C.c_int32(16 * psteps + 64)))
+    for _ in range(psteps):
+        tr.training_step_()
+    torch.cuda.synchronize()
+    core.check(L.tdgs_profile_end(ms, cnt))
+    assert tr.iteration_nb < to.adc_start_iteration_nb
+    stage["unfused"] = {}
+    for name in ("backward_project", "adam"):
+        i = STAGES.index(name)
+        if cnt[i] > 0:
+            stage["unfused"][name] = round(ms[i] / psteps, 4)
     return steps / (t1 - t0), (t1 - t0) * 1000.0 / steps, stage, loss
 
 
@@ -339,8 +352,9 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit)
     8-bit-digit LSD sort of the 64-bit keys (8 M + 24 M ceil(end_bit / 8)) whatever digit
     width and pass count the build uses, over the depth and tile sort times; K4 = tile ranges
     (8 M + 4 T); K5 = blend bytes (40 M + 20 P); K7 = backward projection ((160 + 24h) N_f);
-    K8 = Adam (28 (11 + 3h) N_f + 4 N_f). K7 and K8 use the render leg's counts (same
-    Gaussians and cameras, before any densification)."""
+    K8 = Adam (28 (11 + 3h) N_f + 4 N_f), both from the separate launches; K7_K8_fused = the
+    trainer's fused backward projection and Adam, priced as K7 + K8 over its time. K7 and K8
+    use the render leg's counts (same Gaussians and cameras, before any densification)."""
     rows = {
         "K1_project": (16 * n + (28 + 12 * h) * nf + 8 * nf + 56 * nb, ["cull_compact", "project"], stage_ms),
         "K2_scan_keys": (8 * nf + 24 * nb + 12 * m, ["count_scan", "emit"], stage_ms),
@@ -349,8 +363,12 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit)
         "K5_blend": (40 * m + 20 * npx, ["blend"], stage_ms),
     }
     if train_stage:
-        rows["K7_backward_project"] = ((160 + 24 * h) * nf, ["backward_project"], train_stage)
-        rows["K8_adam"] = (28 * (11 + 3 * h) * nf + 4 * nf, ["adam"], train_stage)
+        k7, k8 = (160 + 24 * h) * nf, 28 * (11 + 3 * h) * nf + 4 * nf
+        sep = train_stage.get("unfused", {})
+        rows["K7_backward_project"] = (k7, ["backward_project"], sep)
+        rows["K8_adam"] = (k8, ["adam"], sep)
+        if "adam" not in train_stage:   # the trainer's fused launch, priced as K7 + K8
+            rows["K7_K8_fused"] = (k7 + k8, ["backward_project"], train_stage)
     out = {}
     for k, (b, stages, src) in rows.items():
         if not all(s_ in src for s_ in stages):
