@@ -880,7 +880,10 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
 // entries is converted to blending parameters once per tile and staged in LDS, where every
 // lane reads the same record (broadcast). A wavefront skips an entry when no pixel it still
 // blends can reach min_alpha (exponent below e_cut), leaves the batch when all its pixels
-// are done, and the tile stops loading batches once every pixel is done.
+// are done, and the tile stops loading batches once every pixel is done. The steps of a batch
+// run in blend_batch, except for the counting replay (COUNT) and for batches whose live
+// exponents may leave [-87, 88] (`checked`), which take the loop below with exp_f's range
+// handling.
 template <bool RGB, bool DEPTH, bool COUNT = false>
 __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     extern __shared__ BlendRec s_rec[];
