@@ -743,7 +743,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
     const float c6 = 1.38888888888889e-3f;   // exp_f_core's coefficient of r^6 (a VGPR operand)
     uint64_t act, live, ctb, stp, sav;
     int32_t idx;
-#define TDGS_BLEND_ASM(DEPTH_FMA)                                                                  \
+#define TDGS_BLEND_ASM(DEPTH_FMA, READ_C)                                                                  \
     asm volatile(                                                                                  \
         "s_and_b64 %[act], exec, exec\n"                                                           \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
@@ -751,12 +751,12 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_mov_b32 v39, %[addr]\n"                                                                 \
         "ds_read_b128 v[40:43], v39\n"                                                             \
         "ds_read_b128 v[44:47], v39 offset:16\n"                                                   \
-        "ds_read_b64 v[48:49], v39 offset:32\n"                                                    \
+        READ_C("v[48:49]", "v48", "32")                                                              \
         ".Lstep_%=:\n"                                                                             \
         "s_waitcnt lgkmcnt(0)\n"                                                                   \
         "ds_read_b128 v[50:53], v39 offset:48\n"                                                   \
         "ds_read_b128 v[54:57], v39 offset:64\n"                                                   \
-        "ds_read_b64 v[58:59], v39 offset:80\n"                                                    \
+        READ_C("v[58:59]", "v58", "80")                                                              \
         "v_fma_f32 v60, v44, %[cv], v45\n"                                                         \
         "v_fmac_f32 v60, v43, %[cu]\n"                                                             \
         "v_fmac_f32 v60, v42, %[uv]\n"                                                             \
@@ -806,7 +806,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "s_waitcnt lgkmcnt(0)\n"                                                                   \
         "ds_read_b128 v[40:43], v39 offset:48\n"                                                   \
         "ds_read_b128 v[44:47], v39 offset:64\n"                                                   \
-        "ds_read_b64 v[48:49], v39 offset:80\n"                                                    \
+        READ_C("v[48:49]", "v48", "80")                                                              \
         "v_fma_f32 v60, v54, %[cv], v55\n"                                                         \
         "v_fmac_f32 v60, v53, %[cu]\n"                                                             \
         "v_fmac_f32 v60, v52, %[uv]\n"                                                             \
@@ -866,13 +866,18 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
           "scc", "memory")
 #define TDGS_DEPTH_ON(R) "v_fmac_f32 %[D], v61, " R "\n"
 #define TDGS_DEPTH_OFF(R) ""
+// the record's last floats: blue and depth (b64), or blue alone (b32) without depth
+#define TDGS_READ_BD(PAIR, ONE, OFF) "ds_read_b64 " PAIR ", v39 offset:" OFF "\n"
+#define TDGS_READ_B(PAIR, ONE, OFF) "ds_read_b32 " ONE ", v39 offset:" OFF "\n"
     if constexpr (DEPTH)
-        TDGS_BLEND_ASM(TDGS_DEPTH_ON);
+        TDGS_BLEND_ASM(TDGS_DEPTH_ON, TDGS_READ_BD);
     else
-        TDGS_BLEND_ASM(TDGS_DEPTH_OFF);
+        TDGS_BLEND_ASM(TDGS_DEPTH_OFF, TDGS_READ_B);
 #undef TDGS_BLEND_ASM
 #undef TDGS_DEPTH_ON
 #undef TDGS_DEPTH_OFF
+#undef TDGS_READ_BD
+#undef TDGS_READ_B
     return act;
 }
 
