@@ -253,6 +253,7 @@ class RenderBuffers:
         self.keys = torch.empty(kc, dtype=torch.int64, device=d)
         self.values = torch.empty(kc, dtype=torch.int32, device=d)
         self._sorted_keys = torch.empty(kc, dtype=torch.int64, device=d)
+        self._keys_pending = None   # new key arrays hold no render's keys
         self.sorted_values = torch.empty(kc, dtype=torch.int32, device=d)
         tb = lib().tdgs_render_temp_bytes(self.capacity, kc, C.byref(self.tiling.to_c()))
         self.temp = torch.empty(int(tb), dtype=torch.uint8, device=d)
