@@ -724,7 +724,9 @@ struct BlendArgs {
 // Per record it performs exactly the single-precision operations of the C++ loop in
 // k_render_tiles below (same operands, same order: the exponent's five fused multiply-adds,
 // exp_f_core's sequence, min with max_alpha, 1 - alpha, the products and the colour fused
-// multiply-adds), so every result is bit for bit the compiled loop's. What differs is the
+// multiply-adds; exp_f_core's final product with 2^n is one v_ldexp_f32, which rounds exactly
+// as that product does, subnormal results included), so every result is bit for bit the
+// compiled loop's. What differs is the
 // bookkeeping: the lanes still blending (act), live, contributing and stopping lanes are
 // 64-bit lane masks combined with scalar instructions, the exponential is skipped (scalar
 // branch) when no lane is live, and the state update runs under exec = contributing and not
@@ -777,8 +779,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_cvt_i32_f32 v61, v61\n"                                                                 \
-        "v_lshl_add_u32 v61, v61, 23, 1.0\n"                                                       \
-        "v_mul_f32 v62, v62, v61\n"                                                                \
+        "v_ldexp_f32 v62, v62, v61\n"                                                              \
         "v_min_f32 v62, %[maxa], v62\n"                                                            \
         "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                        \
         "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
@@ -799,14 +800,13 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         ".Lnexta_%=:\n"                                                                            \
-        "v_add_u32 v39, 48, v39\n"                                                                 \
         "s_add_u32 %[idx], %[idx], 1\n"                                                            \
         "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         "s_waitcnt lgkmcnt(0)\n"                                                                   \
-        "ds_read_b128 v[40:43], v39 offset:48\n"                                                   \
-        "ds_read_b128 v[44:47], v39 offset:64\n"                                                   \
-        READ_C("v[48:49]", "v48", "80")                                                              \
+        "ds_read_b128 v[40:43], v39 offset:96\n"                                                   \
+        "ds_read_b128 v[44:47], v39 offset:112\n"                                                   \
+        READ_C("v[48:49]", "v48", "128")                                                              \
         "v_fma_f32 v60, v54, %[cv], v55\n"                                                         \
         "v_fmac_f32 v60, v53, %[cu]\n"                                                             \
         "v_fmac_f32 v60, v52, %[uv]\n"                                                             \
@@ -827,8 +827,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_cvt_i32_f32 v61, v61\n"                                                                 \
-        "v_lshl_add_u32 v61, v61, 23, 1.0\n"                                                       \
-        "v_mul_f32 v62, v62, v61\n"                                                                \
+        "v_ldexp_f32 v62, v62, v61\n"                                                              \
         "v_min_f32 v62, %[maxa], v62\n"                                                            \
         "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                        \
         "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
@@ -849,7 +848,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
         ".Lnextb_%=:\n"                                                                            \
-        "v_add_u32 v39, 48, v39\n"                                                                 \
+        "v_add_u32 v39, 0x60, v39\n"                                                               \
         "s_add_u32 %[idx], %[idx], 1\n"                                                            \
         "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
         "s_cbranch_scc1 .Lstep_%=\n"                                                               \
