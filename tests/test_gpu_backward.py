@@ -69,7 +69,8 @@ def test_backward_test_scene(gpu, oracle, deg):
 
 
 @pytest.mark.parametrize("cfg,n,tile,exact", [(1, 20_000, (16, 16), False), (1, 20_000, (16, 16), True),
-                                              (2, 60_000, (16, 32), False), (0, None, (16, 16), False)])
+                                              (2, 60_000, (16, 32), False), (0, None, (16, 16), False),
+                                              (0, None, (32, 32), False), (0, None, (8, 8), False)])
 def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact):
     w = synthetic.config(cfg, n=n, cameras=2)
     cam = w.cameras[-1]

@@ -104,6 +104,20 @@ def test_render_synthetic_bit_exact(gpu, oracle, cfg, n, tile):
     _assert_forward_equal(r, out, buf)
 
 
+@pytest.mark.parametrize("w,h,tile", [(37, 23, (32, 32)), (301, 173, (8, 8)), (64, 64, (64, 16)), (1, 1, (16, 16))])
+def test_render_odd_sizes_and_tiles(gpu, oracle, w, h, tile):
+    """Partial tiles at the right and bottom edges, 1024-thread (32x32) and 64-pixel tiles,
+    and a one-pixel image."""
+    from tdgs_amd.host import look_at_camera
+    wl = synthetic.config(0, n=2000)
+    cam = look_at_camera(w, h, 60.0, (0.0, 0.0, -4.0))
+    t = host.Tiling.for_camera(cam, *tile)
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.1, 0.2, 0.3))
+    r = oracle.render(wl.gaussians, cam, t, opts)
+    out, buf = _gpu_render(gpu, wl.gaussians, cam, t, opts)
+    _assert_forward_equal(r, out, buf)
+
+
 @pytest.mark.parametrize("width", [2040, 2048])
 def test_render_tile_id_width_boundary(gpu, oracle, width):
     """8x8 tiles on width x 2056 pixels: 255 x 257 = 65535 tiles (the largest tiling whose
