@@ -168,6 +168,27 @@ def test_render_needle_gaussians_without_dilation(gpu, oracle):
     _assert_forward_equal(r, out, buf)
 
 
+@pytest.mark.parametrize("depth", [False, True])
+def test_render_without_last_contributors(gpu, oracle, depth):
+    """The blending variants that do not track the last contributor (its output not requested)
+    give the same images."""
+    w = synthetic.config(1, n=20_000, cameras=2)
+    cam = w.cameras[-1]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, w.gaussians.sh_degree, background_color=(0.1, 0.2, 0.3))
+    r = oracle.render(w.gaussians, cam, t, opts)
+    g = gpu.TrainableGaussiansVector.from_host(w.gaussians, 0)
+    out = gpu.RenderOutputs.for_camera(cam, 0, include_depth=depth, include_last_contributing_indices=False)
+    buf = gpu.RenderBuffers(len(g), t, 0)
+    gpu.render_(out, g, cam, t, opts, buf)
+    torch.cuda.synchronize()
+    assert out.last is None
+    np.testing.assert_array_equal(out.rgb.cpu().numpy(), r["rgb"])
+    np.testing.assert_array_equal(out.T.cpu().numpy(), r["T"])
+    if depth:
+        np.testing.assert_array_equal(out.depth.cpu().numpy(), r["depth"])
+
+
 def test_render_tiny_min_alpha_takes_range_checked_path(gpu, oracle):
     """min_alpha = 1e-38 puts the exponent cut below -87: every batch then leaves the
     hand-scheduled blending steps for the loop that evaluates exp_f with its range handling."""

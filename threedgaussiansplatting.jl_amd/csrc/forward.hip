@@ -737,7 +737,7 @@ struct BlendArgs {
 // last record. Valid only when every live exponent lies in [-87, 88] (the batch is not
 // `checked`). v39-v63 are its scratch registers (the kernel stays within 64 VGPRs, 8
 // wavefronts per SIMD). Returns the mask of the lanes that did not stop.
-template <bool DEPTH>
+template <bool DEPTH, bool LAST>
 __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0, int32_t idx_end, float uu,
                                                 float vv, float uv, float cu, float cv, float e_cut,
                                                 float max_alpha, float min_alpha, float min_T, float& T,
@@ -745,7 +745,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
     const float c6 = 1.38888888888889e-3f;   // exp_f_core's coefficient of r^6 (a VGPR operand)
     uint64_t act, live, ctb, stp, sav;
     int32_t idx;
-#define TDGS_BLEND_ASM(DEPTH_FMA, READ_C)                                                                  \
+#define TDGS_BLEND_ASM(DEPTH_FMA, READ_C, LAST_MOV)                                                                  \
     asm volatile(                                                                                  \
         "s_and_b64 %[act], exec, exec\n"                                                           \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
@@ -795,7 +795,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 %[C2], v61, v48\n"                                                             \
         DEPTH_FMA("v49")                                                                           \
         "v_mov_b32 %[T], v63\n"                                                                    \
-        "v_mov_b32 %[last], %[idx]\n"                                                              \
+        LAST_MOV                                                                                   \
         "s_mov_b64 exec, %[sav]\n"                                                                 \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
@@ -843,7 +843,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 %[C2], v61, v58\n"                                                             \
         DEPTH_FMA("v59")                                                                           \
         "v_mov_b32 %[T], v63\n"                                                                    \
-        "v_mov_b32 %[last], %[idx]\n"                                                              \
+        LAST_MOV                                                                                   \
         "s_mov_b64 exec, %[sav]\n"                                                                 \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
         "s_cbranch_scc0 .Lend_%=\n"                                                                \
@@ -868,15 +868,24 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
 // the record's last floats: blue and depth (b64), or blue alone (b32) without depth
 #define TDGS_READ_BD(PAIR, ONE, OFF) "ds_read_b64 " PAIR ", v39 offset:" OFF "\n"
 #define TDGS_READ_B(PAIR, ONE, OFF) "ds_read_b32 " ONE ", v39 offset:" OFF "\n"
-    if constexpr (DEPTH)
-        TDGS_BLEND_ASM(TDGS_DEPTH_ON, TDGS_READ_BD);
+// the last contributing index is tracked only when it is an output
+#define TDGS_LAST_ON "v_mov_b32 %[last], %[idx]\n"
+#define TDGS_LAST_OFF ""
+    if constexpr (DEPTH && LAST)
+        TDGS_BLEND_ASM(TDGS_DEPTH_ON, TDGS_READ_BD, TDGS_LAST_ON);
+    else if constexpr (DEPTH)
+        TDGS_BLEND_ASM(TDGS_DEPTH_ON, TDGS_READ_BD, TDGS_LAST_OFF);
+    else if constexpr (LAST)
+        TDGS_BLEND_ASM(TDGS_DEPTH_OFF, TDGS_READ_B, TDGS_LAST_ON);
     else
-        TDGS_BLEND_ASM(TDGS_DEPTH_OFF, TDGS_READ_B);
+        TDGS_BLEND_ASM(TDGS_DEPTH_OFF, TDGS_READ_B, TDGS_LAST_OFF);
 #undef TDGS_BLEND_ASM
 #undef TDGS_DEPTH_ON
 #undef TDGS_DEPTH_OFF
 #undef TDGS_READ_BD
 #undef TDGS_READ_B
+#undef TDGS_LAST_ON
+#undef TDGS_LAST_OFF
     return act;
 }
 
@@ -888,7 +897,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
 // run in blend_batch, except for the counting replay (COUNT) and for batches whose live
 // exponents may leave [-87, 88] (`checked`), which take the loop below with exp_f's range
 // handling.
-template <bool RGB, bool DEPTH, bool COUNT = false>
+template <bool RGB, bool DEPTH, bool COUNT = false, bool LAST = true>
 __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     extern __shared__ BlendRec s_rec[];
     const int NT = a.TW * a.TH;
@@ -935,7 +944,7 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
         if (!COUNT && !checked) {
             if (!done) {
                 const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) BlendRec*)s_rec;
-                const uint64_t act = blend_batch<DEPTH>(lds, (int32_t)(base + 1), (int32_t)(base + nb + 1), uu,
+                const uint64_t act = blend_batch<DEPTH, LAST>(lds, (int32_t)(base + 1), (int32_t)(base + nb + 1), uu,
                                                         vv, uv, cu, cv, a.e_cut, a.max_alpha, a.min_alpha,
                                                         a.min_T, T, C0, C1, C2, D, last);
                 done = ((act >> __lane_id()) & 1ull) == 0;
@@ -1056,10 +1065,20 @@ static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs
         return TDGS_OK;
     }
     const bool rgb = out->rgb != nullptr, dep = out->depth != nullptr;
-    if (rgb && dep) k_render_tiles<true, true><<<grid, nt, lds, s>>>(a);
-    else if (rgb) k_render_tiles<true, false><<<grid, nt, lds, s>>>(a);
-    else if (dep) k_render_tiles<false, true><<<grid, nt, lds, s>>>(a);
-    else k_render_tiles<false, false><<<grid, nt, lds, s>>>(a);
+    const bool last = out->last != nullptr;
+    if (rgb && dep) {
+        if (last) k_render_tiles<true, true, false, true><<<grid, nt, lds, s>>>(a);
+        else k_render_tiles<true, true, false, false><<<grid, nt, lds, s>>>(a);
+    } else if (rgb) {
+        if (last) k_render_tiles<true, false, false, true><<<grid, nt, lds, s>>>(a);
+        else k_render_tiles<true, false, false, false><<<grid, nt, lds, s>>>(a);
+    } else if (dep) {
+        if (last) k_render_tiles<false, true, false, true><<<grid, nt, lds, s>>>(a);
+        else k_render_tiles<false, true, false, false><<<grid, nt, lds, s>>>(a);
+    } else {
+        if (last) k_render_tiles<false, false, false, true><<<grid, nt, lds, s>>>(a);
+        else k_render_tiles<false, false, false, false><<<grid, nt, lds, s>>>(a);
+    }
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
