@@ -7,7 +7,9 @@
 // thread per pixel. The reference lets every pixel start at its own last contributor and
 // issues 9 float atomics per (pixel, Gaussian) pair. Here the wavefront walks the tile's
 // sorted list back to front in lock step (a lane whose last contributor lies before the
-// current entry contributes zero), so the per-pixel order of operations is the reference's.
+// current entry contributes zero), so every pixel meets its entries in the reference's order;
+// the per-pair arithmetic is regrouped (backward_pair_sums) with the same gradients up to
+// rounding.
 // The 9 gradient contributions of 7 contributing entries at a time are summed over the
 // wavefront in one transpose-sum (permlane swaps and DPP, one add per value), over the
 // workgroup's wavefronts with LDS atomics, and reach global memory once per
@@ -82,6 +84,35 @@ __device__ __forceinline__ int wave_max_i32(int v) {
     return v;
 }
 
+// backward_pair (backward_core.jl:249-272) in the form the wavefront sums. The partial colour
+// psi enters only through g . psi, kept as one scalar gpsi; the terms linear in the entry's M
+// or carrying a constant factor are summed over the pixels without it, and the flush applies
+// M and the factors once per (tile, Gaussian):
+//   dmu = M (sum out[0], sum out[1]),  dM11 = -sum out[3] / 2,  dM21 = -sum out[4],
+//   dM22 = -sum out[5] / 2.
+// out = [aa du, aa dv, G dalpha, aa du du, aa du dv, aa dv dv, T alpha g] with aa = alpha dalpha.
+__device__ __forceinline__ void backward_pair_sums(float alpha, float inv1ma, float G, float du, float dv,
+                                                   const float c[3], const float g[3], float* T, float* gpsi,
+                                                   float out[9]) {
+    const float Tn = *T * inv1ma;
+    *T = Tn;
+    const float tgc = Tn * fmaf(g[2], c[2], fmaf(g[1], c[1], g[0] * c[0]));
+    *gpsi = fmaf(alpha, tgc, *gpsi);
+    const float dalpha = inv1ma * (tgc - *gpsi);
+    const float aa = alpha * dalpha;
+    const float adu = aa * du, adv = aa * dv;
+    out[0] = adu;
+    out[1] = adv;
+    out[2] = G * dalpha;
+    out[3] = adu * du;
+    out[4] = adu * dv;
+    out[5] = adv * dv;
+    const float ta = Tn * alpha;
+    out[6] = ta * g[0];
+    out[7] = ta * g[1];
+    out[8] = ta * g[2];
+}
+
 constexpr int kSlots = 7;   // 7 entries x 9 gradient components = 63 of the 64 lanes
 
 struct __align__(16) BackRec {
@@ -139,7 +170,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         g1 = a.rgb_grad[3 * px + 1];
         g2 = a.rgb_grad[3 * px + 2];
     }
-    float psi[3] = {T * a.bg0, T * a.bg1, T * a.bg2};
+    float gpsi = T * fmaf(g2, a.bg2, fmaf(g1, a.bg1, g0 * a.bg0));   // g . psi, psi = T bg
     const float g[3] = {g0, g1, g2};
     const float cu = (float)U - 0.5f, cv = (float)V - 0.5f;
     // entries past the last contributor of every pixel of the wavefront / tile are skipped
@@ -200,7 +231,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
                         const float alpha = __builtin_fminf(aG, a.max_alpha);
                         if (!(alpha < a.min_alpha)) {
                             const float c[3] = {rb.z, rb.w, rc.x};
-                            backward_pair(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), G, du, dv, ra.w, rb.x, rb.y, c, g, &T, psi, o);
+                            backward_pair_sums(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), G, du, dv, c, g, &T, &gpsi, o);
                             contrib = true;
                         }
                     }
@@ -224,14 +255,25 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         __syncthreads();
         // Flush with lane i on component i % 9 of entry i / 9: one atomic instruction covers
         // the 36-byte slots of ~7 Gaussians instead of one scattered word of 64.
+        // The sums of backward_pair_sums become the gradient components here.
         for (int i = t; i < 9 * nb; i += NT) {
-            const int e = i / 9;
+            const int e = i / 9, k = i - 9 * e;
             const int64_t f = (int64_t)a.sorted_f[lo + e] - 1;
-            const float v = s_acc[i];
-            if (v != 0.0f) unsafeAtomicAdd(a.grads2d + 9 * f + (i - 9 * e), v);
-            s_acc[i] = 0.0f;
+            float v = s_acc[i];
+            if (k < 2) {
+                const float4 rb = s_rec[e].b;
+                const float m_a = k == 0 ? s_rec[e].a.w : rb.x;   // M11 or M21
+                const float m_b = k == 0 ? rb.x : rb.y;           // M21 or M22
+                v = fmaf(m_a, s_acc[9 * e], m_b * s_acc[9 * e + 1]);
+            } else if (k == 3 || k == 5) {
+                v *= -0.5f;
+            } else if (k == 4) {
+                v = -v;
+            }
+            if (v != 0.0f) unsafeAtomicAdd(a.grads2d + 9 * f + k, v);
         }
         __syncthreads();
+        for (int i = t; i < 9 * nb; i += NT) s_acc[i] = 0.0f;   // the next batch sums after its barrier
         hi = lo;
     }
 }
