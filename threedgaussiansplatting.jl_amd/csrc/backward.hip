@@ -182,25 +182,38 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
     __syncthreads();
     int64_t hi = s_max_last < end ? (int64_t)s_max_last : end;  // exclusive (0-based)
 
+    // The records of the next batch are gathered into registers (pf, pr) while the current
+    // batch is blended, so the gather's latency is not spent behind a barrier.
+    int32_t pf = 0;
+    float pr[9];
+    auto gather = [&](int64_t lo_, int nb_) {
+        if (t < nb_) {
+            pf = a.sorted_f[lo_ + t] - 1;
+            const float* r = a.f2d + 9 * (int64_t)pf;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) pr[k] = r[k];
+        }
+    };
+    if (hi > beg) gather(hi - NT > beg ? hi - NT : beg, (int)(hi - (hi - NT > beg ? hi - NT : beg)));
     while (hi > beg) {
         const int64_t lo = hi - NT > beg ? hi - NT : beg;
         const int nb = (int)(hi - lo);
         bool low = false;   // a cut below -87 (tiny min_alpha, huge or NaN opacity)
         if (t < nb) {
-            const int64_t f = (int64_t)a.sorted_f[lo + t] - 1;
-            const float* r = a.f2d + 9 * f;
             BackRec rec;
-            rec.a = make_float4(r[0], r[1], r[2], r[3]);
-            rec.b = make_float4(r[4], r[5], r[6], r[7]);
+            rec.a = make_float4(pr[0], pr[1], pr[2], pr[3]);
+            rec.b = make_float4(pr[4], pr[5], pr[6], pr[7]);
             // a * exp_f(e) < min_alpha for e < cut (log_f and exp_f errors ~1e-6 absolute,
-            // inside the 1e-3 margin of log_min_alpha; a NaN cut never skips)
-            rec.c = make_float4(r[8], a.log_min_alpha - log_f(r[2]), 0.0f, 0.0f);
+            // inside the 1e-3 margin of log_min_alpha; a NaN cut never skips); the Gaussian's
+            // index rides along for the flush
+            rec.c = make_float4(pr[8], a.log_min_alpha - log_f(pr[2]), __builtin_bit_cast(float, pf), 0.0f);
             s_rec[t] = rec;
             low = !(rec.c.y >= -87.0f);
         }
         // A live exponent lies in [cut, 0]; with every cut of the batch at least -87 that is
         // inside exp_f's polynomial range, so the range vote is skipped.
         const bool checked = __syncthreads_or(low);
+        if (lo > beg) gather(lo - NT > beg ? lo - NT : beg, (int)(lo - (lo - NT > beg ? lo - NT : beg)));
         const int jtop = (int)((int64_t)wave_last - lo < nb ? (int64_t)wave_last - lo : nb);
         const int last_rel = (int)((int64_t)last - lo);   // entry jj of the batch is before last iff jj < last_rel
         // Entries back to front; the 9 contributions of up to kSlots consecutive contributing
@@ -258,7 +271,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         // The sums of backward_pair_sums become the gradient components here.
         for (int i = t; i < 9 * nb; i += NT) {
             const int e = i / 9, k = i - 9 * e;
-            const int64_t f = (int64_t)a.sorted_f[lo + e] - 1;
+            const int64_t f = __builtin_bit_cast(int32_t, s_rec[e].c.z);
             float v = s_acc[i];
             if (k < 2) {
                 const float4 rb = s_rec[e].b;
