@@ -4,7 +4,7 @@
 // Reference: src/backward_core.jl:37-452 (+ helpers :465-964), src/backward_structs.jl:250-257.
 //
 // Backward blending (backward_render_tiles_kernel!, :96-293): one workgroup per tile, one
-// thread per pixel. The reference lets every pixel start at its own last contributor and
+// thread per two pixels. The reference lets every pixel start at its own last contributor and
 // issues 9 float atomics per (pixel, Gaussian) pair. Here the wavefront walks the tile's
 // sorted list back to front in lock step (a lane whose last contributor lies before the
 // current entry contributes zero), so every pixel meets its entries in the reference's order;
@@ -90,7 +90,7 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 // M and the factors once per (tile, Gaussian):
 //   dmu = M (sum out[0], sum out[1]),  dM11 = -sum out[3] / 2,  dM21 = -sum out[4],
 //   dM22 = -sum out[5] / 2.
-// out = [aa du, aa dv, G dalpha, aa du du, aa du dv, aa dv dv, T alpha g] with aa = alpha dalpha.
+// out += [aa du, aa dv, G dalpha, aa du du, aa du dv, aa dv dv, T alpha g] with aa = alpha dalpha.
 __device__ __forceinline__ void backward_pair_sums(float alpha, float inv1ma, float G, float du, float dv,
                                                    const float c[3], const float g[3], float* T, float* gpsi,
                                                    float out[9]) {
@@ -101,16 +101,16 @@ __device__ __forceinline__ void backward_pair_sums(float alpha, float inv1ma, fl
     const float dalpha = inv1ma * (tgc - *gpsi);
     const float aa = alpha * dalpha;
     const float adu = aa * du, adv = aa * dv;
-    out[0] = adu;
-    out[1] = adv;
-    out[2] = G * dalpha;
-    out[3] = adu * du;
-    out[4] = adu * dv;
-    out[5] = adv * dv;
+    out[0] += adu;
+    out[1] += adv;
+    out[2] = fmaf(G, dalpha, out[2]);
+    out[3] = fmaf(adu, du, out[3]);
+    out[4] = fmaf(adu, dv, out[4]);
+    out[5] = fmaf(adv, dv, out[5]);
     const float ta = Tn * alpha;
-    out[6] = ta * g[0];
-    out[7] = ta * g[1];
-    out[8] = ta * g[2];
+    out[6] = fmaf(ta, g[0], out[6]);
+    out[7] = fmaf(ta, g[1], out[7]);
+    out[8] = fmaf(ta, g[2], out[8]);
 }
 
 constexpr int kSlots = 7;   // 7 entries x 9 gradient components = 63 of the 64 lanes
@@ -135,11 +135,16 @@ struct BackBlendArgs {
     float* grads2d;
 };
 
-__global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
+__global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
     extern __shared__ float4 s_raw4[];
+    // Two pixels per lane: thread t takes pixels t and t + NB of the tile (NB = blockDim.x =
+    // NT / 2 rounded up to whole wavefronts; a pixel index past NT is off), so the per-entry
+    // record reads, votes, slot bookkeeping and transpose-sum serve 128 pixels per wavefront.
+    // A batch holds NB entries.
     const int NT = a.TW * a.TH;
+    const int NB = (int)blockDim.x;
     BackRec* s_rec = reinterpret_cast<BackRec*>(s_raw4);
-    float* s_acc = reinterpret_cast<float*>(s_rec + NT);  // [NT][9]
+    float* s_acc = reinterpret_cast<float*>(s_rec + NB);  // [NB][9]
     __shared__ int s_max_last;
     const int t = threadIdx.x;
     const int lane = __lane_id();
@@ -150,33 +155,41 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
     // for 32 to 1024 bands).
     const int tx = blockIdx.x + 1, ty = blockIdx.y + 1;
     const int tile = tx + (ty - 1) * a.ntx;
-    int u_in, v_in;
-    tile_pixel(t, a.TW, a.TH, &u_in, &v_in);
-    const int U = u_in + (tx - 1) * a.TW, V = v_in + (ty - 1) * a.TH;
-    const bool on = U <= a.W && V <= a.H;
     int64_t end = a.tiles_end[tile - 1];
     int64_t beg = tile == 1 ? 0 : a.tiles_end[tile - 2];
     if (end > a.m) end = a.m;
     if (beg < 0) beg = 0;
     if (beg > end) beg = end;
 
-    float T = 0.0f, g0 = 0.0f, g1 = 0.0f, g2 = 0.0f;
-    int32_t last = 0;
-    if (on) {
-        const int64_t px = (int64_t)(V - 1) + (int64_t)a.H * (U - 1);
-        T = a.T[px];
-        last = a.last[px];
-        g0 = a.rgb_grad[3 * px];
-        g1 = a.rgb_grad[3 * px + 1];
-        g2 = a.rgb_grad[3 * px + 2];
+    float T[2], gpsi[2], g[2][3], cu[2], cv[2];
+    int32_t last[2];
+    bool on[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int q = t + p * NB;
+        int u_in = 1, v_in = 1;
+        if (q < NT) tile_pixel(q, a.TW, a.TH, &u_in, &v_in);
+        const int U = u_in + (tx - 1) * a.TW, V = v_in + (ty - 1) * a.TH;
+        on[p] = q < NT && U <= a.W && V <= a.H;
+        T[p] = 0.0f;
+        last[p] = 0;
+        g[p][0] = g[p][1] = g[p][2] = 0.0f;
+        if (on[p]) {
+            const int64_t px = (int64_t)(V - 1) + (int64_t)a.H * (U - 1);
+            T[p] = a.T[px];
+            last[p] = a.last[px];
+            g[p][0] = a.rgb_grad[3 * px];
+            g[p][1] = a.rgb_grad[3 * px + 1];
+            g[p][2] = a.rgb_grad[3 * px + 2];
+        }
+        gpsi[p] = T[p] * fmaf(g[p][2], a.bg2, fmaf(g[p][1], a.bg1, g[p][0] * a.bg0));   // g . psi, psi = T bg
+        cu[p] = (float)U - 0.5f;
+        cv[p] = (float)V - 0.5f;
     }
-    float gpsi = T * fmaf(g2, a.bg2, fmaf(g1, a.bg1, g0 * a.bg0));   // g . psi, psi = T bg
-    const float g[3] = {g0, g1, g2};
-    const float cu = (float)U - 0.5f, cv = (float)V - 0.5f;
     // entries past the last contributor of every pixel of the wavefront / tile are skipped
-    const int wave_last = wave_max_i32(last);
+    const int wave_last = wave_max_i32(last[0] > last[1] ? last[0] : last[1]);
     if (t == 0) s_max_last = 0;
-    for (int k = t; k < NT * 9; k += NT) s_acc[k] = 0.0f;
+    for (int k = t; k < NB * 9; k += NB) s_acc[k] = 0.0f;
     __syncthreads();
     if (lane == 0) atomicMax(&s_max_last, wave_last);
     __syncthreads();
@@ -194,9 +207,9 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
             for (int k = 0; k < 9; ++k) pr[k] = r[k];
         }
     };
-    if (hi > beg) gather(hi - NT > beg ? hi - NT : beg, (int)(hi - (hi - NT > beg ? hi - NT : beg)));
+    if (hi > beg) gather(hi - NB > beg ? hi - NB : beg, (int)(hi - (hi - NB > beg ? hi - NB : beg)));
     while (hi > beg) {
-        const int64_t lo = hi - NT > beg ? hi - NT : beg;
+        const int64_t lo = hi - NB > beg ? hi - NB : beg;
         const int nb = (int)(hi - lo);
         bool low = false;   // a cut below -87 (tiny min_alpha, huge or NaN opacity)
         if (t < nb) {
@@ -213,9 +226,10 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         // A live exponent lies in [cut, 0]; with every cut of the batch at least -87 that is
         // inside exp_f's polynomial range, so the range vote is skipped.
         const bool checked = __syncthreads_or(low);
-        if (lo > beg) gather(lo - NT > beg ? lo - NT : beg, (int)(lo - (lo - NT > beg ? lo - NT : beg)));
+        if (lo > beg) gather(lo - NB > beg ? lo - NB : beg, (int)(lo - (lo - NB > beg ? lo - NB : beg)));
         const int jtop = (int)((int64_t)wave_last - lo < nb ? (int64_t)wave_last - lo : nb);
-        const int last_rel = (int)((int64_t)last - lo);   // entry jj of the batch is before last iff jj < last_rel
+        // entry jj of the batch is before pixel p's last contributor iff jj < last_rel[p]
+        const int last_rel[2] = {(int)((int64_t)last[0] - lo), (int)((int64_t)last[1] - lo)};
         // Entries back to front; the 9 contributions of up to kSlots consecutive contributing
         // entries are kept per lane and summed over the wavefront in one transpose-sum, after
         // which lane l holds component l % 9 of slot l / 9 and adds it to the tile's LDS sum.
@@ -230,22 +244,31 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
                 while (j >= 0) {
                     const int jj = j--;
                     const float4 ra = s_rec[jj].a, rb = s_rec[jj].b, rc = s_rec[jj].c;
-                    float du, dv;
-                    const float ex = backward_exponent(cu, cv, ra.x, ra.y, ra.w, rb.x, rb.y, &du, &dv);
-                    const bool live = on && jj < last_rel && !(ex < rc.y);
-                    if (!wave_any(live)) continue;
+                    float du[2], dv[2], ex[2];
+                    bool live[2];
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        ex[p] = backward_exponent(cu[p], cv[p], ra.x, ra.y, ra.w, rb.x, rb.y, &du[p], &dv[p]);
+                        live[p] = on[p] && jj < last_rel[p] && !(ex[p] < rc.y);
+                    }
+                    if (!wave_any(live[0] || live[1])) continue;
                     bool contrib = false;
-                    const bool wide = checked && wave_any(live && !(ex >= -87.0f && ex <= 88.0f));
-                    if (live) {
-                        const float G = wide ? exp_f_sel(ex) : exp_f_core(ex);   // exp_f(ex)
-                        const float aG = ra.z * G;
-                        // min(aG, max_alpha): the select aG < max_alpha ? aG : max_alpha for a
-                        // non-NaN max_alpha, NaN aG included
-                        const float alpha = __builtin_fminf(aG, a.max_alpha);
-                        if (!(alpha < a.min_alpha)) {
-                            const float c[3] = {rb.z, rb.w, rc.x};
-                            backward_pair_sums(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), G, du, dv, c, g, &T, &gpsi, o);
-                            contrib = true;
+                    const bool wide = checked && wave_any((live[0] && !(ex[0] >= -87.0f && ex[0] <= 88.0f)) ||
+                                                          (live[1] && !(ex[1] >= -87.0f && ex[1] <= 88.0f)));
+                    const float c[3] = {rb.z, rb.w, rc.x};
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        if (live[p]) {
+                            const float G = wide ? exp_f_sel(ex[p]) : exp_f_core(ex[p]);   // exp_f(ex)
+                            const float aG = ra.z * G;
+                            // min(aG, max_alpha): the select aG < max_alpha ? aG : max_alpha for a
+                            // non-NaN max_alpha, NaN aG included
+                            const float alpha = __builtin_fminf(aG, a.max_alpha);
+                            if (!(alpha < a.min_alpha)) {
+                                backward_pair_sums(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), G, du[p], dv[p], c, g[p],
+                                                   &T[p], &gpsi[p], o);
+                                contrib = true;
+                            }
                         }
                     }
                     if (wave_any(contrib)) {
@@ -269,7 +292,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
         // Flush with lane i on component i % 9 of entry i / 9: one atomic instruction covers
         // the 36-byte slots of ~7 Gaussians instead of one scattered word of 64.
         // The sums of backward_pair_sums become the gradient components here.
-        for (int i = t; i < 9 * nb; i += NT) {
+        for (int i = t; i < 9 * nb; i += NB) {
             const int e = i / 9, k = i - 9 * e;
             const int64_t f = __builtin_bit_cast(int32_t, s_rec[e].c.z);
             float v = s_acc[i];
@@ -286,7 +309,7 @@ __global__ __launch_bounds__(1024) void k_backward_blend(BackBlendArgs a) {
             if (v != 0.0f) unsafeAtomicAdd(a.grads2d + 9 * f + k, v);
         }
         __syncthreads();
-        for (int i = t; i < 9 * nb; i += NT) s_acc[i] = 0.0f;   // the next batch sums after its barrier
+        for (int i = t; i < 9 * nb; i += NB) s_acc[i] = 0.0f;   // the next batch sums after its barrier
         hi = lo;
     }
 }
@@ -620,7 +643,9 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
     a.m = buf->key_capacity;
     a.tiles_end = buf->tiles_end; a.sorted_f = buf->sorted_values; a.f2d = buf->f2d;
     a.rgb_grad = rgb_grad; a.T = out->T; a.last = out->last; a.grads2d = grads->grads2d;
-    const int nt = tiling->tile_width * tiling->tile_height;
+    // two pixels per thread, in whole wavefronts (the transpose-sum reads all 64 lanes; the
+    // tile's pixel count is a multiple of 64, so half of it is one of 32)
+    const int nt = (tiling->tile_width * tiling->tile_height / 2 + kWave - 1) / kWave * kWave;
     const size_t lds = (size_t)nt * (sizeof(BackRec) + 9 * sizeof(float));
     k_backward_blend<<<dim3(tiling->nb_tiles_x, tiling->nb_tiles_y), nt, lds, s>>>(a);
     TDGS_LAUNCHED();
