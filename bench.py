@@ -386,8 +386,8 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards by "
-              "views or image bands, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard "
+              "by camera views or by image bands of tiles; no multi-GPU path is built)", file=sys.stderr)
         sys.exit(2)
     import torch
     from tdgs_amd import core, host, synthetic
