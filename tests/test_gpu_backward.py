@@ -70,7 +70,10 @@ def test_backward_test_scene(gpu, oracle, deg):
 
 @pytest.mark.parametrize("cfg,n,tile,exact", [(1, 20_000, (16, 16), False), (1, 20_000, (16, 16), True),
                                               (2, 60_000, (16, 32), False), (0, None, (16, 16), False),
-                                              (0, None, (32, 32), False), (0, None, (8, 8), False)])
+                                              (0, None, (32, 32), False), (0, None, (8, 8), False),
+                                              # 192 pixels: 128 threads, so the second pixel of
+                                              # lanes 64-127 lies past the tile
+                                              (0, None, (24, 8), False), (0, None, (8, 24), False)])
 def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact):
     w = synthetic.config(cfg, n=n, cameras=2)
     cam = w.cameras[-1]
