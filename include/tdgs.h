@@ -42,14 +42,15 @@
 extern "C" {
 #endif
 
-#define TDGS_ABI_VERSION 1
+#define TDGS_ABI_VERSION 2
 
 enum {
     TDGS_OK = 0,
     TDGS_ERR_INVALID = 1,     /* bad argument: null pointer, size, degree, tile shape */
     TDGS_ERR_CAPACITY = 2,    /* a caller buffer is too small; the *_out count says how big */
     TDGS_ERR_HIP = 3,         /* a HIP runtime call failed */
-    TDGS_ERR_UNSUPPORTED = 4  /* option combination not implemented */
+    TDGS_ERR_UNSUPPORTED = 4, /* option combination not implemented */
+    TDGS_ERR_DEVICE = 5       /* a kernel detected inconsistent data (reported at a sync point) */
 };
 
 enum { TDGS_TRAINABLE = 0, TDGS_RENDER_ONLY = 1 };
@@ -133,13 +134,23 @@ typedef struct tdgs_render_outputs {
     int32_t* last;   /* h x w last contributing sorted index (1-based, 0 = none) */
 } tdgs_render_outputs;
 
-/* FilteredGaussiansGradientsVector (src/backward_structs.jl:1-93). The four 2D gradient
- * arrays (mean2d 2, opacity 1, inverse covariance lower 3, colour 3) are interleaved per
- * filtered Gaussian as 9 x capacity; the 3D gradient arrays keep the reference layout. */
+/* FilteredGaussiansGradientsVector (src/backward_structs.jl:1-93). The 2D gradients come in
+ * either of two layouts:
+ *   - the reference's four arrays (grads2d null): mean2d_grads 2 x capacity, opacity_grads
+ *     capacity, licov2d_grads (lower [M11, M21, M22]) 3 x capacity, color_grads 3 x capacity,
+ *     exactly as backward_structs.jl:17-22 holds them, so a Julia caller passes its arrays;
+ *   - one interleaved 9 x capacity array (grads2d non-null, the four pointers ignored):
+ *     [dmu_x, dmu_y, da, dM11, dM21, dM22, dr, dg, db] per filtered Gaussian, so the nine
+ *     accumulations of one Gaussian hit one or two cache lines (the faster layout).
+ * The 3D gradient arrays keep the reference layout. */
 typedef struct tdgs_gradients {
     int32_t capacity;
     int32_t sh_degree;          /* storage degree of sh */
-    float* grads2d;             /* 9 x capacity */
+    float* grads2d;             /* 9 x capacity, or null for the four arrays below */
+    float* mean2d_grads;        /* 2 x capacity (used when grads2d is null) */
+    float* opacity_grads;       /* capacity */
+    float* licov2d_grads;       /* 3 x capacity */
+    float* color_grads;         /* 3 x capacity */
     float* mean3d;              /* 3 x capacity */
     float* opacity_feature;     /* capacity */
     float* scaling_features;    /* 3 x capacity */
@@ -206,6 +217,31 @@ int tdgs_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int tdgs_memset(void* dst, int value, size_t bytes, void* stream);
 int tdgs_stream_synchronize(void* stream);
 
+/* Streams, events and pinned host memory, so that a caller without a GPU runtime of its own
+ * can order work as training_step! does with CUDA.jl's task-local stream (training.jl:173-244)
+ * and overlap the ground-truth upload (the copyto! of training.jl:196-201) with kernels: a copy
+ * stream uploads from pinned host memory, an event records the copy, the compute stream waits
+ * on it. Streams are created at the default priority. The reference's CUB call has no stream
+ * argument (cub_sort_pairs_wrapper.cu:37-42); every call here takes one. */
+int tdgs_stream_create(void** stream_out);
+int tdgs_stream_destroy(void* stream);
+int tdgs_event_create(void** event_out);
+int tdgs_event_destroy(void* event);
+int tdgs_event_record(void* event, void* stream);
+int tdgs_stream_wait_event(void* stream, void* event);
+int tdgs_event_synchronize(void* event);
+/* Milliseconds between two recorded events (both complete). */
+int tdgs_event_elapsed_ms(void* start, void* stop, float* ms_out);
+int tdgs_host_malloc(void** ptr_out, size_t bytes);   /* pinned (page-locked) host memory */
+int tdgs_host_free(void* ptr);
+
+/* Synchronises the stream and reports an inconsistency a kernel of an earlier call on this
+ * context detected after that call returned (for example radix-sort counts that disagree
+ * with the keys, which leaves sorted lists incomplete): TDGS_ERR_DEVICE with a message, and
+ * the condition is cleared. Every call of the library that synchronises (tdgs_render,
+ * tdgs_project, tdgs_fill_fgidx_to_gidx, tdgs_scan_counts, tdgs_adc_plan) checks it too. */
+int tdgs_ctx_check(tdgs_ctx* ctx, void* stream);
+
 /* Stage profiler (calling host thread): while enabled, library calls record a pair of HIP
  * events around each stage on the stream they run on (no extra synchronisation). At most
  * max_records stage executions are recorded. tdgs_profile_end waits for the recorded
@@ -215,6 +251,18 @@ int tdgs_profile_begin(int32_t max_records);
 int tdgs_profile_end(double* ms_out, int64_t* executions_out);
 
 /* ---- forward building blocks (each replaces one reference kernel) ------------------- */
+
+/* The first half of render! (forward_core.jl:222-254): fill_keep_gaussians_kernel! (:326-355),
+ * accumulate! + fill_fgidx_to_gidx_kernel! (:231-244, 371-386) and project_fgaussians_kernel!
+ * (:411-517), fused. Writes buf->fgidx_to_gidx (1-based, ascending), and for every filtered
+ * Gaussian with a non-empty bounding box its depth, f2d record, tile rectangle; counts gets
+ * every filtered Gaussian's overlapped-tile count (0 for an empty box; such a Gaussian's f2d
+ * record is written as zeros, its depth and rectangle are left unwritten as in the reference).
+ * buf->keep is written when non-null.
+ * Scratch: buf->temp (tdgs_render_temp_bytes). Synchronises to return N_f. */
+int tdgs_project(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
+                 const tdgs_tiling* tiling, const tdgs_render_options* opt,
+                 tdgs_render_buffers* buf, int32_t* nb_fgaussians_out);
 
 /* fill_keep_gaussians_kernel! (forward_core.jl:326-355): keep[g] = culling test. */
 int tdgs_fill_keep(void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,

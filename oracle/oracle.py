@@ -49,7 +49,14 @@ def lib():
         _LIB.oracle_sort_pairs.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                            C.c_int64, C.c_int32]
         _LIB.oracle_tile_ranges.argtypes = [C.c_int64, C.c_void_p, C.c_int32, C.c_void_p]
+        _LIB.oracle_set_threads.argtypes = [C.c_int32]
     return _LIB
+
+
+def set_threads(n):
+    """Threads of the oracle's per-tile loops (forward images are identical for any count;
+    backward sums in double precision, per thread, added in thread order)."""
+    lib().oracle_set_threads(int(n))
 
 
 def ptr(a):
@@ -134,6 +141,19 @@ def render(g, cam, tiling, opts, *, rgb=True, T=True, depth=True, last=True):
     return res
 
 
+def blend_tile(cam, tiling, opts, f2d, depths, entries, beg, tx, ty, rgb, T, depth, last):
+    """render_tiles_kernel! (forward_core.jl:756-993) for tile (tx, ty) alone: its sorted
+    entries beg, beg + 1, ... are `entries` (1-based fgidx values); writes that tile's pixels
+    of the given full-size images (any may be None)."""
+    entries = np.ascontiguousarray(entries, np.int32)
+    f2d = np.ascontiguousarray(f2d, np.float32)
+    depths = np.ascontiguousarray(depths, np.float32)
+    c_cam, c_t, c_o = cam.to_c(), tiling.to_c(), opts.to_c()
+    lib().oracle_blend_tile(C.byref(c_cam), C.byref(c_t), C.byref(c_o), ptr(f2d), ptr(depths), ptr(entries),
+                            C.c_int64(beg), C.c_int64(beg + entries.size), C.c_int32(tx), C.c_int32(ty),
+                            ptr(rgb), ptr(T), ptr(depth), ptr(last))
+
+
 def fill_fgidx_to_gidx(keep):
     keep = np.ascontiguousarray(keep, dtype=np.uint8)
     n = keep.size
@@ -204,6 +224,34 @@ def backward(g, cam, tiling, opts, fwd, rgb_grad):
         L.oracle_backward_project(C.byref(gaussians_struct(g)), C.byref(c_cam), C.byref(c_o),
                                   C.c_int32(nf), ptr(fwd["fgidx_to_gidx"]), ptr(fwd["f2d"]),
                                   ptr(fwd["counts"]), ptr(grads2d), C.byref(gr))
+    return out
+
+
+def backward_project(g, cam, opts, fwd, grads2d, grads_sh_degree=None):
+    """backward_project_fgaussians_kernel! (backward_core.jl:309-452) alone, from given 2D
+    gradients ((nf, 9) interleaved) and the intermediates of render(); returns the 3D
+    gradients by fgidx."""
+    abi = _abi()
+    nf = fwd["nb_fgaussians"]
+    hg = ((g.sh_degree if grads_sh_degree is None else grads_sh_degree) + 1) ** 2
+    out = {
+        "mean3d": np.zeros((nf, 3), np.float32),
+        "opacity_feature": np.zeros(nf, np.float32),
+        "scaling_features": np.zeros((nf, 3), np.float32),
+        "rotation_features": np.zeros((nf, 4), np.float32),
+        "sh": np.zeros((nf, 3, hg), np.float32),
+    }
+    if nf == 0:
+        return out
+    gr = abi.GradientsC()
+    gr.capacity = nf
+    gr.sh_degree = int(round(hg ** 0.5)) - 1
+    for k in out:
+        setattr(gr, k, out[k].ctypes.data)
+    g2 = np.ascontiguousarray(grads2d[:nf], np.float32)
+    lib().oracle_backward_project(C.byref(gaussians_struct(g)), C.byref(cam.to_c()), C.byref(opts.to_c()),
+                                  C.c_int32(nf), ptr(fwd["fgidx_to_gidx"]), ptr(fwd["f2d"]), ptr(fwd["counts"]),
+                                  ptr(g2), C.byref(gr))
     return out
 
 

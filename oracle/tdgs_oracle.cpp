@@ -40,9 +40,32 @@ inline void gaussian_params(const tdgs_gaussians& g, int64_t gi, float params[7]
     }
 }
 
+// Threads for the per-tile loops (oracle_set_threads). Tiles are independent in the forward
+// pass, so any thread count gives the same images bit for bit; the backward pass sums each
+// thread's contributions in double precision and adds the per-thread sums in thread order.
+int g_threads = 1;
+
+// Runs body(ty) for every tile row ty in [1, nty], tile rows dealt round-robin to threads.
+template <class F>
+void for_tile_rows(int nty, F body) {
+    const int nt = std::max(1, std::min(g_threads, nty));
+    if (nt == 1) {
+        for (int ty = 1; ty <= nty; ++ty) body(ty, 0);
+        return;
+    }
+    std::vector<std::thread> pool;
+    for (int k = 0; k < nt; ++k)
+        pool.emplace_back([&, k]() {
+            for (int ty = 1 + k; ty <= nty; ty += nt) body(ty, k);
+        });
+    for (auto& th : pool) th.join();
+}
+
 }  // namespace
 
 extern "C" {
+
+void oracle_set_threads(int32_t threads) { g_threads = threads > 0 ? threads : 1; }
 
 // fill_keep_gaussians_kernel! (forward_core.jl:326-355).
 void oracle_fill_keep(const tdgs_gaussians* g, const tdgs_camera* cam,
@@ -150,56 +173,71 @@ void oracle_tile_ranges(int64_t m, const int64_t* sorted_keys, int32_t nb_tiles,
         tiles_end[cur - 1] = (int32_t)m;
 }
 
-// render_tiles_kernel! (forward_core.jl:756-993), one pixel at a time.
+// render_tiles_kernel! (forward_core.jl:756-993) for tile (tx, ty), one pixel at a time:
+// entries [beg, end) of the sorted list, entry s being values[s - base].
+static void blend_tile(const tdgs_camera* cam, const tdgs_tiling* t, const tdgs_render_options* opt,
+                       const float* f2d, const float* depths, const int32_t* values, int64_t base, int64_t beg,
+                       int64_t end, int tx, int ty, float* rgb, float* T_img, float* depth_img, int32_t* last_img) {
+    const int W = cam->width, H = cam->height, TW = t->tile_width, TH = t->tile_height;
+    const float u0 = (float)((tx - 1) * TW), v0 = (float)((ty - 1) * TH);
+    for (int pv = 1; pv <= TH; ++pv) {
+        for (int pu = 1; pu <= TW; ++pu) {
+            const int U = pu + (tx - 1) * TW, Vv = pv + (ty - 1) * TH;
+            if (U > W || Vv > H) continue;
+            const float cu = (float)pu - 0.5f, cv = (float)pv - 0.5f;
+            const float uu = cu * cu, uv = cu * cv, vv = cv * cv;
+            float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f}, D = 0.0f;
+            int32_t last = 0;
+            for (int64_t s = beg; s < end; ++s) {
+                const int64_t f = values[s - base] - 1;
+                const float* r = f2d + 9 * f;
+                float p[6];
+                blend_params(r[0], r[1], r[2], r[3], r[4], r[5], u0, v0, p);
+                const float alpha = fminf(opt->max_alpha, exp_f(blend_exponent(p, cu, cv, uu, uv, vv)));
+                if (alpha < opt->min_alpha) continue;
+                const float Tn = T * (1.0f - alpha);
+                if (Tn < opt->min_transmittance) break;
+                const float w = T * alpha;
+                C[0] = fmaf(w, r[6], C[0]);
+                C[1] = fmaf(w, r[7], C[1]);
+                C[2] = fmaf(w, r[8], C[2]);
+                D = fmaf(w, depths[f], D);
+                T = Tn;
+                last = (int32_t)(s + 1);
+            }
+            const int64_t px = (int64_t)(Vv - 1) + (int64_t)H * (U - 1);
+            if (rgb) {
+                rgb[3 * px + 0] = fmaf(T, opt->background[0], C[0]);
+                rgb[3 * px + 1] = fmaf(T, opt->background[1], C[1]);
+                rgb[3 * px + 2] = fmaf(T, opt->background[2], C[2]);
+            }
+            if (T_img) T_img[px] = T;
+            if (depth_img) depth_img[px] = D;
+            if (last_img) last_img[px] = last;
+        }
+    }
+}
+
 void oracle_render_tiles(const tdgs_camera* cam, const tdgs_tiling* t,
                          const tdgs_render_options* opt, const float* f2d, const float* depths,
                          const int32_t* sorted_values, const int32_t* tiles_end,
                          float* rgb, float* T_img, float* depth_img, int32_t* last_img) {
-    const int W = cam->width, H = cam->height, TW = t->tile_width, TH = t->tile_height;
-    for (int ty = 1; ty <= t->nb_tiles_y; ++ty) {
+    for_tile_rows(t->nb_tiles_y, [&](int ty, int) {
         for (int tx = 1; tx <= t->nb_tiles_x; ++tx) {
             const int tile = tx + (ty - 1) * t->nb_tiles_x;
             const int64_t beg = tile == 1 ? 0 : tiles_end[tile - 2];
             const int64_t end = tiles_end[tile - 1];
-            const float u0 = (float)((tx - 1) * TW), v0 = (float)((ty - 1) * TH);
-            for (int pv = 1; pv <= TH; ++pv) {
-                for (int pu = 1; pu <= TW; ++pu) {
-                    const int U = pu + (tx - 1) * TW, Vv = pv + (ty - 1) * TH;
-                    if (U > W || Vv > H) continue;
-                    const float cu = (float)pu - 0.5f, cv = (float)pv - 0.5f;
-                    const float uu = cu * cu, uv = cu * cv, vv = cv * cv;
-                    float T = 1.0f, C[3] = {0.0f, 0.0f, 0.0f}, D = 0.0f;
-                    int32_t last = 0;
-                    for (int64_t s = beg; s < end; ++s) {
-                        const int64_t f = sorted_values[s] - 1;
-                        const float* r = f2d + 9 * f;
-                        float p[6];
-                        blend_params(r[0], r[1], r[2], r[3], r[4], r[5], u0, v0, p);
-                        const float alpha = fminf(opt->max_alpha, exp_f(blend_exponent(p, cu, cv, uu, uv, vv)));
-                        if (alpha < opt->min_alpha) continue;
-                        const float Tn = T * (1.0f - alpha);
-                        if (Tn < opt->min_transmittance) break;
-                        const float w = T * alpha;
-                        C[0] = fmaf(w, r[6], C[0]);
-                        C[1] = fmaf(w, r[7], C[1]);
-                        C[2] = fmaf(w, r[8], C[2]);
-                        D = fmaf(w, depths[f], D);
-                        T = Tn;
-                        last = (int32_t)(s + 1);
-                    }
-                    const int64_t px = (int64_t)(Vv - 1) + (int64_t)H * (U - 1);
-                    if (rgb) {
-                        rgb[3 * px + 0] = fmaf(T, opt->background[0], C[0]);
-                        rgb[3 * px + 1] = fmaf(T, opt->background[1], C[1]);
-                        rgb[3 * px + 2] = fmaf(T, opt->background[2], C[2]);
-                    }
-                    if (T_img) T_img[px] = T;
-                    if (depth_img) depth_img[px] = D;
-                    if (last_img) last_img[px] = last;
-                }
-            }
+            blend_tile(cam, t, opt, f2d, depths, sorted_values, 0, beg, end, tx, ty, rgb, T_img, depth_img, last_img);
         }
-    }
+    });
+}
+
+// The same for one tile whose sorted entries [beg, end) are given as list[0 .. end - beg)
+// (a slice of a sorted list too large to copy whole); writes only that tile's pixels.
+void oracle_blend_tile(const tdgs_camera* cam, const tdgs_tiling* t, const tdgs_render_options* opt,
+                       const float* f2d, const float* depths, const int32_t* list, int64_t beg, int64_t end,
+                       int32_t tx, int32_t ty, float* rgb, float* T_img, float* depth_img, int32_t* last_img) {
+    blend_tile(cam, t, opt, f2d, depths, list, beg, beg, end, tx, ty, rgb, T_img, depth_img, last_img);
 }
 
 // render_void! (forward_structs.jl:743-757).
@@ -256,7 +294,15 @@ void oracle_backward_render_tiles(const tdgs_camera* cam, const tdgs_tiling* t,
                                   const float* rgb_grad, const float* T_img,
                                   const int32_t* last_img, double* grads2d_acc) {
     const int W = cam->width, H = cam->height, TW = t->tile_width, TH = t->tile_height;
-    for (int ty = 1; ty <= t->nb_tiles_y; ++ty) {
+    // nb_f is not passed: the accumulator covers the largest referenced fgidx
+    int64_t nb_f = 0;
+    const int64_t m = tiles_end[(int64_t)t->nb_tiles_x * t->nb_tiles_y - 1];
+    for (int64_t s = 0; s < m; ++s) nb_f = std::max<int64_t>(nb_f, sorted_values[s]);
+    const int nt = std::max(1, std::min(g_threads, t->nb_tiles_y));
+    std::vector<std::vector<double>> part(nt > 1 ? nt : 0);
+    for (auto& p : part) p.assign(9 * nb_f, 0.0);
+    for_tile_rows(t->nb_tiles_y, [&](int ty, int k) {
+        double* acc = nt > 1 ? part[k].data() : grads2d_acc;
         for (int tx = 1; tx <= t->nb_tiles_x; ++tx) {
             const int tile = tx + (ty - 1) * t->nb_tiles_x;
             const int64_t first = tile == 1 ? 1 : (int64_t)tiles_end[tile - 2] + 1;
@@ -281,12 +327,14 @@ void oracle_backward_render_tiles(const tdgs_camera* cam, const tdgs_tiling* t,
                         if (alpha < opt->min_alpha) continue;
                         float o[9];
                         backward_pair(alpha, 1.0f / (1.0f - alpha), G, du, dv, r[3], r[4], r[5], r + 6, g, &T, psi, o);
-                        for (int k = 0; k < 9; ++k) grads2d_acc[9 * f + k] += (double)o[k];
+                        for (int k = 0; k < 9; ++k) acc[9 * f + k] += (double)o[k];
                     }
                 }
             }
         }
-    }
+    });
+    for (int k = 0; k < (int)part.size(); ++k)
+        for (int64_t i = 0; i < 9 * nb_f; ++i) grads2d_acc[i] += part[k][i];
 }
 
 // backward_project_fgaussians_kernel! (backward_core.jl:309-452) + compute_sh_coeffs_grad!

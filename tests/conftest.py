@@ -29,6 +29,9 @@ def oracle():
     import build as oracle_build  # oracle/build.py
     oracle_build.build(force=False)
     import oracle as orc
+    # per-tile loops on up to 16 host threads (the GPU box's CPU share); images do not depend
+    # on the thread count
+    orc.set_threads(min(16, os.cpu_count() or 1))
     return orc
 
 

@@ -43,7 +43,7 @@ def test_every_declared_function_is_exported(lib):
 
 
 def test_abi_version(lib):
-    assert lib.tdgs_abi_version() == 1
+    assert lib.tdgs_abi_version() == 2
 
 
 def test_argument_validation_without_gpu(lib):
@@ -84,3 +84,37 @@ def test_ctypes_mirrors_match_header_layout(tmp_path):
         assert int(got[cname]) == C.sizeof(py), cname
         for fname, _ in py._fields_:
             assert int(got[f"{cname}.{fname}"]) == getattr(py, fname).offset, (cname, fname)
+
+
+def test_new_entry_points_validate_without_gpu(lib):
+    """Argument checks of tdgs_project, the stream/event plumbing, tdgs_ctx_check and the 2D
+    gradient layouts run before any HIP call."""
+    assert lib.tdgs_project(None, None, None, None, None, None, None, None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_stream_create(None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_stream_destroy(None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_event_create(None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_event_record(None, None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_stream_wait_event(None, None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_event_synchronize(None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_event_elapsed_ms(None, None, None) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_host_malloc(None, C.c_size_t(16)) == abi.TDGS_ERR_INVALID
+    assert lib.tdgs_ctx_check(None, None) == abi.TDGS_ERR_INVALID
+    # backward blending with neither 2D gradient layout
+    cam = abi.Camera(width=32, height=32)
+    tiling = abi.TilingC(16, 16, 2, 2)
+    opts = abi.RenderOptionsC(min_alpha=1 / 255, max_alpha=0.99, min_transmittance=1e-4)
+    gr = abi.GradientsC(capacity=4, sh_degree=0)
+    gr.mean2d_grads = 0x1000   # three of the four reference arrays only
+    gr.opacity_grads = 0x1000
+    gr.licov2d_grads = 0x1000
+    dummy = C.c_void_p(0x1000)
+    out = abi.RenderOutputsC(None, 0x1000, None, 0x1000)
+    buf = abi.RenderBuffersC()
+    rc = lib.tdgs_backward_render_tiles(None, C.byref(gr), dummy, C.byref(out), C.byref(cam), C.byref(tiling),
+                                        C.byref(opts), C.byref(buf))
+    assert rc == abi.TDGS_ERR_INVALID and b"color_grads" in lib.tdgs_last_error()
+    # tiles of more than 1024 pixels
+    big = abi.TilingC(40, 40, 1, 1)
+    cam40 = abi.Camera(width=40, height=40)
+    rc = lib.tdgs_render_tiles(None, C.byref(cam40), C.byref(big), C.byref(opts), C.byref(buf), C.byref(out))
+    assert rc == abi.TDGS_ERR_INVALID and b"1024" in lib.tdgs_last_error()

@@ -68,18 +68,27 @@ def test_backward_test_scene(gpu, oracle, deg):
                 np.testing.assert_allclose(np.atleast_1d(v), np.atleast_1d(r), rtol=1e-2)
 
 
-@pytest.mark.parametrize("cfg,n,tile,exact", [(1, 20_000, (16, 16), False), (1, 20_000, (16, 16), True),
-                                              (2, 60_000, (16, 32), False), (0, None, (16, 16), False),
-                                              (0, None, (32, 32), False), (0, None, (8, 8), False),
-                                              # 192 pixels: 128 threads, so the second pixel of
-                                              # lanes 64-127 lies past the tile
-                                              (0, None, (24, 8), False), (0, None, (8, 24), False)])
-def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact):
+AA = {"use_antialiasing": True}
+FILTER = {"clip_mode": 1}   # TDGS_CLIP_FILTER (BoundaryFilter)
+
+
+@pytest.mark.parametrize("cfg,n,tile,exact,extra", [
+    (1, 20_000, (16, 16), False, {}), (1, 20_000, (16, 16), True, {}),
+    (2, 60_000, (16, 32), False, {}), (0, None, (16, 16), False, {}),
+    (0, None, (32, 32), False, {}), (0, None, (8, 8), False, {}),
+    # 192 pixels: 128 threads, so the second pixel of lanes 64-127 lies past the tile
+    (0, None, (24, 8), False, {}), (0, None, (8, 24), False, {}),
+    # antialiasing (forward_core.jl:450-462, backward_core.jl:331-341, 480) and the
+    # BoundaryFilter clip mode (forward_core.jl:343, backward_core.jl:373-381)
+    (1, 20_000, (16, 16), False, AA), (2, 60_000, (16, 16), False, AA),
+    (1, 20_000, (16, 16), False, FILTER), (2, 60_000, (16, 16), False, FILTER),
+    (2, 60_000, (16, 16), True, {**AA, **FILTER})])
+def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact, extra):
     w = synthetic.config(cfg, n=n, cameras=2)
     cam = w.cameras[-1]
     t = host.Tiling.for_camera(cam, *tile)
     opts = host.RenderOptions.for_camera(cam, w.gaussians.sh_degree, background_color=(0.2, 0.1, 0.3),
-                                         exact_sh_jacobian=exact)
+                                         exact_sh_jacobian=exact, **extra)
     gen = torch.Generator(device="cuda").manual_seed(7)
 
     def rand_grad(rgb):

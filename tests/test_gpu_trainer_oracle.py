@@ -1,0 +1,107 @@
+"""training_step! on the GPU against the same steps driven through the CPU oracle.
+
+The Trainer (training.jl:173-244) runs eight iterations across a density-control step (the
+ADC at iteration 600) with the optimiser fused into the backward projection and without.
+Each iteration is replayed on the CPU with the oracle's functions in the reference's order:
+render! (checked bit for bit against the GPU's image), the backward projection from the GPU's
+2D gradients of that iteration, the ADC statistics, at iteration 600 the masks, compaction
+(same split sampler and seed) and fgidx remap, the annealed means learning rate, and update!.
+The Gaussians, the Adam moments and the update count must then equal the GPU's bit for bit
+after every iteration: this pins the step's orchestration (what runs, in which order, on which
+index maps). The 2D gradients are the GPU's own because the float atomics of backward blending
+sum in a different order than the oracle (that kernel is checked at relative L2 1e-3
+elsewhere); everything downstream of them is deterministic.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tdgs_amd import host, synthetic, training
+
+pytestmark = pytest.mark.gpu
+
+
+def _host_state(tr):
+    g = tr.gaussians.to_host()
+    m = tr.optimizer.moments
+    adam = {k: getattr(m, k).cpu().numpy() for k in ("means", "opacity", "scaling", "rotation", "sh")}
+    return g, adam
+
+
+@pytest.mark.parametrize("fuse", [True, False])
+def test_trainer_steps_match_oracle_driven_steps(gpu, oracle, monkeypatch, fuse):
+    w = synthetic.config(3, n=20_000, cameras=4)
+    cams = w.cameras
+    tiling = synthetic.tiling_for(w, cams[0])
+    g0 = gpu.TrainableGaussiansVector.from_host(w.gaussians, 0)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    images = [torch.rand((c.width, c.height, 3), generator=gen, device="cuda") for c in cams]
+    ropts = host.RenderOptions.for_camera(cams[0], 3)
+    # thresholds that make iteration 600 prune, clone and split some of 20k Gaussians
+    to = training.TrainingOptions.for_scene(host.scene_radius(cams), nb_iterations=3000,
+                                            densification_mean2d_grad_norm_threshold_ndc=1e-6,
+                                            base_densification_size_threshold=0.003, pruning_min_opacity=0.1)
+    tr = training.Trainer(g0, cams, images, ropts, tiling, to, seed=9, fuse_optimizer=fuse)
+    tr.iteration_nb = 595
+
+    captured = []
+    orig_b2, orig_b = training.backward_render_tiles_, training.backward_
+
+    def cap_b2(fg, grad, out, cam, t, o, buf):
+        r = orig_b2(fg, grad, out, cam, t, o, buf)
+        captured.append(fg.grads2d_matrix(buf.nb_fgaussians).cpu().numpy().copy())
+        return r
+
+    def cap_b(fg, grad, out, g, cam, t, o, buf):
+        r = orig_b(fg, grad, out, g, cam, t, o, buf)
+        captured.append(fg.grads2d_matrix(buf.nb_fgaussians).cpu().numpy().copy())
+        return r
+
+    monkeypatch.setattr(training, "backward_render_tiles_", cap_b2)
+    monkeypatch.setattr(training, "backward_", cap_b)
+
+    g, moments = _host_state(tr)
+    adam = oracle.AdamHost(len(g.means_opacity), 3, tr.optimizer.moments.lrs())
+    for k, v in moments.items():
+        getattr(adam, k)[...] = v
+    adc = oracle.AdcHost(len(g.means_opacity))
+    f32 = np.float32
+    adc_steps = 0
+    for step in range(8):
+        tr.training_step_()
+        torch.cuda.synchronize()
+        it = tr.iteration_nb
+        cam = tr.last_camera
+        assert len(captured) == step + 1
+        g2 = captured[-1]
+        fwd = oracle.render(g, cam, tiling, ropts)
+        nf = fwd["nb_fgaussians"]
+        assert g2.shape[0] == nf
+        np.testing.assert_array_equal(tr.render_outputs.rgb.cpu().numpy(), fwd["rgb"])
+        grads = oracle.backward_project(g, cam, ropts, fwd, g2)
+        f2g = fwd["fgidx_to_gidx"][:nf]
+        oracle.adc_stats(adc, g2, f2g, cam.width, cam.height)
+        if it % to.adc_interval == 0 and to.adc_start_iteration_nb <= it <= to.adc_final_iteration_nb:
+            n_new = oracle.adc_plan(adc, g, float(host.logit32(to.pruning_min_opacity)),
+                                    it > to.opacity_reset_interval, float(np.log(f32(to.pruning_3d_max_scale))),
+                                    to.densification_mean2d_grad_norm_threshold_ndc,
+                                    float(np.log(f32(to.densification_size_threshold))))
+            n_old = len(g.means_opacity)
+            assert int(adc.prune.sum()) > 0 and int((adc.densify & adc.clone).sum()) > 0
+            assert int((adc.densify & ~adc.clone.astype(bool)).sum()) > 0
+            g, adam = oracle.adc_apply(adc, g, adam, float(np.log(f32(to.splitting_scale_factor))),
+                                       tr.seed * 1_000_003 + it)
+            f2g = oracle.adc_remap_fgidx(adc, f2g)
+            adc = oracle.AdcHost(n_new)
+            adc_steps += 1
+            assert len(g.means_opacity) == n_new != n_old
+        adam.lrs[0] = training.annealed_means_lr(it, to)
+        oracle.adam_step(g, adam, grads, f2g, ropts.sh_degree)
+        got_g, got_m = _host_state(tr)
+        for k in ("means_opacity", "scaling", "rotation", "sh"):
+            np.testing.assert_array_equal(getattr(got_g, k), getattr(g, k), err_msg=f"iteration {it}: {k}")
+        for k in ("means", "opacity", "scaling", "rotation", "sh"):
+            np.testing.assert_array_equal(got_m[k], getattr(adam, k), err_msg=f"iteration {it}: moments {k}")
+        assert tr.optimizer.update_count == adam.update_count
+        assert tr.optimizer.moments.means_lr == adam.lrs[0]
+    assert adc_steps == 1

@@ -10,6 +10,7 @@ TDGS_ERR_INVALID = 1
 TDGS_ERR_CAPACITY = 2
 TDGS_ERR_HIP = 3
 TDGS_ERR_UNSUPPORTED = 4
+TDGS_ERR_DEVICE = 5
 
 TDGS_TRAINABLE = 0
 TDGS_RENDER_ONLY = 1
@@ -66,7 +67,8 @@ class RenderOutputsC(C.Structure):
 
 class GradientsC(C.Structure):
     _fields_ = [("capacity", C.c_int32), ("sh_degree", C.c_int32), ("grads2d", C.c_void_p),
-                ("mean3d", C.c_void_p), ("opacity_feature", C.c_void_p),
+                ("mean2d_grads", C.c_void_p), ("opacity_grads", C.c_void_p), ("licov2d_grads", C.c_void_p),
+                ("color_grads", C.c_void_p), ("mean3d", C.c_void_p), ("opacity_feature", C.c_void_p),
                 ("scaling_features", C.c_void_p), ("rotation_features", C.c_void_p),
                 ("sh", C.c_void_p)]
 

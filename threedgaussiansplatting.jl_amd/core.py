@@ -311,6 +311,25 @@ def render_(outputs: RenderOutputs, gaussians, camera: PinholeCamera, tiling: Ti
     return outputs
 
 
+def project_(gaussians, camera: PinholeCamera, tiling: Tiling, options: RenderOptions, buffers: RenderBuffers):
+    """The cull, compaction and projection half of render! (forward_core.jl:222-254, kernels
+    :326-355, 371-386, 411-517) as one call (tdgs_project): fills buffers' keep flags (when
+    allocated), fgidx_to_gidx, depths, f2d, tile_ranges and counts; returns N_f."""
+    dev = gaussians.device.index
+    buffers.ensure_capacity(len(gaussians))
+    nbf = C.c_int32(0)
+    check(lib().tdgs_project(context(dev), stream_ptr(dev), C.byref(gaussians.struct()), C.byref(camera.to_c()),
+                             C.byref(tiling.to_c()), C.byref(options.to_c()), C.byref(buffers.struct()),
+                             C.byref(nbf)))
+    buffers.nb_fgaussians = int(nbf.value)
+    return buffers.nb_fgaussians
+
+
+def ctx_check(device=0):
+    """tdgs_ctx_check: synchronise and raise on a device-side error flag of the context."""
+    check(lib().tdgs_ctx_check(context(device), stream_ptr(device)))
+
+
 # ------------------------------------------------------------------------------------
 # Building blocks (one reference kernel each)
 # ------------------------------------------------------------------------------------
@@ -391,43 +410,68 @@ def image_to_rgb8(image: torch.Tensor, kind=abi.TDGS_IMAGE_RGB, min_depth=0.0, m
 
 class FilteredGaussiansGradientsVector:
     """FilteredGaussiansGradientsVector (src/backward_structs.jl:1-156): per filtered Gaussian
-    2D gradients (9 interleaved: mean2d 2, opacity 1, inverse covariance lower 3, colour 3)
-    and 3D gradients in the reference layouts."""
+    2D gradients and 3D gradients in the reference layouts.
 
-    def __init__(self, capacity, sh_degree, device=0):
+    The 2D gradients are either interleaved (layout="interleaved", the default: one (n, 9)
+    array [mean2d 2, opacity 1, inverse covariance lower 3, colour 3], the faster layout) or
+    the reference's four arrays (layout="reference": mean2d_grads 2 x n, opacity_grads n,
+    licov2d_grads 3 x n, color_grads 3 x n, backward_structs.jl:17-22)."""
+
+    def __init__(self, capacity, sh_degree, device=0, layout="interleaved"):
         d = _dev(device)
         cap = max(int(capacity), 1)
         h = (int(sh_degree) + 1) ** 2
+        if layout not in ("interleaved", "reference"):
+            raise ValueError(f"unknown 2D gradient layout {layout!r}")
+        self.layout = layout
         self.capacity = cap
         self.sh_degree = int(sh_degree)
-        self.grads2d = torch.zeros((cap, 9), dtype=torch.float32, device=d)
+        if layout == "interleaved":
+            self.grads2d = torch.zeros((cap, 9), dtype=torch.float32, device=d)
+            self.mean2d = self.grads2d[:, 0:2]
+            self.opacity = self.grads2d[:, 2]
+            self.licov2d = self.grads2d[:, 3:6]
+            self.color = self.grads2d[:, 6:9]
+        else:
+            self.grads2d = None
+            self.mean2d = torch.zeros((cap, 2), dtype=torch.float32, device=d)
+            self.opacity = torch.zeros(cap, dtype=torch.float32, device=d)
+            self.licov2d = torch.zeros((cap, 3), dtype=torch.float32, device=d)
+            self.color = torch.zeros((cap, 3), dtype=torch.float32, device=d)
         self.mean3d = torch.zeros((cap, 3), dtype=torch.float32, device=d)
         self.opacity_feature = torch.zeros(cap, dtype=torch.float32, device=d)
         self.scaling_features = torch.zeros((cap, 3), dtype=torch.float32, device=d)
         self.rotation_features = torch.zeros((cap, 4), dtype=torch.float32, device=d)
         self.sh = torch.zeros((cap, 3, h), dtype=torch.float32, device=d)
 
-    @property
-    def mean2d(self):
-        return self.grads2d[:, 0:2]
+    def grads2d_matrix(self, n=None):
+        """The 2D gradients of the first n filtered Gaussians as one (n, 9) tensor (a copy for
+        the reference layout)."""
+        n = self.capacity if n is None else n
+        if self.grads2d is not None:
+            return self.grads2d[:n]
+        return torch.cat([self.mean2d[:n], self.opacity[:n, None], self.licov2d[:n], self.color[:n]], dim=1)
 
-    @property
-    def opacity(self):
-        return self.grads2d[:, 2]
-
-    @property
-    def licov2d(self):
-        return self.grads2d[:, 3:6]
-
-    @property
-    def color(self):
-        return self.grads2d[:, 6:9]
+    def zero_2d_(self, n):
+        """zero_2d_grads! (backward_structs.jl:250-257) on the first n entries."""
+        if self.grads2d is not None:
+            self.grads2d[:n].zero_()
+        else:
+            for t in (self.mean2d, self.opacity, self.licov2d, self.color):
+                t[:n].zero_()
 
     def struct(self):
         s = abi.GradientsC()
         s.capacity = self.capacity
         s.sh_degree = self.sh_degree
-        s.grads2d = dptr(self.grads2d)
+        if self.grads2d is not None:
+            s.grads2d = dptr(self.grads2d)
+        else:
+            s.grads2d = None
+            s.mean2d_grads = dptr(self.mean2d)
+            s.opacity_grads = dptr(self.opacity)
+            s.licov2d_grads = dptr(self.licov2d)
+            s.color_grads = dptr(self.color)
         s.mean3d = dptr(self.mean3d)
         s.opacity_feature = dptr(self.opacity_feature)
         s.scaling_features = dptr(self.scaling_features)
@@ -446,7 +490,7 @@ def backward_render_tiles_(fgradients: FilteredGaussiansGradientsVector, rgb_ima
     nbf = buffers.nb_fgaussians
     if nbf <= 0:
         return fgradients
-    fgradients.grads2d[:nbf].zero_()
+    fgradients.zero_2d_(nbf)
     check(lib().tdgs_backward_render_tiles(stream_ptr(dev), C.byref(fgradients.struct()),
                                            C.c_void_p(dptr(rgb_image_grad)), C.byref(outputs.struct()),
                                            C.byref(camera.to_c()), C.byref(tiling.to_c()), C.byref(options.to_c()),

@@ -132,9 +132,12 @@ struct BackBlendArgs {
     const float* rgb_grad;
     const float* T;
     const int32_t* last;
-    float* grads2d;
+    Grads2D g2;
 };
 
+// SEP: the 2D gradients are the reference's four arrays (component addresses by select);
+// otherwise the interleaved 9 x capacity array (base[0] + 9 f + k).
+template <bool SEP>
 __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
     extern __shared__ float4 s_raw4[];
     // Two pixels per lane: thread t takes pixels t and t + NB of the tile (NB = blockDim.x =
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
             } else if (k == 4) {
                 v = -v;
             }
-            if (v != 0.0f) unsafeAtomicAdd(a.grads2d + 9 * f + k, v);
+            if (v != 0.0f) unsafeAtomicAdd(SEP ? a.g2.at_dynamic(k, f) : a.g2.base[0] + 9 * f + k, v);
         }
         __syncthreads();
         for (int i = t; i < 9 * nb; i += NB) s_acc[i] = 0.0f;   // the next batch sums after its barrier
@@ -340,6 +343,7 @@ struct BackProjectArgs {
     const float* f2d;
     const int32_t* counts;
     tdgs_gradients gr;
+    Grads2D g2;
     AdamInPlace adam;
 };
 
@@ -505,9 +509,8 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
         const float* r = a.f2d + 9 * f;
         in.mux = r[0]; in.muy = r[1]; in.a = r[2]; in.m11 = r[3]; in.m21 = r[4]; in.m22 = r[5];
         in.rgb[0] = r[6]; in.rgb[1] = r[7]; in.rgb[2] = r[8];
-        const float* g2 = a.gr.grads2d + 9 * f;
 #pragma unroll
-        for (int k = 0; k < 9; ++k) in.g2[k] = g2[k];
+        for (int k = 0; k < 9; ++k) in.g2[k] = *a.g2.at(k, f);
         const BackwardProjectOut o = backward_project(in, a.cam, a.opt);
         if (ADAM) {
             adam_geometry(a, gi, o.dm, o.dlogit, o.dlogs, o.dq);
@@ -610,10 +613,28 @@ static int check_gradients(const tdgs_gradients* gr, int64_t nbf, int data_degre
     TDGS_REQUIRE(gr->capacity >= nbf, "gradient buffers hold %d, need %lld", gr->capacity, (long long)nbf);
     TDGS_REQUIRE(gr->sh_degree >= 0 && gr->sh_degree <= 3, "bad gradient SH degree");
     (void)data_degree;
-    if (nbf > 0)
-        TDGS_REQUIRE(gr->grads2d && gr->mean3d && gr->opacity_feature && gr->scaling_features &&
-                         gr->rotation_features && gr->sh,
+    if (nbf > 0) {
+        Grads2D v;
+        TDGS_TRY(grads2d_view(gr, &v));
+        TDGS_REQUIRE(gr->mean3d && gr->opacity_feature && gr->scaling_features && gr->rotation_features && gr->sh,
                      "null gradient arrays");
+    }
+    return TDGS_OK;
+}
+
+// zero_2d_grads! (backward_structs.jl:250-257) on the first nbf entries.
+static int zero_grads2d(hipStream_t s, const tdgs_gradients* gr, int64_t nbf) {
+    if (gr->grads2d) {
+        k_zero_f32<<<(unsigned)ceil_div(9 * nbf, 256), 256, 0, s>>>(gr->grads2d, 9 * nbf);
+        TDGS_LAUNCHED();
+        return TDGS_OK;
+    }
+    float* const arr[4] = {gr->mean2d_grads, gr->opacity_grads, gr->licov2d_grads, gr->color_grads};
+    const int comps[4] = {2, 1, 3, 3};
+    for (int k = 0; k < 4; ++k) {
+        k_zero_f32<<<(unsigned)ceil_div(comps[k] * nbf, 256), 256, 0, s>>>(arr[k], comps[k] * nbf);
+        TDGS_LAUNCHED();
+    }
     return TDGS_OK;
 }
 
@@ -628,8 +649,10 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
                                const tdgs_tiling* tiling, const tdgs_render_options* opt,
                                const tdgs_render_buffers* buf) {
     TDGS_TRY(check_tiling(tiling, cam));
-    TDGS_REQUIRE(grads && grads->grads2d && rgb_grad && out && out->T && out->last && opt && buf,
+    TDGS_REQUIRE(grads && rgb_grad && out && out->T && out->last && opt && buf,
                  "backward blending needs gradients, rgb_grad, T and last");
+    Grads2D g2v;
+    TDGS_TRY(grads2d_view(grads, &g2v));
     TDGS_REQUIRE(buf->tiles_end && buf->sorted_values && buf->f2d, "null render buffers");
     TDGS_TRY(check_thresholds(opt));
     hipStream_t s = (hipStream_t)stream;
@@ -642,12 +665,15 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
     a.log_min_alpha = opt->min_alpha > 0.0f ? (float)(std::log((double)opt->min_alpha) - 1e-3) : -__builtin_inff();
     a.m = buf->key_capacity;
     a.tiles_end = buf->tiles_end; a.sorted_f = buf->sorted_values; a.f2d = buf->f2d;
-    a.rgb_grad = rgb_grad; a.T = out->T; a.last = out->last; a.grads2d = grads->grads2d;
+    a.rgb_grad = rgb_grad; a.T = out->T; a.last = out->last; a.g2 = g2v;
     // two pixels per thread, in whole wavefronts (the transpose-sum reads all 64 lanes; the
-    // tile's pixel count is a multiple of 64, so half of it is one of 32)
-    const int nt = (tiling->tile_width * tiling->tile_height / 2 + kWave - 1) / kWave * kWave;
+    // pixels past the tile's are off)
+    const int nt = ((tiling->tile_width * tiling->tile_height + 1) / 2 + kWave - 1) / kWave * kWave;
     const size_t lds = (size_t)nt * (sizeof(BackRec) + 9 * sizeof(float));
-    k_backward_blend<<<dim3(tiling->nb_tiles_x, tiling->nb_tiles_y), nt, lds, s>>>(a);
+    if (grads->grads2d)
+        k_backward_blend<false><<<dim3(tiling->nb_tiles_x, tiling->nb_tiles_y), nt, lds, s>>>(a);
+    else
+        k_backward_blend<true><<<dim3(tiling->nb_tiles_x, tiling->nb_tiles_y), nt, lds, s>>>(a);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
@@ -666,6 +692,7 @@ int tdgs_backward_project(void* stream, tdgs_gradients* grads, const tdgs_gaussi
     BackProjectArgs a;
     a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nb_fgaussians;
     a.fgidx_to_gidx = buf->fgidx_to_gidx; a.f2d = buf->f2d; a.counts = buf->counts; a.gr = *grads;
+    TDGS_TRY(grads2d_view(grads, &a.g2));
     k_backward_project<false><<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(a);
     TDGS_LAUNCHED();
     return TDGS_OK;
@@ -681,14 +708,15 @@ int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_g
     TDGS_REQUIRE(grads->sh_degree >= opt->sh_degree, "gradient SH storage below the render degree");
     TDGS_REQUIRE(st && cam && buf && buf->fgidx_to_gidx && buf->f2d && buf->counts, "null arguments");
     if (nb_fgaussians > 0) {
-        TDGS_REQUIRE(grads->grads2d && st->means_moments && st->opacity_moments && st->scaling_moments &&
-                         st->rotation_moments && st->sh_moments,
+        TDGS_REQUIRE(st->means_moments && st->opacity_moments && st->scaling_moments && st->rotation_moments &&
+                         st->sh_moments,
                      "null arrays");
         hipStream_t s = (hipStream_t)stream;
         StageScope sc(TDGS_STAGE_BACKWARD_PROJECT, s);
         BackProjectArgs a;
         a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nb_fgaussians;
         a.fgidx_to_gidx = buf->fgidx_to_gidx; a.f2d = buf->f2d; a.counts = buf->counts; a.gr = *grads;
+        TDGS_TRY(grads2d_view(grads, &a.g2));
         AdamInPlace& d = a.adam;
         d.m_means = st->means_moments; d.m_op = st->opacity_moments; d.m_sc = st->scaling_moments;
         d.m_rot = st->rotation_moments; d.m_sh = st->sh_moments;
@@ -713,9 +741,7 @@ int tdgs_backward(void* stream, tdgs_gradients* grads, const float* rgb_grad, co
     TDGS_TRY(check_gradients(grads, nb_fgaussians, g ? g->sh_degree : 0));
     if (nb_fgaussians <= 0) return TDGS_OK;
     hipStream_t s = (hipStream_t)stream;
-    const int64_t n2 = 9 * (int64_t)nb_fgaussians;
-    k_zero_f32<<<(unsigned)ceil_div(n2, 256), 256, 0, s>>>(grads->grads2d, n2);  // zero_2d_grads!
-    TDGS_LAUNCHED();
+    TDGS_TRY(zero_grads2d(s, grads, nb_fgaussians));
     TDGS_TRY(tdgs_backward_render_tiles(stream, grads, rgb_grad, out, cam, tiling, opt, buf));
     return tdgs_backward_project(stream, grads, g, cam, opt, buf, nb_fgaussians);
 }

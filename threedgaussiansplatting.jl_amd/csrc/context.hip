@@ -22,10 +22,22 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line) {
     return TDGS_ERR_HIP;
 }
 
-int read_counters(tdgs_ctx* ctx, hipStream_t stream, int count) {
-    TDGS_HIP(hipMemcpyAsync(ctx->h_counters, ctx->d_counters, sizeof(int64_t) * count,
+int read_counters(tdgs_ctx* ctx, hipStream_t stream) {
+    TDGS_HIP(hipMemcpyAsync(ctx->h_counters, ctx->d_counters, sizeof(int64_t) * kCounters,
                             hipMemcpyDeviceToHost, stream));
     TDGS_HIP(hipStreamSynchronize(stream));
+    const uint32_t flags = (uint32_t)ctx->h_counters[kErrSlot];
+    if (flags != 0) {
+        TDGS_HIP(hipMemsetAsync(ctx->d_counters + kErrSlot, 0, sizeof(int64_t), stream));
+        TDGS_HIP(hipStreamSynchronize(stream));
+        ctx->h_counters[kErrSlot] = 0;
+        if (flags & kErrSortCounts)
+            set_error("a radix sort on this context found counts that disagree with its keys; the sorted "
+                      "lists of that call are incomplete (device flags 0x%x)", flags);
+        else
+            set_error("device error flags 0x%x raised on this context", flags);
+        return TDGS_ERR_DEVICE;
+    }
     return TDGS_OK;
 }
 
@@ -163,6 +175,77 @@ int tdgs_profile_end(double* ms_out, int64_t* executions_out) {
 int tdgs_stream_synchronize(void* stream) {
     TDGS_HIP(hipStreamSynchronize((hipStream_t)stream));
     return TDGS_OK;
+}
+
+int tdgs_stream_create(void** stream_out) {
+    TDGS_REQUIRE(stream_out, "null output");
+    *stream_out = nullptr;
+    hipStream_t s;
+    TDGS_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));   // default priority
+    *stream_out = (void*)s;
+    return TDGS_OK;
+}
+
+int tdgs_stream_destroy(void* stream) {
+    TDGS_REQUIRE(stream, "null stream (the default stream is not destroyed)");
+    TDGS_HIP(hipStreamDestroy((hipStream_t)stream));
+    return TDGS_OK;
+}
+
+int tdgs_event_create(void** event_out) {
+    TDGS_REQUIRE(event_out, "null output");
+    *event_out = nullptr;
+    hipEvent_t e;
+    TDGS_HIP(hipEventCreate(&e));
+    *event_out = (void*)e;
+    return TDGS_OK;
+}
+
+int tdgs_event_destroy(void* event) {
+    TDGS_REQUIRE(event, "null event");
+    TDGS_HIP(hipEventDestroy((hipEvent_t)event));
+    return TDGS_OK;
+}
+
+int tdgs_event_record(void* event, void* stream) {
+    TDGS_REQUIRE(event, "null event");
+    TDGS_HIP(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+    return TDGS_OK;
+}
+
+int tdgs_stream_wait_event(void* stream, void* event) {
+    TDGS_REQUIRE(event, "null event");
+    TDGS_HIP(hipStreamWaitEvent((hipStream_t)stream, (hipEvent_t)event, 0));
+    return TDGS_OK;
+}
+
+int tdgs_event_synchronize(void* event) {
+    TDGS_REQUIRE(event, "null event");
+    TDGS_HIP(hipEventSynchronize((hipEvent_t)event));
+    return TDGS_OK;
+}
+
+int tdgs_event_elapsed_ms(void* start, void* stop, float* ms_out) {
+    TDGS_REQUIRE(start && stop && ms_out, "null arguments");
+    TDGS_HIP(hipEventElapsedTime(ms_out, (hipEvent_t)start, (hipEvent_t)stop));
+    return TDGS_OK;
+}
+
+int tdgs_host_malloc(void** ptr_out, size_t bytes) {
+    TDGS_REQUIRE(ptr_out, "null output");
+    *ptr_out = nullptr;
+    TDGS_HIP(hipHostMalloc(ptr_out, bytes > 0 ? bytes : 1, hipHostMallocDefault));
+    return TDGS_OK;
+}
+
+int tdgs_host_free(void* ptr) {
+    if (ptr) TDGS_HIP(hipHostFree(ptr));
+    return TDGS_OK;
+}
+
+int tdgs_ctx_check(tdgs_ctx* ctx, void* stream) {
+    TDGS_REQUIRE(ctx, "null ctx");
+    return read_counters(ctx, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1114,11 +1114,119 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(ceil_div(key_cap, kEmitTile) + 2);  // first Gaussian of each emission block
 }
 
+// The scratch arrays of tdgs_render / tdgs_project inside buf->temp (render_layout's order).
+struct RenderScratch {
+    uint32_t *dkey, *dkey_alt, *dkey_sorted;
+    int32_t *dval, *dval_alt, *sorted_f, *cs;
+    void* stemp;
+    size_t sbytes;
+    int32_t *block_counts, *group_counts;
+    void* rtemp;
+    size_t rbytes;
+    int32_t* rect_diff;
+    int64_t ndiff;
+    int32_t* blk_first;
+    int64_t nblk;
+};
+
+static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const tdgs_tiling* tiling) {
+    RenderScratch r;
+    const int64_t cap = buf->capacity;
+    Arena ar(buf->temp, buf->temp_bytes);
+    ar.take<int64_t>(kCounters);
+    r.dkey = ar.take<uint32_t>(cap);
+    r.dkey_alt = ar.take<uint32_t>(cap);
+    r.dkey_sorted = ar.take<uint32_t>(cap);
+    r.dval = ar.take<int32_t>(cap);
+    r.dval_alt = ar.take<int32_t>(cap);
+    r.sorted_f = ar.take<int32_t>(cap);
+    r.cs = ar.take<int32_t>(cap);
+    r.sbytes = scan_temp_bytes_for(cap);
+    r.stemp = ar.take<char>((int64_t)r.sbytes);
+    r.block_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub) * kKeepSub);
+    r.group_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub));
+    const int64_t big = cap > buf->key_capacity ? cap : buf->key_capacity;
+    r.rbytes = radix_temp_bytes(big);
+    r.rtemp = ar.take<char>((int64_t)r.rbytes);
+    r.ndiff = rect_diff_size(tiling);
+    r.rect_diff = ar.take<int32_t>(kRectCopies * r.ndiff);
+    r.nblk = ceil_div(buf->key_capacity, kEmitTile) + 2;
+    r.blk_first = ar.take<int32_t>(r.nblk);
+    return r;
+}
+
+// Arguments shared by tdgs_render and tdgs_project.
+static int check_render_args(const tdgs_gaussians* g, const tdgs_camera* cam, const tdgs_tiling* tiling,
+                             const tdgs_render_options* opt, const tdgs_render_buffers* buf) {
+    TDGS_TRY(check_gaussians(g, false));
+    TDGS_TRY(check_tiling(tiling, cam));
+    TDGS_TRY(check_options(opt, g->sh_degree));
+    TDGS_REQUIRE(cam->near_z >= 0.0f, "near clipping plane must be >= 0 (got %g)", (double)cam->near_z);
+    TDGS_REQUIRE(buf->capacity >= g->n, "render buffers hold %d Gaussians, need %d", buf->capacity, g->n);
+    if (g->n == 0) return TDGS_OK;
+    TDGS_REQUIRE(buf->fgidx_to_gidx && buf->depths && buf->f2d && buf->tile_ranges && buf->counts &&
+                     buf->tiles_end && buf->temp,
+                 "null render buffers");
+    TDGS_REQUIRE(((uintptr_t)buf->f2d & 15) == 0 && ((uintptr_t)buf->tile_ranges & 15) == 0,
+                 "render buffers: f2d and tile_ranges must be 16-byte aligned");
+    const size_t need = tdgs_render_temp_bytes(buf->capacity, buf->key_capacity, tiling);
+    if (buf->temp_bytes < need) {
+        set_error("render scratch too small: need %zu bytes, have %zu", need, buf->temp_bytes);
+        return TDGS_ERR_CAPACITY;
+    }
+    return TDGS_OK;
+}
+
+// Steps 1-3 of the pipeline: keep counts, then compaction + projection (N_f into d_nbf).
+// depth_keys / depth_vals (may be null) receive the depth presort's input.
+static int launch_keep_and_project(hipStream_t s, const tdgs_gaussians* g, const tdgs_camera* cam,
+                                   const tdgs_tiling* tiling, const tdgs_render_options* opt,
+                                   const tdgs_render_buffers* buf, const RenderScratch& r, int64_t* d_nbf,
+                                   uint32_t* depth_keys, int32_t* depth_vals) {
+    const int64_t n = g->n;
+    const int64_t nblocks = ceil_div(n, kProjThreads);
+    const int64_t ngroups = ceil_div(nblocks, kKeepSub);
+    {
+        StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
+        KeepEval ev{g->means_opacity, g->kind, *cam, *opt, buf->keep};
+        k_keep_counts<<<(unsigned)ngroups, 256, 0, s>>>(ev, n, r.block_counts, r.group_counts, nblocks);
+        TDGS_LAUNCHED();
+    }
+    ProjectArgs pa;
+    pa.g = *g; pa.cam = *cam; pa.tiling = *tiling; pa.opt = *opt;
+    pa.block_counts = r.block_counts; pa.group_counts = r.group_counts; pa.ngroups = ngroups; pa.d_nbf = d_nbf;
+    pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
+    pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
+    pa.depth_keys = depth_keys; pa.depth_vals = depth_vals;
+    StageScope sc(TDGS_STAGE_PROJECT, s);
+    if (g->kind == TDGS_TRAINABLE)
+        k_project<TDGS_TRAINABLE><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
+    else
+        k_project<TDGS_RENDER_ONLY><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
 }  // namespace tdgs
 
 using namespace tdgs;
 
 extern "C" {
+
+int tdgs_project(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
+                 const tdgs_tiling* tiling, const tdgs_render_options* opt, tdgs_render_buffers* buf,
+                 int32_t* nb_fgaussians_out) {
+    TDGS_REQUIRE(ctx && buf && nb_fgaussians_out, "null arguments");
+    TDGS_TRY(check_render_args(g, cam, tiling, opt, buf));
+    *nb_fgaussians_out = 0;
+    if (g->n == 0) return TDGS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const RenderScratch r = carve_render_scratch(buf, tiling);
+    TDGS_TRY(launch_keep_and_project(s, g, cam, tiling, opt, buf, r, ctx->d_counters, nullptr, nullptr));
+    TDGS_TRY(read_counters(ctx, s));
+    *nb_fgaussians_out = (int32_t)ctx->h_counters[0];
+    return TDGS_OK;
+}
 
 int tdgs_fill_keep(void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
                    const tdgs_render_options* opt, uint8_t* keep) {
@@ -1144,7 +1252,7 @@ int tdgs_fill_fgidx_to_gidx(tdgs_ctx* ctx, void* stream, const uint8_t* keep, in
     hipStream_t s = (hipStream_t)stream;
     TDGS_TRY(device_scan(ItemsU8{keep}, ItemsU8{keep}, CompactOut{fgidx_to_gidx, keep_cs}, n, temp,
                          temp_bytes, ctx->d_counters, s));
-    TDGS_TRY(read_counters(ctx, s, 1));
+    TDGS_TRY(read_counters(ctx, s));
     *nb_fgaussians_out = (int32_t)ctx->h_counters[0];
     return TDGS_OK;
 }
@@ -1158,7 +1266,7 @@ int tdgs_scan_counts(tdgs_ctx* ctx, void* stream, const int32_t* counts, int32_t
     hipStream_t s = (hipStream_t)stream;
     TDGS_TRY(device_scan(ItemsI32{counts}, ItemsI32{counts}, WriteInclusiveI32{counts_cs}, n, temp,
                          temp_bytes, ctx->d_counters, s));
-    TDGS_TRY(read_counters(ctx, s, 1));
+    TDGS_TRY(read_counters(ctx, s));
     *total_out = ctx->h_counters[0];
     if (*total_out >= (int64_t)INT32_MAX) {
         set_error("%lld duplicated keys exceed the int32 index range", (long long)*total_out);
@@ -1261,81 +1369,41 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
                 const tdgs_tiling* tiling, const tdgs_render_options* opt, tdgs_render_buffers* buf,
                 const tdgs_render_outputs* out, int32_t* nb_fgaussians_out, int64_t* nb_keys_out) {
     TDGS_REQUIRE(ctx && buf && out && nb_fgaussians_out && nb_keys_out, "null arguments");
-    TDGS_TRY(check_gaussians(g, false));
-    TDGS_TRY(check_tiling(tiling, cam));
-    TDGS_TRY(check_options(opt, g->sh_degree));
-    TDGS_REQUIRE(cam->near_z >= 0.0f, "near clipping plane must be >= 0 (got %g)", (double)cam->near_z);
-    TDGS_REQUIRE(buf->capacity >= g->n, "render buffers hold %d Gaussians, need %d", buf->capacity, g->n);
+    TDGS_TRY(check_render_args(g, cam, tiling, opt, buf));
     hipStream_t s = (hipStream_t)stream;
     *nb_fgaussians_out = 0;
     *nb_keys_out = 0;
     const int64_t n = g->n;
     if (n == 0) return launch_render_void(s, cam, opt, out);
-    TDGS_REQUIRE(buf->fgidx_to_gidx && buf->depths && buf->f2d && buf->tile_ranges && buf->counts &&
-                     buf->tiles_end && buf->temp,
-                 "null render buffers");
-    TDGS_REQUIRE(((uintptr_t)buf->f2d & 15) == 0, "render buffers: f2d must be 16-byte aligned");
-    const size_t need = tdgs_render_temp_bytes(buf->capacity, buf->key_capacity, tiling);
-    if (buf->temp_bytes < need) {
-        set_error("render scratch too small: need %zu bytes, have %zu", need, buf->temp_bytes);
-        return TDGS_ERR_CAPACITY;
-    }
-    const int64_t cap = buf->capacity;
-    Arena ar(buf->temp, buf->temp_bytes);
-    ar.take<int64_t>(kCounters);
-    uint32_t* dkey = ar.take<uint32_t>(cap);
-    uint32_t* dkey_alt = ar.take<uint32_t>(cap);
-    uint32_t* dkey_sorted = ar.take<uint32_t>(cap);
-    int32_t* dval = ar.take<int32_t>(cap);
-    int32_t* dval_alt = ar.take<int32_t>(cap);
-    int32_t* sorted_f = ar.take<int32_t>(cap);
-    int32_t* cs = ar.take<int32_t>(cap);
-    const size_t sbytes = scan_temp_bytes_for(cap);
-    void* stemp = ar.take<char>((int64_t)sbytes);
-    int32_t* block_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub) * kKeepSub);
-    int32_t* group_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub));
-    const int64_t big = cap > buf->key_capacity ? cap : buf->key_capacity;
-    const size_t rbytes = radix_temp_bytes(big);
-    void* rtemp = ar.take<char>((int64_t)rbytes);
-    const int64_t ndiff = rect_diff_size(tiling);
-    int32_t* rect_diff = ar.take<int32_t>(kRectCopies * ndiff);
-    const int64_t nblk = ceil_div(buf->key_capacity, kEmitTile) + 2;
-    int32_t* blk_first = ar.take<int32_t>(nblk);
+    const RenderScratch r = carve_render_scratch(buf, tiling);
+    uint32_t* dkey = r.dkey;
+    uint32_t* dkey_alt = r.dkey_alt;
+    uint32_t* dkey_sorted = r.dkey_sorted;
+    int32_t* dval = r.dval;
+    int32_t* dval_alt = r.dval_alt;
+    int32_t* sorted_f = r.sorted_f;
+    int32_t* cs = r.cs;
+    void* stemp = r.stemp;
+    const size_t sbytes = r.sbytes;
+    void* rtemp = r.rtemp;
+    const size_t rbytes = r.rbytes;
+    const int64_t ndiff = r.ndiff;
+    int32_t* rect_diff = r.rect_diff;
+    const int64_t nblk = r.nblk;
+    int32_t* blk_first = r.blk_first;
     int64_t* d_nbf = ctx->d_counters;
     int64_t* d_m = ctx->d_counters + 1;
+    uint32_t* d_err = ctx_error_word(ctx);
 
-
-    // 1-2: keep flags, keep counts per projection block, their scan (N_f)
-    const int64_t nblocks = ceil_div(n, kProjThreads);
-    const int64_t ngroups = ceil_div(nblocks, kKeepSub);
-    {
-        StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
-        KeepEval ev{g->means_opacity, g->kind, *cam, *opt, buf->keep};
-        k_keep_counts<<<(unsigned)ngroups, 256, 0, s>>>(ev, n, block_counts, group_counts, nblocks);
-        TDGS_LAUNCHED();
-    }
-    // 3: compaction + projection
-    ProjectArgs pa;
-    pa.g = *g; pa.cam = *cam; pa.tiling = *tiling; pa.opt = *opt;
-    pa.block_counts = block_counts; pa.group_counts = group_counts; pa.ngroups = ngroups; pa.d_nbf = d_nbf;
-    pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
-    pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
-    pa.depth_keys = dkey; pa.depth_vals = dval;
-    {
-        StageScope sc(TDGS_STAGE_PROJECT, s);
-        if (g->kind == TDGS_TRAINABLE)
-            k_project<TDGS_TRAINABLE><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
-        else
-            k_project<TDGS_RENDER_ONLY><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
-        TDGS_LAUNCHED();
-    }
+    // 1-3: keep counts, compaction + projection
+    TDGS_TRY(launch_keep_and_project(s, g, cam, tiling, opt, buf, r, d_nbf, dkey, dval));
     // 4: the N_b non-empty Gaussians by (depth bits, fgidx); empty and culled ones (all-ones
     // depth key) are dropped by the first pass, the later passes sort N_b pairs
     int64_t* d_nb = ctx->d_counters + 4;
     {
         StageScope sc(TDGS_STAGE_DEPTH_SORT, s);
         TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
-                                            rtemp, rbytes, s, nullptr, nullptr, d_nb));
+                                            rtemp, rbytes, s, nullptr, d_err, d_nb));
     }
     // 5: tile counts in depth order -> M
     {
@@ -1344,7 +1412,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
                              SortedCounts{sorted_f, buf->counts, d_nb}, WriteScanAndBlocks{cs, blk_first, nblk}, n, stemp,
                              sbytes, d_m, s, d_nb));
     }
-    TDGS_TRY(read_counters(ctx, s, 5));
+    TDGS_TRY(read_counters(ctx, s));
     const int64_t nbf = ctx->h_counters[0];
     const int64_t m = ctx->h_counters[1];
     const int64_t nb = ctx->h_counters[4];   // non-empty Gaussians: the sorted depth order's length
@@ -1395,11 +1463,11 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         if (tile16)
             TDGS_TRY(radix_sort_pairs<uint16_t>((const uint16_t*)ek, t16_out, ev2, buf->sorted_values, t16_alt,
                                                 buf->values, m, tb, te_bit, rtemp, rbytes, s,
-                                                radix_count_table(rtemp)));
+                                                radix_count_table(rtemp), d_err));
         else
             TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
                                                 buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, tb,
-                                                te_bit, rtemp, rbytes, s, radix_count_table(rtemp)));
+                                                te_bit, rtemp, rbytes, s, radix_count_table(rtemp), d_err));
     }
     // 8: tile ranges
     {

@@ -14,9 +14,16 @@ struct tdgs_ctx {
 namespace tdgs {
 
 constexpr int kCounters = 8;
+// Slot of ctx->d_counters holding the sticky device error flags (low 32 bits): kernels OR
+// kErr* bits into it; every host synchronisation through read_counters reports and clears it.
+constexpr int kErrSlot = 7;
+constexpr uint32_t kErrSortCounts = 1u;   // radix-sort counts disagreed with the keys
 
-// Copy the first count device counters to the host and wait for the stream.
-int read_counters(tdgs_ctx* ctx, hipStream_t stream, int count);
+inline uint32_t* ctx_error_word(tdgs_ctx* ctx) { return reinterpret_cast<uint32_t*>(ctx->d_counters + kErrSlot); }
+
+// Copy the device counters to the host and wait for the stream; returns TDGS_ERR_DEVICE (and
+// clears the flags) when a kernel has raised an error flag since the last check.
+int read_counters(tdgs_ctx* ctx, hipStream_t stream);
 
 // Stage profiler: records a start/stop HIP event pair around a stage when enabled.
 void profile_mark(int stage, bool start, hipStream_t stream);
@@ -51,6 +58,52 @@ __device__ __forceinline__ void tile_pixel(int t, int TW, int TH, int* u_in, int
     }
 }
 
+// The 2D gradients of a tdgs_gradients in either layout: component k (0-8: dmu_x, dmu_y, da,
+// dM11, dM21, dM22, dr, dg, db) of filtered Gaussian f (0-based) is base[k][stride[k] * f].
+struct Grads2D {
+    float* base[9];
+    int32_t stride[9];
+    __device__ __forceinline__ float* at(int k, int64_t f) const { return base[k] + (int64_t)stride[k] * f; }
+    // the same for a k that differs between lanes (selects instead of an indexed argument)
+    __device__ __forceinline__ float* at_dynamic(int k, int64_t f) const {
+        float* b = base[0];
+        int32_t st = stride[0];
+#pragma unroll
+        for (int i = 1; i < 9; ++i) {
+            if (k == i) {
+                b = base[i];
+                st = stride[i];
+            }
+        }
+        return b + (int64_t)st * f;
+    }
+};
+
+// Host: the view of grads' 2D gradients; TDGS_ERR_INVALID when the arrays of neither layout are
+// given.
+inline int grads2d_view(const tdgs_gradients* g, Grads2D* v) {
+    TDGS_REQUIRE(g != nullptr, "null gradients");
+    if (g->grads2d) {
+        for (int k = 0; k < 9; ++k) {
+            v->base[k] = g->grads2d + k;
+            v->stride[k] = 9;
+        }
+        return TDGS_OK;
+    }
+    TDGS_REQUIRE(g->mean2d_grads && g->opacity_grads && g->licov2d_grads && g->color_grads,
+                 "2D gradients: neither grads2d nor all of mean2d_grads, opacity_grads, licov2d_grads and "
+                 "color_grads given");
+    float* const arr[4] = {g->mean2d_grads, g->opacity_grads, g->licov2d_grads, g->color_grads};
+    const int comps[4] = {2, 1, 3, 3};
+    int k = 0;
+    for (int a = 0; a < 4; ++a)
+        for (int c = 0; c < comps[a]; ++c, ++k) {
+            v->base[k] = arr[a] + c;
+            v->stride[k] = comps[a];
+        }
+    return TDGS_OK;
+}
+
 inline int check_gaussians(const tdgs_gaussians* g, bool trainable_only) {
     TDGS_REQUIRE(g != nullptr, "gaussians is null");
     TDGS_REQUIRE(g->n >= 0, "negative Gaussian count %d", g->n);
@@ -68,8 +121,10 @@ inline int check_gaussians(const tdgs_gaussians* g, bool trainable_only) {
 inline int check_tiling(const tdgs_tiling* t, const tdgs_camera* cam) {
     TDGS_REQUIRE(t && cam, "null tiling or camera");
     TDGS_REQUIRE(t->tile_width > 0 && t->tile_height > 0, "bad tile size");
-    const int nt = t->tile_width * t->tile_height;
-    TDGS_REQUIRE(nt <= 1024 && nt % 64 == 0, "tile of %d pixels: need a multiple of 64 up to 1024", nt);
+    // any tile shape the reference's Tiling accepts (forward_structs.jl:340-424) whose pixels fit
+    // one workgroup: the kernels run one thread per pixel (two in the backward pass)
+    const int64_t nt = (int64_t)t->tile_width * t->tile_height;
+    TDGS_REQUIRE(nt <= 1024, "tile of %lld pixels: at most 1024 are supported", (long long)nt);
     TDGS_REQUIRE(cam->width > 0 && cam->height > 0, "bad image size");
     TDGS_REQUIRE(t->nb_tiles_x == (cam->width + t->tile_width - 1) / t->tile_width &&
                      t->nb_tiles_y == (cam->height + t->tile_height - 1) / t->tile_height,

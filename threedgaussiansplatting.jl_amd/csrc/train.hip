@@ -131,11 +131,13 @@ __global__ __launch_bounds__(256) void k_adam(AdamArgs a) {
 
 // update_adc_stats_kernel! (training.jl:472-497). ((h^2, w^2) ./ 4 is a Float64 pair there,
 // so the norm is formed in double precision.)
-__global__ void k_adc_stats(const float* __restrict__ grads2d, const int32_t* __restrict__ f2g, int64_t nbf,
-                            double sw, double sh, float* __restrict__ acc, int32_t* __restrict__ cnt) {
+// mean2d: the x component of the first mean gradient, the y component follows it; stride
+// floats from one filtered Gaussian to the next (9 interleaved, 2 for the reference's array).
+__global__ void k_adc_stats(const float* __restrict__ mean2d, int32_t stride, const int32_t* __restrict__ f2g,
+                            int64_t nbf, double sw, double sh, float* __restrict__ acc, int32_t* __restrict__ cnt) {
     const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (f >= nbf) return;
-    const float gx = grads2d[9 * f], gy = grads2d[9 * f + 1];
+    const float gx = mean2d[stride * f], gy = mean2d[stride * f + 1];
     if (gx != 0.0f || gy != 0.0f) {
         const int64_t gi = (int64_t)f2g[f] - 1;
         const double nrm = sqrt((double)(gx * gx) * sw + (double)(gy * gy) * sh);
@@ -400,11 +402,14 @@ int tdgs_adc_stats(void* stream, tdgs_adc_buffers* adc, const tdgs_gradients* gr
                    int32_t nb_fgaussians, int32_t width, int32_t height) {
     TDGS_REQUIRE(adc && grads && fgidx_to_gidx, "null arguments");
     if (nb_fgaussians <= 0) return TDGS_OK;
-    TDGS_REQUIRE(adc->accum_grad_norms && adc->contribution_counts && grads->grads2d, "null arrays");
+    TDGS_REQUIRE(adc->accum_grad_norms && adc->contribution_counts, "null arrays");
+    Grads2D g2;
+    TDGS_TRY(grads2d_view(grads, &g2));
     hipStream_t s = (hipStream_t)stream;
     StageScope sc(TDGS_STAGE_ADC, s);
     const double sw = (double)width * width / 4.0, sh = (double)height * height / 4.0;
-    k_adc_stats<<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(grads->grads2d, fgidx_to_gidx, nb_fgaussians,
+    k_adc_stats<<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(g2.base[0], g2.stride[0], fgidx_to_gidx,
+                                                                       nb_fgaussians,
                                                                        sw, sh, adc->accum_grad_norms,
                                                                        adc->contribution_counts);
     TDGS_LAUNCHED();
@@ -432,9 +437,8 @@ int tdgs_adc_plan(tdgs_ctx* ctx, void* stream, tdgs_adc_buffers* adc, const tdgs
                              AdcPlanOut{adc->new_counts_cs, adc->ngidx_to_gidx, adc->new_capacity}, g->n,
                              adc->temp, adc->temp_bytes, ctx->d_counters + 2, s));
     }
-    TDGS_HIP(hipMemcpyAsync(ctx->h_counters, ctx->d_counters + 2, sizeof(int64_t), hipMemcpyDeviceToHost, s));
-    TDGS_HIP(hipStreamSynchronize(s));
-    const int64_t nn = ctx->h_counters[0];
+    TDGS_TRY(read_counters(ctx, s));
+    const int64_t nn = ctx->h_counters[2];
     *n_new_out = (int32_t)nn;
     if (nn > adc->new_capacity) {
         set_error("ngidx_to_gidx holds %d entries, %lld needed", adc->new_capacity, (long long)nn);

@@ -71,6 +71,16 @@ class TrainingOptions:
                    pruning_3d_max_scale=float(f32(prune_scale) * f32(R)), **kw)
 
 
+def annealed_means_lr(iteration_nb: int, options: TrainingOptions) -> float:
+    """The means learning rate update_learning_rates! (training.jl:287-302) sets at iteration
+    iteration_nb (1-based), in float32 as the reference computes it:
+    x = clamp((it - 1) / (nb_lr_annealing_steps - 1), 0, 1), lr = exp((1 - x) log lr0 + x log lr1)."""
+    x = f32(min(max(f32(iteration_nb - 1) / f32(options.nb_lr_annealing_steps - 1), f32(0)), f32(1)))
+    lr = np.exp(f32(f32(f32(1) - x) * np.log(f32(options.initial_means_lr)))
+                + f32(x * np.log(f32(options.final_means_lr))))
+    return float(f32(lr))
+
+
 class GaussianAdamMomentsLearningRatesVector:
     """Adam moments (m1, m2 interleaved) and learning rates (optimizer.jl:9-195)."""
 
@@ -460,11 +470,8 @@ class Trainer:
             opacity_reset_(self.gaussians, o.opacity_reset_max_value, self.optimizer.moments.opacity)
 
     def update_learning_rates_(self):
-        """update_learning_rates! (training.jl:287-302), log-linear in float32."""
-        o = self.options
-        x = f32(min(max((self.iteration_nb - 1) / f32(o.nb_lr_annealing_steps - 1), 0.0), 1.0))
-        lr = np.exp(f32(f32(1 - x) * np.log(f32(o.initial_means_lr)) + x * np.log(f32(o.final_means_lr))))
-        self.optimizer.moments.means_lr = float(f32(lr))
+        """update_learning_rates! (training.jl:287-302)."""
+        self.optimizer.moments.means_lr = annealed_means_lr(self.iteration_nb, self.options)
 
     def maybe_densify_and_prune_(self):
         """maybe_densify_and_prune! (training.jl:313-444); True when an ADC step ran."""
