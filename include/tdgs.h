@@ -283,6 +283,17 @@ int tdgs_fill_fgidx_to_gidx(tdgs_ctx* ctx, void* stream, const uint8_t* keep, in
 int tdgs_scan_counts(tdgs_ctx* ctx, void* stream, const int32_t* counts, int32_t n,
                      int32_t* counts_cs, void* temp, size_t temp_bytes, int64_t* total_out);
 
+/* No counterpart in the reference: tdgs_scan_counts for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc). It
+ * calls no allocating routine and needs no context or scratch argument: the per-tile partial
+ * sums live in a fixed static device array of 64 KiB (per GPU, held until the process ends),
+ * so n may be at most TDGS_SCAN_NOALLOC_MAX_ITEMS (TDGS_ERR_INVALID beyond). It does not
+ * synchronise: the total is written to total_dev (device memory, one int64). Calls that
+ * overlap on one GPU (different streams or host threads) share that array and race. */
+#define TDGS_SCAN_NOALLOC_MAX_ITEMS 16777216
+int tdgs_scan_counts_noalloc(void* stream, const int32_t* counts, int32_t n, int32_t* counts_cs,
+                             int64_t* total_dev);
+
 /* fill_df2dgs_codes_and_dfgidx_to_fgidx_kernel! (forward_core.jl:531-603). */
 int tdgs_emit_keys(void* stream, int32_t nb_fgaussians, const float* depths,
                    const int32_t* tile_ranges, const int32_t* counts_cs,

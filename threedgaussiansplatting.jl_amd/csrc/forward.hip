@@ -25,11 +25,40 @@
 // depth order is already in place, the tile sort needs only the tile ids: it moves 6 bytes
 // per key instead of 12, and the 64-bit keys are assembled only on request
 // (tdgs_render_sorted_keys).
+#include <mutex>
+
 #include "internal.hpp"
 #include "scan.hpp"
 #include "sort.hpp"
 
 namespace tdgs {
+
+// Scratch of tdgs_scan_counts_noalloc: the per-tile sums of the scan, in a fixed device array
+// (one copy per GPU). Host code uses the address hipGetSymbolAddress gives for the current
+// device, never the array's name.
+constexpr int64_t kNoAllocScanTiles = TDGS_SCAN_NOALLOC_MAX_ITEMS / kScanTile;
+static_assert(kNoAllocScanTiles * kScanTile == TDGS_SCAN_NOALLOC_MAX_ITEMS, "whole tiles");
+static __device__ __align__(256) int64_t scratch[kNoAllocScanTiles];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mutex;
+static int64_t* g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the current device, looked up once per device.
+static int noalloc_scratch(int64_t** out) {
+    int dev = -1;
+    TDGS_HIP(hipGetDevice(&dev));
+    TDGS_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d beyond the %d supported", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        TDGS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        TDGS_REQUIRE(p != nullptr, "no device address for the scan scratch");
+        g_scratch_ptr[dev] = static_cast<int64_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return TDGS_OK;
+}
 
 // ------------------------------------------------------------------------------------
 // Culling + compaction
@@ -1272,6 +1301,21 @@ int tdgs_scan_counts(tdgs_ctx* ctx, void* stream, const int32_t* counts, int32_t
         set_error("%lld duplicated keys exceed the int32 index range", (long long)*total_out);
         return TDGS_ERR_CAPACITY;
     }
+    return TDGS_OK;
+}
+
+int tdgs_scan_counts_noalloc(void* stream, const int32_t* counts, int32_t n, int32_t* counts_cs,
+                             int64_t* total_dev) {
+    TDGS_REQUIRE(n >= 0 && n <= TDGS_SCAN_NOALLOC_MAX_ITEMS, "%d items: the allocation-free scan takes at most %d",
+                 n, TDGS_SCAN_NOALLOC_MAX_ITEMS);
+    TDGS_REQUIRE(total_dev && (n == 0 || (counts && counts_cs)), "null arrays");
+    int64_t* tile_sums = nullptr;
+    TDGS_TRY(noalloc_scratch(&tile_sums));
+    hipStream_t s = (hipStream_t)stream;
+    // n == 0 still runs the one-block total pass so that *total_dev is written (0), in order
+    const int64_t nn = n > 0 ? n : 1;
+    TDGS_TRY(device_scan(ItemsI32Bounded{counts, n}, ItemsI32Bounded{counts, n}, WriteInclusiveI32Bounded{counts_cs, n},
+                         nn, tile_sums, sizeof(int64_t) * kNoAllocScanTiles, total_dev, s));
     return TDGS_OK;
 }
 

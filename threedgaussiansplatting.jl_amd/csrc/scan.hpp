@@ -148,6 +148,20 @@ struct ItemsU32 {
     const uint32_t* p;
     __device__ int32_t operator()(int64_t i) const { return (int32_t)p[i]; }
 };
+// The same with items past n read as zero and not written (a scan launched over
+// max(n, 1) items, so that an empty input still produces its total).
+struct ItemsI32Bounded {
+    const int32_t* p;
+    int64_t n;
+    __device__ int32_t operator()(int64_t i) const { return i < n ? p[i] : 0; }
+};
+struct WriteInclusiveI32Bounded {
+    int32_t* p;
+    int64_t n;
+    __device__ void operator()(int64_t i, int64_t incl, int32_t) const {
+        if (i < n) p[i] = (int32_t)incl;
+    }
+};
 struct WriteInclusiveI32 {
     int32_t* p;
     __device__ void operator()(int64_t i, int64_t incl, int32_t) const { p[i] = (int32_t)incl; }
