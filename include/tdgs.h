@@ -58,6 +58,12 @@ enum { TDGS_CLIP_CLAMP = 0, TDGS_CLIP_FILTER = 1 };  /* CovarianceBoundaryClamp 
 
 /* tdgs_render_options.flags */
 #define TDGS_FLAG_EXACT_SH_JACOBIAN 0x1  /* use basis coefficient 16 where src/sh.jl:249 uses 15 */
+/* With antialiasing the forward pass scales the opacity by f = max(aa_min, sqrt(det0 / det))
+ * (forward_core.jl:450-462), but the reference's backward pass adds a0 * dL/da * d(det0/det)/dSigma
+ * to the covariance gradient (backward_core.jl:480-490, derived for f = det0/det in
+ * docs/src/math.md:194-197): the derivative of f^2, not of f. That is reproduced by default; this
+ * flag uses the derivative of f instead (d(f^2)/dSigma / (2 f), zero where f is clamped to aa_min). */
+#define TDGS_FLAG_EXACT_AA_GRADIENT 0x2
 
 /* PinholeCamera (src/cameras.jl:50-106): P = K [R^T | -R^T t] cached as 3x4, row-major here. */
 typedef struct tdgs_camera {

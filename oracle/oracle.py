@@ -315,6 +315,22 @@ def exp(x):
     return lib().oracle_exp(float(x))
 
 
+def exp_array(x):
+    """exp_f of every element of a float32 array."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().oracle_exp_array(ptr(x), ptr(y), C.c_int64(x.size))
+    return y
+
+
+def log_array(x):
+    """log_f of every element of a float32 array."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().oracle_log_array(ptr(x), ptr(y), C.c_int64(x.size))
+    return y
+
+
 def log(x):
     return lib().oracle_log(float(x))
 

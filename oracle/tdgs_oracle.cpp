@@ -8,9 +8,12 @@
 // filtered Gaussian, key, pixel at a time), with the per-element mathematics shared with
 // the kernels (threedgaussiansplatting.jl_amd/csrc/tdgs_math.hpp). The comments give the
 // reference file:line each function follows. Pinning of each function against the
-// reference's own golden vectors, closed forms and brute force is in tests/ (see the
-// module docstrings there). Functions without such a check: oracle_adc_apply's split
-// means (statistical check only: the reference samples them with device randn).
+// reference's own golden vectors, closed forms, brute force and an independent float64
+// restatement differentiated by torch autograd is in tests/ (see the module docstrings
+// there: test_oracle_goldens, test_oracle_pins, test_oracle_closed_forms,
+// test_oracle_float64, test_oracle_training). Parity unpinned: the individual split draws of
+// oracle_adc_apply (the reference samples them with device randn; their distribution
+// R (z * s), z ~ N(0, I), is pinned by a sample-covariance closed form).
 //
 // Built by oracle/build.py into oracle/liboracle.so (g++ -O2 -ffp-contract=off).
 
@@ -669,6 +672,12 @@ void cpu_render_reference(const tdgs_gaussians* g, const tdgs_camera* cam,
 // Scalar helpers exposed for closed-form checks of the shared mathematics.
 float oracle_exp(float x) { return exp_f(x); }
 float oracle_log(float x) { return log_f(x); }
+void oracle_exp_array(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = exp_f(x[i]);
+}
+void oracle_log_array(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = log_f(x[i]);
+}
 float oracle_sigmoid(float x) { return sigmoid_f(x); }
 void oracle_quat_to_rot(const float* q, float* R) { quat_to_rot(q[0], q[1], q[2], q[3], R); }
 void oracle_normal_pair(uint64_t seed, uint64_t stream, uint32_t pair, float* out) {

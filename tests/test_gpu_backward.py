@@ -82,7 +82,8 @@ FILTER = {"clip_mode": 1}   # TDGS_CLIP_FILTER (BoundaryFilter)
     # BoundaryFilter clip mode (forward_core.jl:343, backward_core.jl:373-381)
     (1, 20_000, (16, 16), False, AA), (2, 60_000, (16, 16), False, AA),
     (1, 20_000, (16, 16), False, FILTER), (2, 60_000, (16, 16), False, FILTER),
-    (2, 60_000, (16, 16), True, {**AA, **FILTER})])
+    (2, 60_000, (16, 16), True, {**AA, **FILTER}),
+    (2, 60_000, (16, 16), False, {**AA, "exact_aa_gradient": True})])
 def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact, extra):
     w = synthetic.config(cfg, n=n, cameras=2)
     cam = w.cameras[-1]

@@ -17,6 +17,7 @@ TDGS_RENDER_ONLY = 1
 TDGS_CLIP_CLAMP = 0
 TDGS_CLIP_FILTER = 1
 TDGS_FLAG_EXACT_SH_JACOBIAN = 0x1
+TDGS_FLAG_EXACT_AA_GRADIENT = 0x2
 TDGS_IMAGE_RGB = 0
 TDGS_IMAGE_TRANSMITTANCE = 1
 TDGS_IMAGE_DEPTH = 2

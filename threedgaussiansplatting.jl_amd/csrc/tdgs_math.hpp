@@ -616,10 +616,21 @@ TDGS_HD BackwardProjectOut backward_project(const BackwardProjectIn& in, const t
     dS[1] = -fmaf(2.0f * bd, gD, fmaf(b_sq + ad, gB, 2.0f * ab * gA));
     dS[2] = -fmaf(d_sq, gD, fmaf(bd, gB, b_sq * gA));
     if (o.antialiasing) {
+        // opacity correction f = sqrt(det0 / det) (backward_core.jl:480-490): the reference adds
+        // a0 dL/da d(f^2)/dSigma, in terms of M = Sigma^-1 = [A B; B D]:
+        //   d(f^2)/dSigma = [A^2 Dx + B^2 Dy - A delta, 2 B (A Dx + D Dy - delta), B^2 Dx + D^2 Dy - D delta]
+        // with delta = (AD - B^2) Dx Dy, written with B^2 Dx in the first entry as the reference
+        // does (the same for equal dilations). TDGS_FLAG_EXACT_AA_GRADIENT divides by 2 f (the
+        // derivative of f itself), and gives 0 where f was clamped to aa_min.
         const float Dx = o.dilation_x, Dy = o.dilation_y;
         const float det = (ad - b_sq) * Dx * Dy;
-        const float k = a0 * da;
-        dS[0] = fmaf(k, a_sq * Dx + b_sq * Dx - A * det, dS[0]);
+        float k = a0 * da;
+        const bool exact = (o.flags & TDGS_FLAG_EXACT_AA_GRADIENT) != 0;
+        if (exact) {
+            const float f = in.a / a0;
+            k = f > o.aa_min_factor ? k / (2.0f * f) : 0.0f;
+        }
+        dS[0] = fmaf(k, a_sq * Dx + b_sq * (exact ? Dy : Dx) - A * det, dS[0]);
         dS[1] = fmaf(k, 2.0f * B * (A * Dx + D * Dy - det), dS[1]);
         dS[2] = fmaf(k, b_sq * Dx + d_sq * Dy - D * det, dS[2]);
     }

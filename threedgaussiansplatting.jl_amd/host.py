@@ -189,6 +189,7 @@ class RenderOptions:
     clip_y_min_nc: float = -1 - DEFAULT_CLIPPING_MARGIN_NC
     clip_y_max_nc: float = 1 + DEFAULT_CLIPPING_MARGIN_NC
     exact_sh_jacobian: bool = False
+    exact_aa_gradient: bool = False
 
     @classmethod
     def for_camera(cls, cam: PinholeCamera, sh_degree, **kw):
@@ -217,7 +218,8 @@ class RenderOptions:
         o.sh_degree = int(self.sh_degree)
         o.clip_mode = int(self.clip_mode)
         o.antialiasing = 1 if self.use_antialiasing else 0
-        o.flags = abi.TDGS_FLAG_EXACT_SH_JACOBIAN if self.exact_sh_jacobian else 0
+        o.flags = ((abi.TDGS_FLAG_EXACT_SH_JACOBIAN if self.exact_sh_jacobian else 0)
+                   | (abi.TDGS_FLAG_EXACT_AA_GRADIENT if self.exact_aa_gradient else 0))
         return o
 
 
