@@ -34,10 +34,15 @@ __graft_entry__.load_package()
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3       # MI355X vector FP32 (published)
 
-# FLOP of the blending loop per (pixel, sorted entry) evaluation: the exponent, 5 FMA (10),
-# for every evaluation; for one that passes the exponent cut also the exponential (1 mul,
-# 2 + 8 FMA, 1 mul: 22) and 1 - alpha, T (1 - alpha) (2); for a contributing one also the
-# weight T alpha (1) and the colour, 3 FMA (6).
+# FLOP of blending under the metric's accounting: 20 per (pixel, sorted entry) evaluation made
+# before the pixel's early exit (E_f) plus one exponential per evaluation; backward blending
+# ~60 per (pixel, entry) evaluation of the reverse walk (E_b).
+BLEND_FLOP_PER_EVAL, BLEND_EXP_PER_EVAL = 20, 1
+BACKWARD_BLEND_FLOP_PER_EVAL = 60
+# The same loop's FLOP as this build executes it (reported beside, labelled "detailed"): the
+# exponent, 5 FMA (10), for every evaluation; for one that passes the exponent cut also the
+# exponential (1 mul, 2 + 8 FMA, 1 mul: 22) and 1 - alpha, T (1 - alpha) (2); for a
+# contributing one also the weight T alpha (1) and the colour, 3 FMA (6).
 BLEND_FLOP_EVAL, BLEND_FLOP_LIVE, BLEND_FLOP_CONTRIB = 10, 24, 7
 
 STAGES = ["cull_compact", "project", "depth_sort", "count_scan", "emit", "tile_sort", "tile_ranges",
@@ -56,7 +61,6 @@ def parse():
     p.add_argument("--no-extra-configs", action="store_true",
                    help="skip the config 1 / 3 training and config 4 stress legs")
     p.add_argument("--cfg3-iterations", type=int, default=3000)
-    p.add_argument("--cpu-threads", type=int, default=0)
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 10 device-to-device copies of 1 GiB (HBM counter calibration)")
     return p.parse_args()
@@ -86,10 +90,28 @@ def traffic_from_profiles(kernel):
     return None if k is None else k.get("bytes_per_launch")
 
 
-def frame_stats(core, g, cams, tiling, opts, outputs, buffers, idx):
-    """N_f, N_b, M and blending evaluations E for the given cameras (untimed pass)."""
+def backward_evaluations(last, tiles_end, tiling):
+    """E_b: the (pixel, sorted entry) evaluations of backward blending's reverse walk, each
+    pixel from its last contributor back to its tile's first entry (backward_core.jl:212-224):
+    sum over pixels with last > 0 of last - (index before the tile's first entry)."""
+    import torch
+    W, H = last.shape
+    u = torch.arange(W, device=last.device)[:, None] // tiling.tile_width
+    v = torch.arange(H, device=last.device)[None, :] // tiling.tile_height
+    tile0 = u + v * tiling.nb_tiles_x                         # 0-based tile of each pixel
+    te = tiles_end.to(torch.int64)
+    beg = torch.where(tile0 > 0, te[(tile0 - 1).clamp(min=0)], torch.zeros_like(tile0))
+    lst = last.to(torch.int64)
+    return int(torch.where(lst > 0, lst - beg, torch.zeros_like(lst)).sum().item())
+
+
+def frame_stats(core, g, cams, tiling, opts, buffers, idx):
+    """N_f, N_b, M, blending evaluations E_f (all, past the exponent cut, contributing) and the
+    backward walk's evaluations E_b, for the given cameras (untimed pass)."""
     import torch
     L = core.lib()
+    outputs = core.RenderOutputs.for_camera(cams[0], 0, include_rgb=True, include_transmittance=True,
+                                            include_depth=False, include_last_contributing_indices=True)
     ev = torch.zeros(3, dtype=torch.int64, device="cuda")
     st = []
     for k in idx:
@@ -101,7 +123,8 @@ def frame_stats(core, g, cams, tiling, opts, outputs, buffers, idx):
                                             C.byref(opts.to_c()), C.byref(buffers.struct()),
                                             C.c_int64(buffers.nb_keys), C.c_void_p(ev.data_ptr())))
         e = ev.cpu().tolist()
-        st.append((nf, nb, buffers.nb_keys, e[0], e[1], e[2]))
+        eb = backward_evaluations(outputs.last, buffers.tiles_end, tiling)
+        st.append((nf, nb, buffers.nb_keys, e[0], e[1], e[2], eb))
     torch.cuda.synchronize()
     return np.array(st, dtype=np.float64)
 
@@ -229,7 +252,7 @@ def train_cfg3(core, iterations):
     images = [torch.rand((c.width, c.height, 3), generator=gen, device="cuda") for c in cams]
     opts = host.RenderOptions.for_camera(cams[0], 3)
     to = training.TrainingOptions.for_scene(host.scene_radius(cams), nb_iterations=iterations)
-    tr = training.Trainer(g, cams, images, opts, tiling, to, seed=3)
+    tr = training.Trainer(g, cams, images, opts, tiling, to, seed=3, record_adc=True)
     n0 = len(tr.gaussians)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -242,7 +265,7 @@ def train_cfg3(core, iterations):
     return {"workload": w.name + f", {iterations} iterations with density control",
             "train_it_per_s": round(iterations / dt, 2), "seconds": round(dt, 3), "iterations": iterations,
             "gaussians_initial": n0, "gaussians_final": len(tr.gaussians), "gaussians_max": nmax,
-            "loss_last": round(float(tr.current_loss()), 6)}
+            "density_control": tr.adc_history, "loss_last": round(float(tr.current_loss()), 6)}
 
 
 def render_other_tiling(core, w, g, tile, frames=240, warmup=10):
@@ -318,66 +341,153 @@ def stress_cfg4(core, repeats=5):
     core.check(L.tdgs_profile_end(ms, cnt))
     stage = {STAGES[i]: round(ms[i] / cnt[i], 4) for i in range(13) if cnt[i] > 0}
     m = buf.nb_keys
-    sort_gbs = 2 * 24 * m / (stage["tile_sort"] * 1e-3) / 1e9
+    # the tile sort's bytes as the metric prices them (two 8-bit passes of CUB over 24 bytes per
+    # key for the tile bits) and as this build moves them (two passes over 16-bit tile ids and
+    # 32-bit values, or 64-bit keys past 65535 tiles)
+    conv_gbs = 2 * 24 * m / (stage["tile_sort"] * 1e-3) / 1e9
+    impl_b = algorithmic_bytes("tile_sort", 0, 0, 0, m, 0, 0, 0) if tiling.nb_tiles <= 65535 else 2 * 24 * m + 8 * m
+    impl_gbs = impl_b / (stage["tile_sort"] * 1e-3) / 1e9
     return {"workload": w.name, "keys": m, "filtered": buf.nb_fgaussians, "forward_ms": round(float(np.median(fw)), 3),
             "backward_ms": round(float(np.median(bw)), 3), "stage_ms": stage,
-            "tile_sort_algorithmic_GBs": round(sort_gbs, 1), "tile_sort_hbm_frac": round(sort_gbs / HBM_PEAK_GBS, 4)}
+            "tile_sort_convention_GBs": round(conv_gbs, 1), "tile_sort_convention_hbm_frac": round(conv_gbs / HBM_PEAK_GBS, 4),
+            "tile_sort_impl_bytes": int(impl_b), "tile_sort_impl_GBs": round(impl_gbs, 1),
+            "tile_sort_impl_hbm_frac": round(impl_gbs / HBM_PEAK_GBS, 4)}
 
 
 def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles):
-    """Bytes one launch of a stage must move (per frame averages)."""
-    if stage == "cull_compact":
-        return 16 * n + 2 * n + 4 * nf
-    if stage == "project":
-        return (4 + 16 + 12 + 16 + 4) * nf + 8 * n + (56 + 12 * h) * nb
-    if stage == "depth_sort":
-        return 4 * 16 * n
-    if stage == "count_scan":
-        return 12 * n
-    if stage == "emit":
-        return 32 * nb + 12 * m
-    if stage == "tile_sort":
-        return 2 * 24 * m
+    """Bytes one launch of a stage moves as this build's kernels do it (per frame averages),
+    each input read once and each output written once."""
+    if stage == "cull_compact":          # keep test: means + opacity in; per-block counts out
+        return 16 * n
+    if stage == "project":               # parameters of every Gaussian, SH of the non-empty ones;
+        # fgidx, counts, record (36), depth key + value of the kept; depth and rectangle of the
+        # non-empty; depth key + value slots of the culled
+        return 44 * n + 12 * h * nb + (4 + 4 + 36 + 8) * nf + 20 * nb + 8 * (n - nf)
+    if stage == "depth_sort":            # first pass over all N depth keys (count + scatter of the
+        # kept), three more over the N_b non-empty ones: count 4, scatter 8 in + 8 out
+        return 4 * n + 8 * n + 8 * nb + 3 * (4 + 16) * nb
+    if stage == "count_scan":            # sorted fgidx + their counts in, scan out (reduce + apply)
+        return 2 * (4 + 4) * nb + 4 * nb
+    if stage == "emit":                  # scan, fgidx, rectangle of the non-empty in; 16-bit tile id
+        # and value per key out
+        return 24 * nb + 6 * m
+    if stage == "tile_sort":             # two passes over (16-bit tile id, value): scatter 6 in + 6 out
+        # each, the second pass's count 2 in (the first pass's counts come from emission)
+        return 12 * m + 2 * m + 12 * m
     if stage == "tile_ranges":
-        return 8 * m + 4 * ntiles
-    if stage == "blend":
-        return 40 * m + 16 * npx
+        return 2 * m + 4 * ntiles
+    if stage == "blend":                 # metric's K5: 40 per key, 20 per pixel
+        return 40 * m + 20 * npx
     return None
 
 
-def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit):
-    """Per-kernel HBM fractions under the accounting convention of the metric: K1 = cull,
-    compaction and projection (16 N + (28 + 12h) N_f read, 8 N_f + 56 N_b written); K2 = count
-    scan and key emission (8 N_f + 24 N_b + 12 M); K3 = the sort, priced as a full-width
-    8-bit-digit LSD sort of the 64-bit keys (8 M + 24 M ceil(end_bit / 8)) whatever digit
-    width and pass count the build uses, over the depth and tile sort times; K4 = tile ranges
-    (8 M + 4 T); K5 = blend bytes (40 M + 20 P); K7 = backward projection ((160 + 24h) N_f);
-    K8 = Adam (28 (11 + 3h) N_f + 4 N_f), both from the separate launches; K7_K8_fused = the
-    trainer's fused backward projection and Adam, priced as K7 + K8 over its time. K7 and K8
-    use the render leg's counts (same Gaussians and cameras, before any densification)."""
+def measured_traffic():
+    """HBM bytes per launch from the committed rocprofv3 counter summary (FETCH_SIZE +
+    WRITE_SIZE, profiles/hbm_traffic.json), keyed by stage name, or {}."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        t = json.load(f)
+    return {k: v.get("bytes_per_launch") for k, v in t.get("kernels", {}).items()}
+
+
+# the counter-summary kernels of each survey row (sums of their per-launch bytes)
+MEASURED_KERNELS = {
+    "K1_project": ["keep_counts", "project"],
+    "K3_sort": ["depth_sort_count", "depth_sort_scatter", "tile_sort_count", "tile_sort_scatter"],
+    "K4_ranges": ["tile_ranges"],
+    "K5_blend": ["blend"],
+    "K6_backward_blend": ["backward_blend"],
+    "K7_backward_project": ["backward_project"],
+    "K8_adam": ["adam"],
+    "K7_K8_fused": ["backward_project_adam"],
+}
+
+
+def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit, e_f, e_b):
+    """Per-kernel roofline fractions. `bytes` follow the metric's accounting (K1 = cull,
+    compaction and projection: 16 N + (28 + 12h) N_f read, 8 N_f + 56 N_b written; K2 = count
+    scan and key emission: 8 N_f + 24 N_b + 12 M; K3 = the sort, priced as CUB's 8-bit-digit LSD
+    sort of the 64-bit keys: 8 M + 24 M ceil(end_bit / 8); K4 = ranges: 8 M + 4 T; K5 = blend:
+    40 M + 20 P, FLOP 20 E_f + E_f exponentials; K6 = backward blend: 40 M + 20 P + 36 A with A the
+    per-(tile, Gaussian) atomic flushes (<= M), FLOP 60 E_b; K7 = backward projection
+    (160 + 24h) N_f; K8 = Adam 28 (11 + 3h) N_f + 4 N_f; K7_K8_fused = the trainer's fused launch,
+    K7 + K8 without the 3D gradients K7 writes and K8 reads back: (160 + 24h + 28 (11 + 3h) + 4 -
+    8 (11 + 3h)) N_f, 1728 B at SH3). `impl_bytes` are what this build's kernels move
+    (algorithmic_bytes) and `measured_bytes` the counter summary's HBM traffic; each comes with
+    its fraction of the 8 TB/s peak."""
+    g3 = 11 + 3 * h
+    k7, k8 = (160 + 24 * h) * nf, 28 * g3 * nf + 4 * nf
     rows = {
-        "K1_project": (16 * n + (28 + 12 * h) * nf + 8 * nf + 56 * nb, ["cull_compact", "project"], stage_ms),
-        "K2_scan_keys": (8 * nf + 24 * nb + 12 * m, ["count_scan", "emit"], stage_ms),
-        "K3_sort": (8 * m + 24 * m * math.ceil(end_bit / 8), ["depth_sort", "tile_sort"], stage_ms),
-        "K4_ranges": (8 * m + 4 * ntiles, ["tile_ranges"], stage_ms),
-        "K5_blend": (40 * m + 20 * npx, ["blend"], stage_ms),
+        "K1_project": (16 * n + (28 + 12 * h) * nf + 8 * nf + 56 * nb, ["cull_compact", "project"], stage_ms, None),
+        "K2_scan_keys": (8 * nf + 24 * nb + 12 * m, ["count_scan", "emit"], stage_ms, None),
+        "K3_sort": (8 * m + 24 * m * math.ceil(end_bit / 8), ["depth_sort", "tile_sort"], stage_ms, None),
+        "K4_ranges": (8 * m + 4 * ntiles, ["tile_ranges"], stage_ms, None),
+        "K5_blend": (40 * m + 20 * npx, ["blend"], stage_ms, (BLEND_FLOP_PER_EVAL + BLEND_EXP_PER_EVAL) * e_f),
     }
     if train_stage:
-        k7, k8 = (160 + 24 * h) * nf, 28 * (11 + 3 * h) * nf + 4 * nf
         sep = train_stage.get("unfused", {})
-        rows["K7_backward_project"] = (k7, ["backward_project"], sep)
-        rows["K8_adam"] = (k8, ["adam"], sep)
-        if "adam" not in train_stage:   # the trainer's fused launch, priced as K7 + K8
-            rows["K7_K8_fused"] = (k7 + k8, ["backward_project"], train_stage)
+        rows["K6_backward_blend"] = (40 * m + 20 * npx + 36 * m, ["backward_blend"], train_stage,
+                                     BACKWARD_BLEND_FLOP_PER_EVAL * e_b)
+        rows["K7_backward_project"] = (k7, ["backward_project"], sep, None)
+        rows["K8_adam"] = (k8, ["adam"], sep, None)
+        if "adam" not in train_stage:   # the trainer's fused launch
+            rows["K7_K8_fused"] = (k7 + k8 - 2 * 4 * g3 * nf, ["backward_project"], train_stage, None)
+    impl = {s_: algorithmic_bytes(s_, n, nf, nb, m, npx, h, ntiles) for s_ in stage_ms}
+    measured = measured_traffic()
     out = {}
-    for k, (b, stages, src) in rows.items():
+    for k, (b, stages, src, flop) in rows.items():
         if not all(s_ in src for s_ in stages):
             continue
         t = sum(src[s_] for s_ in stages)
         gbs = b / (t * 1e-3) / 1e9
-        out[k] = {"stages": stages, "ms": round(t, 4), "bytes": int(b), "GBs": round(gbs, 1),
-                  "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        row = {"stages": stages, "ms": round(t, 4), "bytes": int(b), "GBs": round(gbs, 1),
+               "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+        ib = [impl.get(s_) for s_ in stages]
+        if all(v is not None for v in ib) and src is stage_ms:
+            row["impl_bytes"] = int(sum(ib))
+            row["impl_hbm_frac"] = round(sum(ib) / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        mk = MEASURED_KERNELS.get(k)
+        if mk and all(measured.get(x) for x in mk):
+            mb = sum(measured[x] for x in mk)
+            row["measured_bytes"] = int(mb)
+            row["measured_hbm_frac"] = round(mb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        if flop:
+            tf = flop / (t * 1e-3) / 1e12
+            row.update({"flop": int(flop), "TFLOPs": round(tf, 2), "valu_frac": round(tf / FP32_PEAK_TFLOPS, 4)})
+        out[k] = row
     return out
+
+
+def cpu_reference_baseline(orc, g, cam, opts, repeats=5, sample_step=16):
+    """The reference's own CPU renderer (render! for CPU arrays, forward_core.jl:25-177,
+    restated in C++ in oracle/) on one frame of the workload, std::chrono::steady_clock, median
+    of `repeats` runs after one warm-up:
+    - banded: all the box's threads (up to 16), each splatting every threads-th image column of
+      the full frame (identical output to one thread);
+    - faithful (single thread, as the reference runs): on a bounded sample, every
+      sample_step-th image column, with the per-Gaussian cull/projection/colour/depth sort in
+      full; the frame time is t(per-Gaussian part) + sample_step x t(sampled columns)."""
+    nproc = os.cpu_count() or 1
+    threads = min(16, nproc)
+    band = [orc.cpu_render_reference_timed(g, cam, opts, threads) for _ in range(repeats + 1)][1:]
+    t_band = float(np.median([a + b for a, b in band]))
+    single = [orc.cpu_render_reference_timed(g, cam, opts, 1, sample_step, 1) for _ in range(repeats + 1)][1:]
+    t_prep = float(np.median([a for a, _ in single]))
+    t_cols = float(np.median([b for _, b in single]))
+    t_single = t_prep + sample_step * t_cols
+    return {"value": round(1.0 / t_band, 4), "unit": "frames/s", "cores": threads, "nproc": nproc, "kind": "port",
+            "sample": f"1 frame (camera 0) of the same workload with the reference CPU renderer "
+                      f"(forward_core.jl:25-177) restated in C++, {threads} threads dealt image columns; "
+                      f"median of {repeats} after 1 warm-up",
+            "frame_s": round(t_band, 4),
+            "single_thread": {"value": round(1.0 / t_single, 5), "unit": "frames/s", "cores": 1,
+                              "frame_s_estimate": round(t_single, 3),
+                              "per_gaussian_s": round(t_prep, 4), "sampled_columns_s": round(t_cols, 4),
+                              "sample": f"one thread, every {sample_step}th image column of the same frame "
+                                        f"plus the full per-Gaussian part, median of {repeats} after 1 "
+                                        f"warm-up; frame = per-Gaussian + {sample_step} x sampled columns"}}
 
 
 def main():
@@ -439,9 +549,9 @@ def main():
     core.check(L.tdgs_profile_end(ms, cnt))
 
     used = sorted({k % ncam for k in range(args.steps)})
-    st = frame_stats(core, g, cams, tiling, opts, out, buf, used)
+    st = frame_stats(core, g, cams, tiling, opts, buf, used)
     n = len(g)
-    nf, nb, m, evals, evals_live, evals_contrib = st.mean(axis=0)
+    nf, nb, m, evals, evals_live, evals_contrib, evals_back = st.mean(axis=0)
     npx = cam0.width * cam0.height
     h = (deg + 1) ** 2
     stage_ms = {STAGES[i]: ms[i] / cnt[i] for i in range(13) if cnt[i] > 0}
@@ -457,12 +567,20 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
                 "algorithmic_bytes_per_launch": int(b_dom), "mean_launch_ms": round(stage_ms[dom], 4)}
     if dom == "blend":
-        flop = BLEND_FLOP_EVAL * evals + BLEND_FLOP_LIVE * evals_live + BLEND_FLOP_CONTRIB * evals_contrib
+        # the metric's FLOP of blending: 20 per evaluation before the early exit plus its
+        # exponential; the loop as this build executes it is reported beside ("detailed")
+        flop = (BLEND_FLOP_PER_EVAL + BLEND_EXP_PER_EVAL) * evals
+        flop_detailed = BLEND_FLOP_EVAL * evals + BLEND_FLOP_LIVE * evals_live + BLEND_FLOP_CONTRIB * evals_contrib
         tflops = flop / (stage_ms[dom] * 1e-3) / 1e12
         if tflops / FP32_PEAK_TFLOPS > roofline["frac"]:
             roofline.update({"bound": "valu", "achieved": round(tflops, 2), "peak": FP32_PEAK_TFLOPS,
                              "unit": "TFLOP/s", "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
-                             "algorithmic_flop_per_launch": int(flop), "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)})
+                             "algorithmic_flop_per_launch": int(flop),
+                             "flop_accounting": "20 E_f + E_f exponentials, E_f = (pixel, entry) evaluations "
+                                                "before each pixel's early exit (counted by a replay)",
+                             "detailed_flop_per_launch": int(flop_detailed),
+                             "detailed_frac": round(flop_detailed / (stage_ms[dom] * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
+                             "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)})
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -470,13 +588,7 @@ def main():
         import build as oracle_build
         oracle_build.build(force=False)
         import oracle as orc
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        c0 = time.perf_counter()
-        orc.cpu_render_reference(w.gaussians, cam0, opts, threads=threads)
-        c1 = time.perf_counter()
-        cpu = {"value": round(1.0 / (c1 - c0), 4), "unit": "frames/s", "cores": threads, "kind": "port",
-               "sample": f"1 frame (camera 0) of the same workload with the reference CPU renderer "
-                         f"(forward_core.jl:25-177) restated in C++, {threads} threads by image columns"}
+        cpu = cpu_reference_baseline(orc, w.gaussians, cam0, opts)
 
     train = None
     if args.train_steps > 0:
@@ -508,13 +620,14 @@ def main():
         "frame_ms_p99": round(float(np.percentile(frame_ms, 99)), 4),
         "mean_counts": {"filtered": round(nf), "nonempty": round(nb), "keys": round(m),
                         "blend_evaluations": round(evals), "blend_evaluations_live": round(evals_live),
-                        "blend_evaluations_contributing": round(evals_contrib)},
+                        "blend_evaluations_contributing": round(evals_contrib),
+                        "backward_blend_evaluations": round(evals_back)},
         "train": train,
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
         "stage_algorithmic_GBs": {k: round(v, 1) for k, v in stage_gbs.items()},
         "roofline": roofline,
         "survey_kernels": survey_kernels(stage_ms, train["stage_ms"] if train else None, n, nf, nb, m, npx, h,
-                                         tiling.nb_tiles, tiling.end_bit()),
+                                         tiling.nb_tiles, tiling.end_bit(), evals, evals_back),
         "cpu_baseline": cpu,
         "extra_configs": extra,
     }

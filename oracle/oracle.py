@@ -311,6 +311,22 @@ def cpu_render_reference(g, cam, opts, threads=1):
     return rgb, T
 
 
+def cpu_render_reference_timed(g, cam, opts, threads=1, column_step=1, first_column=1):
+    """Times the reference's CPU renderer: returns (seconds of the per-Gaussian part,
+    seconds of splatting the image columns u = first_column (mod column_step)) measured with
+    std::chrono::steady_clock."""
+    W, H = cam.width, cam.height
+    u_lo, u_hi = first_column, column_step
+    rgb = np.zeros((W, H, 3), np.float32)
+    T = np.zeros((W, H), np.float32)
+    sec = np.zeros(2, np.float64)
+    c_cam, c_o = cam.to_c(), opts.to_c()
+    lib().cpu_render_reference_timed(C.byref(gaussians_struct(g)), C.byref(c_cam), C.byref(c_o),
+                                     C.c_int32(threads), C.c_int32(u_lo), C.c_int32(u_hi), ptr(rgb), ptr(T),
+                                     ptr(sec))
+    return float(sec[0]), float(sec[1])
+
+
 def exp(x):
     return lib().oracle_exp(float(x))
 

@@ -18,6 +18,7 @@
 // Built by oracle/build.py into oracle/liboracle.so (g++ -O2 -ffp-contract=off).
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -564,9 +565,9 @@ double oracle_l1_loss_grad(const float* rendered, const float* gt, int64_t count
 // The reference's own CPU renderer (render! for CPU arrays, forward_core.jl:25-177):
 // no tiles; per kept Gaussian in depth order, the exact pixel span of its alpha = min_alpha
 // ellipse; a Gaussian that would drop T below min_T is skipped for that pixel only.
-// Used as the CPU baseline. threads > 1 splits the image into column bands, each thread
-// walking all Gaussians over its own columns: per-pixel order is unchanged, so the output
-// equals the single-threaded one bit for bit.
+// Used as the CPU baseline. threads > 1 deals the image columns to the threads (thread k
+// takes the columns u = k + 1 mod threads), each walking all Gaussians over its own columns:
+// per-pixel order is unchanged, so the output equals the single-threaded one bit for bit.
 // ------------------------------------------------------------------------------------
 
 namespace {
@@ -574,9 +575,11 @@ struct CpuGaussian2D {
     float mux, muy, a, m11, m21, m22, depth, rgb[3];
 };
 
+// Splats the Gaussians (in `order`) over the image columns u in [u_lo, u_hi] with
+// u = u_first (mod u_step).
 void cpu_render_band(const std::vector<CpuGaussian2D>& gs, const std::vector<int64_t>& order,
-                     const tdgs_camera& cam, const tdgs_render_options& o, int u_lo, int u_hi,
-                     float* rgb, float* T_img) {
+                     const tdgs_camera& cam, const tdgs_render_options& o, int u_lo, int u_hi, int u_first,
+                     int u_step, float* rgb, float* T_img) {
     const int W = cam.width, H = cam.height;
     for (int64_t oi : order) {
         const CpuGaussian2D& g = gs[oi];
@@ -588,10 +591,11 @@ void cpu_render_band(const std::vector<CpuGaussian2D>& gs, const std::vector<int
         const float us = ceilf(g.mux - x_radius + 0.5f);
         const float ue = rintf(g.mux + x_radius);
         if (!(us == us) || !(ue == ue)) continue;
-        const int u_start = std::max(u_lo, (int)clampf(us, 1.0f, (float)W + 1.0f));
+        int u_start = std::max(u_lo, (int)clampf(us, 1.0f, (float)W + 1.0f));
         const int u_end = std::min(u_hi, (int)clampf(ue, 0.0f, (float)W));
+        u_start += ((u_first - u_start) % u_step + u_step) % u_step;   // next column of the stride
         const float ir = 1.0f / r;
-        for (int u = u_start; u <= u_end; ++u) {
+        for (int u = u_start; u <= u_end; u += u_step) {
             const float du = ((float)u - 0.5f) - g.mux;
             const float disc = fmaf(r, gamma, -(du * du));
             const float sq = disc <= 0.0f ? 0.0f : sqrtf(idet * disc);
@@ -621,14 +625,13 @@ void cpu_render_band(const std::vector<CpuGaussian2D>& gs, const std::vector<int
 }
 }  // namespace
 
-void cpu_render_reference(const tdgs_gaussians* g, const tdgs_camera* cam,
-                          const tdgs_render_options* opt, int32_t threads, float* rgb,
-                          float* T_img) {
-    const int64_t P = (int64_t)cam->width * cam->height;
-    std::fill(rgb, rgb + 3 * P, 0.0f);
-    std::fill(T_img, T_img + P, 1.0f);
+namespace {
+// The per-Gaussian part of the reference CPU renderer: cull, project and colour every
+// Gaussian, then a stable sort by depth (forward_core.jl:25-116).
+void cpu_reference_prepare(const tdgs_gaussians* g, const tdgs_camera* cam, const tdgs_render_options* opt,
+                           std::vector<CpuGaussian2D>& gs, std::vector<int64_t>& order) {
     const int hs = h_of(g->sh_degree);
-    std::vector<CpuGaussian2D> gs;
+    gs.clear();
     gs.reserve(g->n);
     tdgs_tiling unit{1, 1, cam->width, cam->height};
     for (int64_t i = 0; i < g->n; ++i) {
@@ -648,25 +651,62 @@ void cpu_render_reference(const tdgs_gaussians* g, const tdgs_camera* cam,
         project_color(*cam, opt->sh_degree, g->sh + (int64_t)3 * hs * i, hs, mo[0], mo[1], mo[2], c.rgb);
         gs.push_back(c);
     }
-    std::vector<int64_t> order(gs.size());
+    order.resize(gs.size());
     std::iota(order.begin(), order.end(), 0);
-    std::stable_sort(order.begin(), order.end(),
-                     [&](int64_t a, int64_t b) { return gs[a].depth < gs[b].depth; });
+    std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) { return gs[a].depth < gs[b].depth; });
+}
+
+// Splat the sorted Gaussians over the image columns u = u_first (mod u_step) with `threads`
+// threads, thread k taking every threads-th of those columns.
+void cpu_reference_splat(const std::vector<CpuGaussian2D>& gs, const std::vector<int64_t>& order,
+                         const tdgs_camera* cam, const tdgs_render_options* opt, int32_t threads, int u_first,
+                         int u_step, float* rgb, float* T_img) {
     const int W = cam->width;
     if (threads <= 1) {
-        cpu_render_band(gs, order, *cam, *opt, 1, W, rgb, T_img);
-    } else {
-        std::vector<std::thread> pool;
-        for (int k = 0; k < threads; ++k) {
-            const int lo = 1 + (int)((int64_t)W * k / threads);
-            const int hi = (int)((int64_t)W * (k + 1) / threads);
-            pool.emplace_back(cpu_render_band, std::cref(gs), std::cref(order), std::cref(*cam),
-                              std::cref(*opt), lo, hi, rgb, T_img);
-        }
-        for (auto& th : pool) th.join();
+        cpu_render_band(gs, order, *cam, *opt, 1, W, u_first, u_step, rgb, T_img);
+        return;
     }
+    std::vector<std::thread> pool;
+    for (int k = 0; k < threads; ++k)
+        pool.emplace_back(cpu_render_band, std::cref(gs), std::cref(order), std::cref(*cam), std::cref(*opt), 1, W,
+                          u_first + k * u_step, u_step * threads, rgb, T_img);
+    for (auto& th : pool) th.join();
+}
+}  // namespace
+
+void cpu_render_reference(const tdgs_gaussians* g, const tdgs_camera* cam,
+                          const tdgs_render_options* opt, int32_t threads, float* rgb,
+                          float* T_img) {
+    const int64_t P = (int64_t)cam->width * cam->height;
+    std::fill(rgb, rgb + 3 * P, 0.0f);
+    std::fill(T_img, T_img + P, 1.0f);
+    std::vector<CpuGaussian2D> gs;
+    std::vector<int64_t> order;
+    cpu_reference_prepare(g, cam, opt, gs, order);
+    cpu_reference_splat(gs, order, cam, opt, threads, 1, 1, rgb, T_img);
     for (int64_t i = 0; i < P; ++i)
         for (int c = 0; c < 3; ++c) rgb[3 * i + c] = fmaf(T_img[i], opt->background[c], rgb[3 * i + c]);
+}
+
+// Timing of the reference CPU renderer (std::chrono::steady_clock): seconds_out[0] = the
+// per-Gaussian part (cull, projection, colour, depth sort), seconds_out[1] = the splatting of
+// the image columns u = u_first (mod u_step) with `threads` threads. The images receive those
+// columns only.
+void cpu_render_reference_timed(const tdgs_gaussians* g, const tdgs_camera* cam, const tdgs_render_options* opt,
+                                int32_t threads, int32_t u_first, int32_t u_step, float* rgb, float* T_img,
+                                double* seconds_out) {
+    const int64_t P = (int64_t)cam->width * cam->height;
+    std::fill(rgb, rgb + 3 * P, 0.0f);
+    std::fill(T_img, T_img + P, 1.0f);
+    std::vector<CpuGaussian2D> gs;
+    std::vector<int64_t> order;
+    const auto t0 = std::chrono::steady_clock::now();
+    cpu_reference_prepare(g, cam, opt, gs, order);
+    const auto t1 = std::chrono::steady_clock::now();
+    cpu_reference_splat(gs, order, cam, opt, threads, u_first, u_step, rgb, T_img);
+    const auto t2 = std::chrono::steady_clock::now();
+    seconds_out[0] = std::chrono::duration<double>(t1 - t0).count();
+    seconds_out[1] = std::chrono::duration<double>(t2 - t1).count();
 }
 
 // Scalar helpers exposed for closed-form checks of the shared mathematics.

@@ -353,8 +353,12 @@ class Trainer:
 
     def __init__(self, gaussians: TrainableGaussiansVector, cameras, images, render_options: RenderOptions,
                  tiling: Tiling, training_options: TrainingOptions, optimizer: AdamOptimizer | None = None,
-                 seed: int = 0, device=0, fuse_optimizer: bool = True):
+                 seed: int = 0, device=0, fuse_optimizer: bool = True, record_adc: bool = False):
         self.device = _dev(device)
+        # record_adc: keep per density-control step the counts of pruned, cloned and split
+        # Gaussians in adc_history (three reductions and a synchronisation per ADC step)
+        self.record_adc = record_adc
+        self.adc_history = []
         # apply update! inside the backward projection when no density control intervenes
         self.fuse_optimizer = fuse_optimizer
         self.gaussians = gaussians
@@ -487,6 +491,14 @@ class Trainer:
                           it > o.opacity_reset_interval, float(np.log(f32(o.pruning_3d_max_scale))),
                           o.densification_mean2d_grad_norm_threshold_ndc,
                           float(np.log(f32(o.densification_size_threshold))))
+        if self.record_adc:
+            n = len(self.gaussians)
+            a = self.adc
+            dens = a.densify[:n].bool()
+            cl = dens & a.clone[:n].bool()
+            self.adc_history.append({"iteration": it, "before": n, "after": n_new,
+                                     "pruned": int(a.prune[:n].sum().item()), "cloned": int(cl.sum().item()),
+                                     "split": int((dens & ~cl).sum().item())})
         new = adaptive_density_control_(self.adc, self.gaussians, self.optimizer, n_new,
                                         float(np.log(f32(o.splitting_scale_factor))), self.seed * 1_000_003 + it)
         adc_remap_fgidx_(self.adc, self.render_buffers.fgidx_to_gidx, nbf)
