@@ -90,8 +90,9 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 // M and the factors once per (tile, Gaussian):
 //   dmu = M (sum out[0], sum out[1]),  dM11 = -sum out[3] / 2,  dM21 = -sum out[4],
 //   dM22 = -sum out[5] / 2.
-// out += [aa du, aa dv, G dalpha, aa du du, aa du dv, aa dv dv, T alpha g] with aa = alpha dalpha.
-__device__ __forceinline__ void backward_pair_sums(float alpha, float inv1ma, float G, float du, float dv,
+// out += [aa du, aa dv, G dalpha, aa du du, aa du dv, aa dv dv, T alpha g] with aa = alpha dalpha
+// (out = ... when first: the first of the lane's two pixels starts the sums).
+__device__ __forceinline__ void backward_pair_sums(bool first, float alpha, float inv1ma, float G, float du, float dv,
                                                    const float c[3], const float g[3], float* T, float* gpsi,
                                                    float out[9]) {
     const float Tn = *T * inv1ma;
@@ -101,24 +102,39 @@ __device__ __forceinline__ void backward_pair_sums(float alpha, float inv1ma, fl
     const float dalpha = inv1ma * (tgc - *gpsi);
     const float aa = alpha * dalpha;
     const float adu = aa * du, adv = aa * dv;
-    out[0] += adu;
-    out[1] += adv;
-    out[2] = fmaf(G, dalpha, out[2]);
-    out[3] = fmaf(adu, du, out[3]);
-    out[4] = fmaf(adu, dv, out[4]);
-    out[5] = fmaf(adv, dv, out[5]);
     const float ta = Tn * alpha;
-    out[6] = fmaf(ta, g[0], out[6]);
-    out[7] = fmaf(ta, g[1], out[7]);
-    out[8] = fmaf(ta, g[2], out[8]);
+    if (first) {
+        out[0] = adu;
+        out[1] = adv;
+        out[2] = G * dalpha;
+        out[3] = adu * du;
+        out[4] = adu * dv;
+        out[5] = adv * dv;
+        out[6] = ta * g[0];
+        out[7] = ta * g[1];
+        out[8] = ta * g[2];
+    } else {
+        out[0] += adu;
+        out[1] += adv;
+        out[2] = fmaf(G, dalpha, out[2]);
+        out[3] = fmaf(adu, du, out[3]);
+        out[4] = fmaf(adu, dv, out[4]);
+        out[5] = fmaf(adv, dv, out[5]);
+        out[6] = fmaf(ta, g[0], out[6]);
+        out[7] = fmaf(ta, g[1], out[7]);
+        out[8] = fmaf(ta, g[2], out[8]);
+    }
 }
 
 constexpr int kSlots = 7;   // 7 entries x 9 gradient components = 63 of the 64 lanes
 
+// The exponent is evaluated in base-2 units from a pre-scaled inverse covariance:
+// x = log2(e) * (-(M11 du^2 / 2 + M21 du dv + M22 dv^2 / 2)) = du (A du + B dv) + C dv^2, G = 2^x.
 struct __align__(16) BackRec {
-    float4 a;  // mu_x mu_y a M11
-    float4 b;  // M21 M22 r g
-    float4 c;  // b cut - -   (cut: exponent below which a * G < min_alpha)
+    float4 a;  // mu_x mu_y A B
+    float4 b;  // C cut a r     (cut: x below which a * G < min_alpha)
+    float4 c;  // g b f M11     (f: the Gaussian's index, for the flush)
+    float4 d;  // M21 M22 - -
 };
 
 struct BackBlendArgs {
@@ -214,21 +230,17 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
     while (hi > beg) {
         const int64_t lo = hi - NB > beg ? hi - NB : beg;
         const int nb = (int)(hi - lo);
-        bool low = false;   // a cut below -87 (tiny min_alpha, huge or NaN opacity)
         if (t < nb) {
             BackRec rec;
-            rec.a = make_float4(pr[0], pr[1], pr[2], pr[3]);
-            rec.b = make_float4(pr[4], pr[5], pr[6], pr[7]);
-            // a * exp_f(e) < min_alpha for e < cut (log_f and exp_f errors ~1e-6 absolute,
-            // inside the 1e-3 margin of log_min_alpha; a NaN cut never skips); the Gaussian's
-            // index rides along for the flush
-            rec.c = make_float4(pr[8], a.log_min_alpha - log_f(pr[2]), __builtin_bit_cast(float, pf), 0.0f);
+            rec.a = make_float4(pr[0], pr[1], -0.5f * kLog2e * pr[3], -kLog2e * pr[4]);
+            // a 2^x < min_alpha for x < cut (log_f error ~1e-7 absolute, inside the 1e-3 margin
+            // of log_min_alpha; a NaN cut never skips)
+            rec.b = make_float4(-0.5f * kLog2e * pr[5], kLog2e * (a.log_min_alpha - log_f(pr[2])), pr[2], pr[6]);
+            rec.c = make_float4(pr[7], pr[8], __builtin_bit_cast(float, pf), pr[3]);
+            rec.d = make_float4(pr[4], pr[5], 0.0f, 0.0f);
             s_rec[t] = rec;
-            low = !(rec.c.y >= -87.0f);
         }
-        // A live exponent lies in [cut, 0]; with every cut of the batch at least -87 that is
-        // inside exp_f's polynomial range, so the range vote is skipped.
-        const bool checked = __syncthreads_or(low);
+        __syncthreads();
         if (lo > beg) gather(lo - NB > beg ? lo - NB : beg, (int)(lo - (lo - NB > beg ? lo - NB : beg)));
         const int jtop = (int)((int64_t)wave_last - lo < nb ? (int64_t)wave_last - lo : nb);
         // entry jj of the batch is before pixel p's last contributor iff jj < last_rel[p]
@@ -237,50 +249,62 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
         // entries are kept per lane and summed over the wavefront in one transpose-sum, after
         // which lane l holds component l % 9 of slot l / 9 and adds it to the tile's LDS sum.
         int j = __builtin_amdgcn_readfirstlane(jtop - 1);   // wave-uniform: scalar loop control
+        const float max_alpha = a.max_alpha;
         while (j >= 0) {
             float v[64];
             int js[kSlots];
 #pragma unroll
             for (int e = 0; e < kSlots; ++e) {
                 js[e] = -1;
-                float o[9] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+                float* o = v + 9 * e;
                 while (j >= 0) {
                     const int jj = j--;
-                    const float4 ra = s_rec[jj].a, rb = s_rec[jj].b, rc = s_rec[jj].c;
-                    float du[2], dv[2], ex[2];
+                    const float4 ra = s_rec[jj].a, rb = s_rec[jj].b;
+                    const float2 rc = *reinterpret_cast<const float2*>(&s_rec[jj].c);
+                    float du[2], dv[2], x[2];
                     bool live[2];
+                    uint64_t any = 0;
 #pragma unroll
                     for (int p = 0; p < 2; ++p) {
-                        ex[p] = backward_exponent(cu[p], cv[p], ra.x, ra.y, ra.w, rb.x, rb.y, &du[p], &dv[p]);
-                        live[p] = on[p] && jj < last_rel[p] && !(ex[p] < rc.y);
+                        du[p] = cu[p] - ra.x;
+                        dv[p] = cv[p] - ra.y;
+                        x[p] = fmaf(fmaf(ra.z, du[p], ra.w * dv[p]), du[p], rb.x * dv[p] * dv[p]);
+                        // (an off pixel has last = 0, so jj < last_rel fails for it)
+                        const bool before = jj < last_rel[p], above = !(x[p] < rb.y);
+                        live[p] = before & above;
+                        // the vote as masks of the two compares (the mask of their conjunction
+                        // takes two more instructions)
+                        any |= __builtin_amdgcn_ballot_w64(before) & __builtin_amdgcn_ballot_w64(above);
                     }
-                    if (!wave_any(live[0] || live[1])) continue;
-                    bool contrib = false;
-                    const bool wide = checked && wave_any((live[0] && !(ex[0] >= -87.0f && ex[0] <= 88.0f)) ||
-                                                          (live[1] && !(ex[1] >= -87.0f && ex[1] <= 88.0f)));
-                    const float c[3] = {rb.z, rb.w, rc.x};
+                    if (any == 0) continue;
+                    const float c[3] = {rb.w, rc.x, rc.y};
 #pragma unroll
                     for (int p = 0; p < 2; ++p) {
-                        if (live[p]) {
-                            const float G = wide ? exp_f_sel(ex[p]) : exp_f_core(ex[p]);   // exp_f(ex)
-                            const float aG = ra.z * G;
-                            // min(aG, max_alpha): the select aG < max_alpha ? aG : max_alpha for a
-                            // non-NaN max_alpha, NaN aG included
-                            const float alpha = __builtin_fminf(aG, a.max_alpha);
-                            if (!(alpha < a.min_alpha)) {
-                                backward_pair_sums(alpha, __builtin_amdgcn_rcpf(1.0f - alpha), G, du[p], dv[p], c, g[p],
-                                                   &T[p], &gpsi[p], o);
-                                contrib = true;
-                            }
-                        }
+                        // G by the hardware base-2 exponential (v_exp_f32, ~1 ulp over the whole
+                        // float range): the gradients are checked at relative L2, and the forward
+                        // pass's bit-exact exp_f decides the contributors
+                        const float G = __builtin_amdgcn_exp2f(x[p]);
+                        const float aG = rb.z * G;
+                        // min(aG, max_alpha) (v_min_f32: a NaN aG gives max_alpha)
+                        float alpha;
+                        asm("v_min_f32 %0, %1, %2" : "=v"(alpha) : "s"(max_alpha), "v"(aG));
+                        const bool cp = live[p] & !(alpha < a.min_alpha);
+                        // Branch-free: a lane that does not contribute runs the same steps with
+                        // alpha = G = 0, so 1 / (1 - alpha) = 1 exactly and T, g . psi and the
+                        // sums are left unchanged.
+                        const float al = cp ? alpha : 0.0f;
+                        backward_pair_sums(p == 0, al, __builtin_amdgcn_rcpf(1.0f - al), cp ? G : 0.0f, du[p], dv[p],
+                                           c, g[p], &T[p], &gpsi[p], o);
                     }
-                    if (wave_any(contrib)) {
-                        js[e] = __builtin_amdgcn_readfirstlane(jj);
-                        break;
-                    }
+                    // The entry takes a slot when some lane of the wavefront is live for it (its
+                    // sums are zero if no lane's alpha reaches min_alpha after all).
+                    js[e] = __builtin_amdgcn_readfirstlane(jj);
+                    break;
                 }
+                if (js[e] < 0) {   // a slot left empty at the end of the batch sums zeros
 #pragma unroll
-                for (int k = 0; k < 9; ++k) v[9 * e + k] = o[k];
+                    for (int k = 0; k < 9; ++k) o[k] = 0.0f;
+                }
             }
             if (js[0] < 0) break;
             v[63] = 0.0f;
@@ -300,9 +324,9 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
             const int64_t f = __builtin_bit_cast(int32_t, s_rec[e].c.z);
             float v = s_acc[i];
             if (k < 2) {
-                const float4 rb = s_rec[e].b;
-                const float m_a = k == 0 ? s_rec[e].a.w : rb.x;   // M11 or M21
-                const float m_b = k == 0 ? rb.x : rb.y;           // M21 or M22
+                const float4 rd = s_rec[e].d;
+                const float m_a = k == 0 ? s_rec[e].c.w : rd.x;   // M11 or M21
+                const float m_b = k == 0 ? rd.x : rd.y;           // M21 or M22
                 v = fmaf(m_a, s_acc[9 * e], m_b * s_acc[9 * e + 1]);
             } else if (k == 3 || k == 5) {
                 v *= -0.5f;

@@ -405,31 +405,32 @@ __device__ __forceinline__ int emit_slot(int k) {
     return t * kEmitItems + ((i + t) & (kEmitItems - 1));
 }
 
-template <bool TILE16>
-__global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
-    int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
-    const int32_t* __restrict__ blk_first, const float* __restrict__ depths, const int32_t* __restrict__ ranges,
-    int32_t ntx, void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0,
-    uint32_t* __restrict__ counts0, int64_t count_tiles) {
-    __shared__ int32_t s_buf[kEmitTile + 1];
-    __shared__ int64_t s_range[2];
-    __shared__ uint32_t s_h[kRsBins];
+// The tile ids and values of keys d0 + ITEMS t + i (i < ITEMS) of emission block `block`
+// (d0 = block THREADS ITEMS), computed by thread t of a THREADS-thread workgroup into
+// tile[] and val[] (zeros past m). s_buf holds THREADS ITEMS + 1 ints of LDS; ends with a
+// workgroup barrier after its last use of s_buf and s_range.
+template <int THREADS, int ITEMS>
+__device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t block, const int32_t* __restrict__ sorted_f,
+                                              const int32_t* __restrict__ cs, const int32_t* __restrict__ blk_first,
+                                              const int32_t* __restrict__ ranges, int32_t ntx, int32_t* s_buf,
+                                              int64_t* s_range, int32_t (&tile)[ITEMS], int32_t (&val)[ITEMS]) {
+    constexpr int kBlock = THREADS * ITEMS;
+    static_assert(kBlock == kEmitTile, "emission blocks of kEmitTile keys");
     int32_t* const s_cs = s_buf;                      // [0, cnt]: scan values of the span
     int32_t* const s_f = s_buf + kEmitStage + 1;      // staged Gaussians: fgidx,
     int32_t* const s_t0 = s_f + kEmitStage;           // tile id of the rectangle's first tile,
     int32_t* const s_wx = s_t0 + kEmitStage;          // rectangle width in tiles
     const int t = threadIdx.x;
-    s_h[t] = 0;
-    const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
+    const int64_t d0 = block * kBlock;
     // Gaussians owning the block's first and last keys: from the block table of the count scan
     // (the next block's first Gaussian, or the one before it when that one starts exactly at
     // the next block), clamped to [0, nb)
-    if (t == 0) s_range[0] = blk_first[blockIdx.x];
+    if (t == 0) s_range[0] = blk_first[block];
     if (t == 1) {
-        const int64_t dn = d0 + kEmitTile;
+        const int64_t dn = d0 + kBlock;
         int64_t jh = nb - 1;
         if (dn < m) {
-            const int64_t jn = blk_first[blockIdx.x + 1];
+            const int64_t jn = blk_first[block + 1];
             const int64_t sn = jn <= 0 ? 0 : cs[jn - 1];
             jh = sn < dn ? jn : jn - 1;
         }
@@ -442,10 +443,10 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     if (j_lo < 0) j_lo = 0;
     if (j_lo > j_hi) j_lo = j_hi;
     const int64_t cnt = j_hi - j_lo + 1;  // Gaussians spanned (each owns >= 1 key here)
-    const bool staged = cnt <= kEmitTile; // always, with consistent counts
+    const bool staged = cnt <= kBlock;    // always, with consistent counts
     const bool full = cnt <= kEmitStage;
     if (staged) {
-        for (int64_t k = t; k <= cnt; k += kEmitThreads) {
+        for (int64_t k = t; k <= cnt; k += THREADS) {
             const int64_t j = j_lo + k - 1;
             s_cs[k] = j < 0 ? 0 : cs[j];
             if (full && k < cnt) {
@@ -464,8 +465,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
         const int64_t j = j_lo + k - 1;
         return j < 0 ? 0 : cs[j];
     };
-    int32_t tile[kEmitItems], val[kEmitItems];
-    const int64_t first = d0 + (int64_t)t * kEmitItems;
+    const int64_t first = d0 + (int64_t)t * ITEMS;
     if (first < m) {
         int64_t lo = 0, hi = cnt;   // largest k in [0, cnt) with start_of(k) <= first
         while (hi - lo > 1) {
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
         const int32_t local = (int32_t)(first - start_of(lo));
         int32_t q = local / wx, rx = local - q * wx;
 #pragma unroll
-        for (int i = 0; i < kEmitItems; ++i) {
+        for (int i = 0; i < ITEMS; ++i) {
             const int64_t d = first + i;
             if (d >= nxt && lo + 1 < cnt) {   // next Gaussian (each owns >= 1 key)
                 ++lo;
@@ -506,12 +506,29 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < kEmitItems; ++i) tile[i] = val[i] = 0;
+        for (int i = 0; i < ITEMS; ++i) tile[i] = val[i] = 0;
     }
+    __syncthreads();   // s_buf is free again
+}
+
+template <bool TILE16>
+__global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
+    int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
+    const int32_t* __restrict__ blk_first, const float* __restrict__ depths, const int32_t* __restrict__ ranges,
+    int32_t ntx, void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0,
+    uint32_t* __restrict__ counts0, int64_t count_tiles) {
+    __shared__ int32_t s_buf[kEmitTile + 1];
+    __shared__ int64_t s_range[2];
+    __shared__ uint32_t s_h[kRsBins];
+    const int t = threadIdx.x;
+    s_h[t] = 0;
+    const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
+    int32_t tile[kEmitItems], val[kEmitItems];
+    emit_generate<kEmitThreads, kEmitItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf, s_range,
+                                            tile, val);
     // values, then tile ids (or keys), through LDS to coalesced stores
     const int64_t nk = m - d0 < kEmitTile ? m - d0 : kEmitTile;
     const uint32_t mask0 = (1u << nbits0) - 1u;
-    __syncthreads();
 #pragma unroll
     for (int i = 0; i < kEmitItems; ++i) s_buf[t * kEmitItems + ((i + t) & (kEmitItems - 1))] = val[i];
     __syncthreads();
@@ -541,6 +558,84 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     }
     __syncthreads();
     counts0[(int64_t)t * count_tiles + blockIdx.x] = s_h[t];
+}
+
+// The 16-bit tile sort's first pass fused with key emission: emission blocks are radix tiles
+// (kEmitTile keys), generated twice instead of written and read back.
+//   k_emit_count:   the first-pass digit (low nbits0 bits of the tile id) histogram of each
+//                   block's keys, counts0[d][block], for k_rs_scan_rows;
+//   k_emit_scatter: the keys again, moved through LDS into the radix tile layout (wavefront
+//                   w, item k, lane l <-> key w 512 + k 64 + l), then rs_scatter_tile writes
+//                   tile ids and values straight to their first-pass sorted positions.
+constexpr int kEmitSortThreads = kRsThreads;
+constexpr int kEmitSortItems = kEmitTile / kEmitSortThreads;
+static_assert(kEmitSortItems == RsTile<uint16_t>::kItems, "radix tile layout");
+
+__global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int64_t m,
+                                                                 const int32_t* __restrict__ sorted_f,
+                                                                 const int32_t* __restrict__ cs,
+                                                                 const int32_t* __restrict__ blk_first,
+                                                                 const int32_t* __restrict__ ranges, int32_t ntx,
+                                                                 int nbits0, uint32_t* __restrict__ counts0,
+                                                                 int64_t count_tiles) {
+    __shared__ int32_t s_buf[kEmitTile + 1];
+    __shared__ int64_t s_range[2];
+    __shared__ uint32_t s_h[kRsBins];
+    const int t = threadIdx.x;
+    if (t < kRsBins) s_h[t] = 0;
+    int32_t tile[kEmitSortItems], val[kEmitSortItems];
+    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf,
+                                                    s_range, tile, val);
+    const int64_t first = (int64_t)blockIdx.x * kEmitTile + (int64_t)t * kEmitSortItems;
+    const uint32_t mask0 = (1u << nbits0) - 1u;
+#pragma unroll
+    for (int i = 0; i < kEmitSortItems; ++i)
+        if (first + i < m) atomicAdd(&s_h[(uint32_t)tile[i] & mask0], 1u);
+    __syncthreads();
+    if (t < kRsBins) counts0[(int64_t)t * count_tiles + blockIdx.x] = s_h[t];
+}
+
+// Slot of key k of the block in k_emit_scatter's transpose (thread k / 8 writes item k % 8,
+// rotated by the thread index so that neither the writes nor the radix-layout reads of a
+// wavefront meet in one bank).
+__device__ __forceinline__ int emit_sort_slot(int k) {
+    const int t = k / kEmitSortItems, i = k % kEmitSortItems;
+    return t * kEmitSortItems + ((i + t) & (kEmitSortItems - 1));
+}
+
+__global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
+    int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
+    const int32_t* __restrict__ blk_first, const int32_t* __restrict__ ranges, int32_t ntx, int nbits0,
+    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, int64_t count_tiles,
+    uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err) {
+    __shared__ int32_t s_buf[kEmitTile + 1];
+    __shared__ int64_t s_range[2];
+    const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
+    const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
+    int32_t tile[kEmitSortItems], val[kEmitSortItems];
+    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf,
+                                                    s_range, tile, val);
+    uint16_t key[kEmitSortItems];
+    int32_t v[kEmitSortItems];
+    bool valid[kEmitSortItems];
+#pragma unroll
+    for (int i = 0; i < kEmitSortItems; ++i) s_buf[t * kEmitSortItems + ((i + t) & (kEmitSortItems - 1))] = tile[i];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kEmitSortItems; ++k) {
+        const int q = w * (kEmitSortItems * kWave) + k * kWave + lane;
+        key[k] = (uint16_t)s_buf[emit_sort_slot(q)];
+        valid[k] = d0 + q < m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kEmitSortItems; ++i) s_buf[t * kEmitSortItems + ((i + t) & (kEmitSortItems - 1))] = val[i];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kEmitSortItems; ++k) v[k] = s_buf[emit_sort_slot(w * (kEmitSortItems * kWave) + k * kWave + lane)];
+    // (rs_scatter_tile reuses s_buf for its staging after its first barrier)
+    rs_scatter_tile<uint16_t>(key, v, valid, blockIdx.x, m, 0, nbits0, offsets, totals, count_tiles, kout, vout, err,
+                              nullptr, reinterpret_cast<uint32_t*>(s_buf));
 }
 
 // fill_df2dgs_codes_and_dfgidx_to_fgidx_kernel! (forward_core.jl:531-603): reference
@@ -1471,47 +1566,63 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         set_error("key buffers hold %lld keys, %lld needed", (long long)buf->key_capacity, (long long)m);
         return TDGS_ERR_CAPACITY;
     }
-    // 6-7: emit in depth order, then stable sort on the tile bits. With at most 65535 tiles
-    // the sort moves 16-bit tile ids (two arrays carved from buf->keys) and the values; the
-    // 64-bit keys are assembled after it. The first radix pass writes the output arrays when
-    // the pass count is odd and the alternate ones when even; emit into the other.
+    // 6-7: emit in depth order, then stable sort on the tile bits. With at most 65535 tiles the
+    // sort moves 16-bit tile ids (two arrays carved from buf->keys) and the values, and its
+    // first pass is fused with emission (k_emit_count, k_rs_scan_rows, k_emit_scatter: the keys
+    // are generated twice instead of written and read back); the remaining bits take at most
+    // one more pass. Beyond 65535 tiles emission writes 64-bit keys (with the first pass's
+    // counts) and radix_sort_pairs sorts their tile bits.
     const int eb = end_bit_of(tiling);
     const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
     const bool tile16 = nb_tiles <= 65535;
     const int tb = tile16 ? 0 : 32;   // first tile bit of the sorted key
     const int te_bit = tile16 ? eb - 32 : eb;
     const int passes = radix_passes(tb, te_bit);
-    const bool emit_into_out = (passes % 2) == 0;
+    const int nbits0 = radix_digit_bits(tb, te_bit);   // digit of the first tile-sort pass
     uint16_t* t16_out = reinterpret_cast<uint16_t*>(buf->keys);
     uint16_t* t16_alt = t16_out + buf->key_capacity;
-    void* ek = tile16 ? (void*)(emit_into_out ? t16_out : t16_alt)
-                      : (void*)(emit_into_out ? buf->sorted_keys : buf->keys);
-    int32_t* ev2 = emit_into_out ? buf->sorted_values : buf->values;
-    const int64_t count_tiles = tile16 ? radix_tiles<uint16_t>(m) : radix_tiles<uint64_t>(m);
-    {
-        StageScope sc(TDGS_STAGE_EMIT, s);
-        const int nbits0 = radix_digit_bits(tb, te_bit);   // digit of the first tile-sort pass
-        const unsigned grid = (unsigned)ceil_div(m, kEmitTile);
-        if (tile16)
-            k_emit_depth_order<true><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->depths,
-                                                                  buf->tile_ranges, tiling->nb_tiles_x, ek, ev2,
-                                                                  nbits0, radix_count_table(rtemp), count_tiles);
-        else
-            k_emit_depth_order<false><<<grid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->depths,
-                                                                   buf->tile_ranges, tiling->nb_tiles_x, ek, ev2,
-                                                                   nbits0, radix_count_table(rtemp), count_tiles);
-        TDGS_LAUNCHED();
-    }
-    {
+    const unsigned egrid = (unsigned)ceil_div(m, kEmitTile);
+    if (tile16) {
+        const int64_t count_tiles = radix_tiles<uint16_t>(m);
+        uint32_t* table = radix_count_table(rtemp);
+        uint32_t* totals = radix_totals(rtemp, m);
+        const bool one_pass = passes == 1;
+        {
+            StageScope sc(TDGS_STAGE_EMIT, s);
+            k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->tile_ranges,
+                                                            tiling->nb_tiles_x, nbits0, table, count_tiles);
+            TDGS_LAUNCHED();
+        }
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
-        if (tile16)
-            TDGS_TRY(radix_sort_pairs<uint16_t>((const uint16_t*)ek, t16_out, ev2, buf->sorted_values, t16_alt,
-                                                buf->values, m, tb, te_bit, rtemp, rbytes, s,
-                                                radix_count_table(rtemp), d_err));
-        else
-            TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
-                                                buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, tb,
-                                                te_bit, rtemp, rbytes, s, radix_count_table(rtemp), d_err));
+        k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals);
+        TDGS_LAUNCHED();
+        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->tile_ranges,
+                                                          tiling->nb_tiles_x, nbits0, table, totals, count_tiles,
+                                                          one_pass ? t16_out : t16_alt,
+                                                          one_pass ? buf->sorted_values : buf->values, d_err);
+        TDGS_LAUNCHED();
+        if (!one_pass)
+            TDGS_TRY(radix_sort_pairs<uint16_t>(t16_alt, t16_out, buf->values, buf->sorted_values, t16_alt,
+                                                buf->values, m, tb + nbits0, te_bit, rtemp, rbytes, s, nullptr,
+                                                d_err));
+    } else {
+        // the first radix pass writes the output arrays when the pass count is odd and the
+        // alternate ones when even; emit into the other
+        const bool emit_into_out = (passes % 2) == 0;
+        void* ek = emit_into_out ? (void*)buf->sorted_keys : (void*)buf->keys;
+        int32_t* ev2 = emit_into_out ? buf->sorted_values : buf->values;
+        const int64_t count_tiles = radix_tiles<uint64_t>(m);
+        {
+            StageScope sc(TDGS_STAGE_EMIT, s);
+            k_emit_depth_order<false><<<egrid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->depths,
+                                                                    buf->tile_ranges, tiling->nb_tiles_x, ek, ev2,
+                                                                    nbits0, radix_count_table(rtemp), count_tiles);
+            TDGS_LAUNCHED();
+        }
+        StageScope sc(TDGS_STAGE_TILE_SORT, s);
+        TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
+                                            buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, tb, te_bit,
+                                            rtemp, rbytes, s, radix_count_table(rtemp), d_err));
     }
     // 8: tile ranges
     {

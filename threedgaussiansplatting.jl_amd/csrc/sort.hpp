@@ -20,6 +20,8 @@
 // round trips of ~2.5 us under load, which halved the scatter's 5.6 TB/s.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace tdgs {
@@ -155,58 +157,52 @@ static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restric
     if (t == 0) totals[blockIdx.x] = carry;
 }
 
+// The scatter of one radix tile (tile index `tile`, kRsThreads threads) whose keys and values
+// are in registers: thread t = (wave w, lane l) holds in item k the key of tile index
+// w kItems 64 + k 64 + l, valid[k] false for keys that are not sorted (past n, or dropped).
+// Ranks the keys stably (per-wavefront ballot match with per-wave digit counters in LDS,
+// items in index order), stages the tile in digit order in s_raw (kTile 32-bit words, or
+// 64-bit for 64-bit keys), and writes keys and values out as contiguous per-digit runs at
+// totals-prefix[d] + offsets[d][tile] + rank. `n` bounds the output index (an inconsistent
+// count sets *err instead of writing out of bounds). When d_kept is not null, tile 0 writes
+// the number of keys sorted in all.
 template <class K>
-__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_rs_scatter(
-    const K* __restrict__ kin, const int32_t* __restrict__ vin, K* __restrict__ kout,
-    int32_t* __restrict__ vout, int64_t n, int shift, int nbits, const uint32_t* __restrict__ offsets,
-    const uint32_t* __restrict__ totals, int64_t tiles, uint32_t* err, const int64_t* d_n, int drop_max,
-    int64_t* d_kept) {
+__device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems], const int32_t (&val)[RsTile<K>::kItems],
+                                                const bool (&valid)[RsTile<K>::kItems], int64_t tile, int64_t n,
+                                                int shift, int nbits, const uint32_t* __restrict__ offsets,
+                                                const uint32_t* __restrict__ totals, int64_t tiles,
+                                                K* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err,
+                                                int64_t* d_kept, uint32_t* s_raw) {
     constexpr int kRsItems = RsTile<K>::kItems;
     constexpr int kRsTile = RsTile<K>::kTile;
-    // the tile in digit order: keys, then values (room for whichever is wider)
-    constexpr int kBufWords = kRsTile * (sizeof(K) > 4 ? (int)sizeof(K) : 4) / 4;
-    __shared__ uint32_t s_raw[kBufWords];
-    K* s_buf = reinterpret_cast<K*>(s_raw);
+    // Keys narrower than 32 bits are staged as 32-bit words: lanes storing 16-bit keys to
+    // neighbouring positions would share LDS words, which the hardware serialises.
+    using Stage = typename std::conditional<(sizeof(K) < 4), uint32_t, K>::type;
+    Stage* s_buf = reinterpret_cast<Stage*>(s_raw);
     __shared__ uint32_t s_wh[kRsWaves][kRsBins];  // per-wave digit counts -> offsets
     __shared__ uint32_t s_local[kRsBins];         // start of each digit inside the tile
     __shared__ int32_t s_delta[kRsBins];          // output index - tile-local index
     __shared__ uint32_t s_tmp[kRsWaves];
-
     __shared__ uint32_t s_tile_n;                 // keys of the tile that are sorted
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const bool owner = t < kRsBins;
-    const int64_t tile = blockIdx.x;
-    if (d_n) n = *d_n;
     const uint32_t total_t = owner ? totals[t] : 0u;
     const uint32_t off_t = owner ? offsets[(int64_t)t * tiles + tile] : 0u;
     for (int i = t; i < kRsWaves * kRsBins; i += kRsThreads) (&s_wh[0][0])[i] = 0;
     __syncthreads();
-    const int32_t base = (int32_t)(tile * kRsTile);
     const uint32_t mask = (1u << nbits) - 1u;
-    const int32_t wbase = base + w * (kRsItems * kWave) + lane;
     const int32_t nn = (int32_t)n;
-
-    K key[kRsItems];
-    int32_t val[kRsItems];
     uint32_t pos[kRsItems];
-#pragma unroll
-    for (int k = 0; k < kRsItems; ++k) {
-        const int32_t i = wbase + k * kWave;
-        key[k] = i < nn ? kin[i] : (K)0;
-        val[k] = i < nn ? vin[i] : 0;
-    }
     // Rank inside the wavefront, items in index order: the first lane of each group of equal
     // digits advances the wave's counter for that digit after every lane has read it.
-    bool keep[kRsItems];
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        keep[k] = wbase + k * kWave < nn && !(drop_max && key[k] == (K)~(K)0);
         const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
-        const uint64_t peers = match_digit(d, nbits, keep[k]);
+        const uint64_t peers = match_digit(d, nbits, valid[k]);
         const uint64_t below = peers & lanemask_lt();
         const uint32_t cnt = s_wh[w][d];
         pos[k] = cnt + (uint32_t)__popcll(below);
-        if (keep[k] && below == 0) s_wh[w][d] = cnt + (uint32_t)__popcll(peers);
+        if (valid[k] && below == 0) s_wh[w][d] = cnt + (uint32_t)__popcll(peers);
     }
     __syncthreads();
 
@@ -236,10 +232,10 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     // Stage keys in digit order, then write contiguous runs per digit.
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        if (keep[k]) {
+        if (valid[k]) {
             const uint32_t d = (uint32_t)(key[k] >> shift) & mask;
             pos[k] += s_local[d] + s_wh[w][d];
-            if (pos[k] < (uint32_t)kRsTile) s_buf[pos[k]] = key[k];
+            if (pos[k] < (uint32_t)kRsTile) s_buf[pos[k]] = (Stage)key[k];
         }
     }
     __syncthreads();
@@ -250,7 +246,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
         const int i = k * kRsThreads + t;
         opos[k] = -1;
         if (i < tile_n) {
-            const K kk = s_buf[i];
+            const K kk = (K)s_buf[i];
             const uint32_t d = (uint32_t)(kk >> shift) & mask;
             const int32_t o = s_delta[d] + i;
             if (o >= 0 && o < nn) {
@@ -265,7 +261,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     int32_t* s_val = reinterpret_cast<int32_t*>(s_raw);
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
-        if (keep[k] && pos[k] < (uint32_t)kRsTile) s_val[pos[k]] = val[k];
+        if (valid[k] && pos[k] < (uint32_t)kRsTile) s_val[pos[k]] = val[k];
     }
     __syncthreads();
 #pragma unroll
@@ -273,6 +269,42 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
         const int i = k * kRsThreads + t;
         if (opos[k] >= 0) vout[opos[k]] = s_val[i];
     }
+}
+
+// Words of LDS rs_scatter_tile stages a tile of K keys in.
+template <class K>
+constexpr int rs_stage_words() {
+    return RsTile<K>::kTile * (sizeof(K) > 4 ? (int)sizeof(K) : 4) / 4;
+}
+
+template <class K>
+__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_rs_scatter(
+    const K* __restrict__ kin, const int32_t* __restrict__ vin, K* __restrict__ kout,
+    int32_t* __restrict__ vout, int64_t n, int shift, int nbits, const uint32_t* __restrict__ offsets,
+    const uint32_t* __restrict__ totals, int64_t tiles, uint32_t* err, const int64_t* d_n, int drop_max,
+    int64_t* d_kept) {
+    constexpr int kRsItems = RsTile<K>::kItems;
+    constexpr int kRsTile = RsTile<K>::kTile;
+    __shared__ uint32_t s_raw[rs_stage_words<K>()];
+    const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
+    const int64_t tile = blockIdx.x;
+    if (d_n) n = *d_n;
+    const int32_t base = (int32_t)(tile * kRsTile);
+    const int32_t wbase = base + w * (kRsItems * kWave) + lane;
+    const int32_t nn = (int32_t)n;
+    K key[kRsItems];
+    int32_t val[kRsItems];
+    bool valid[kRsItems];
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        const int32_t i = wbase + k * kWave;
+        key[k] = i < nn ? kin[i] : (K)0;
+        val[k] = i < nn ? vin[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) valid[k] = wbase + k * kWave < nn && !(drop_max && key[k] == (K)~(K)0);
+    rs_scatter_tile<K>(key, val, valid, tile, n, shift, nbits, offsets, totals, tiles, kout, vout, err,
+                       drop_max ? d_kept : nullptr, s_raw);
 }
 
 inline int radix_passes(int begin_bit, int end_bit) {
@@ -293,6 +325,11 @@ inline int64_t radix_tiles(int64_t n) { return ceil_div(n > 0 ? n : 1, RsTile<K>
 // The count table inside radix_sort_pairs' scratch, for producers that fill the first
 // pass's counts themselves.
 inline uint32_t* radix_count_table(void* temp) { return (uint32_t*)temp; }
+
+// The digit totals inside radix_sort_pairs' scratch for n keys (after the count table).
+inline uint32_t* radix_totals(void* temp, int64_t n) {
+    return (uint32_t*)((char*)temp + align_up((size_t)ceil_div(n > 0 ? n : 1, kRsMinTile) * kRsBins * sizeof(uint32_t)));
+}
 
 // Scratch for radix_sort_pairs, excluding the ping-pong buffers: the digit-major count
 // table, the digit totals and an error word.
@@ -342,7 +379,7 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
     }
     const int64_t tiles = radix_tiles<K>(n);
     uint32_t* counts = (uint32_t*)temp;
-    uint32_t* totals = (uint32_t*)((char*)temp + align_up((size_t)ceil_div(n, kRsMinTile) * kRsBins * sizeof(uint32_t)));
+    uint32_t* totals = radix_totals(temp, n);
     if (!err) err = totals + kRsBins;
     const K* src_k = kin;
     const int32_t* src_v = vin;
