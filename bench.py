@@ -141,6 +141,10 @@ def train_bench(core, w, cams, tiling, deg, steps, warmup):
     opts = host.RenderOptions.for_camera(cams[0], deg)
     to = training.TrainingOptions.for_scene(host.scene_radius(cams), sh_degree_increase_interval=10**9)
     tr = training.Trainer(g, cams, images, opts, tiling, to, seed=1)
+    # key arrays sized on every camera (synchronous renders grow them): the steps without
+    # density control then run without host synchronisation and none is skipped
+    for c in cams:
+        core.render_(tr.render_outputs, g, c, tiling, opts, tr.render_buffers)
     for _ in range(warmup):
         tr.training_step_()
     torch.cuda.synchronize()
@@ -150,6 +154,8 @@ def train_bench(core, w, cams, tiling, deg, steps, warmup):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     loss = tr.current_loss()
+    tr._grow_keys_from_monitor()
+    assert tr.skipped_steps == 0, "a timed step's keys did not fit the key arrays"
     # stage times from further steps with the stage profiler on (its events are not in the
     # timed loop above)
     L = core.lib()
@@ -515,19 +521,36 @@ def main():
     buf = core.RenderBuffers(len(g), tiling, 0)
     ncam = len(cams)
 
+    # size the key arrays on every camera the timed frames use (synchronous renders, which grow
+    # them), then warm up
+    used = sorted({k % ncam for k in range(args.steps)})
+    for k in used:
+        core.render_(out, g, cams[k], tiling, opts, buf)
     for k in range(args.warmup):
-        core.render_(out, g, cams[k % ncam], tiling, opts, buf)
+        core.render_(out, g, cams[k % ncam], tiling, opts, buf, device_counts=True)
     torch.cuda.synchronize()
 
-    # the timed frames: nothing but render! calls (no events, no stage profiler)
+    # the timed frames: nothing but render! calls (no events, no stage profiler), without host
+    # synchronisation (device-side counts); the frame monitor confirms afterwards that every
+    # frame's keys fit
+    mon = C.POINTER(C.c_int64)()
+    core.check(core.lib().tdgs_ctx_frame_monitor(core.context(0), C.byref(mon)))
+    overflows0 = int(mon[2])
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        core.render_(out, g, cams[k % ncam], tiling, opts, buf, device_counts=True)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    assert int(mon[2]) == overflows0, "a timed frame's keys did not fit the key arrays"
+    wall_ms = (t1 - t0) * 1000.0 / args.steps
+    fps = 1000.0 / wall_ms
+    # the same frames with the counts read on the host every frame (the reference's flow)
     t0 = time.perf_counter()
     for k in range(args.steps):
         core.render_(out, g, cams[k % ncam], tiling, opts, buf)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall_ms = (t1 - t0) * 1000.0 / args.steps
-    fps = 1000.0 / wall_ms
+    fps_sync = args.steps / (time.perf_counter() - t0)
     # per-frame times (HIP events around each frame) and stage times (the library's stage
     # profiler), each over one more pass of the cameras
     nextra = min(args.steps, ncam)
@@ -535,20 +558,20 @@ def main():
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(nextra)]
     for k in range(nextra):
         starts[k].record()
-        core.render_(out, g, cams[k % ncam], tiling, opts, buf)
+        core.render_(out, g, cams[k % ncam], tiling, opts, buf, device_counts=True)
         ends[k].record()
     torch.cuda.synchronize()
     frame_ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
     L = core.lib()
     core.check(L.tdgs_profile_begin(C.c_int32(16 * nextra + 64)))
     for k in range(nextra):
-        core.render_(out, g, cams[k % ncam], tiling, opts, buf)
+        core.render_(out, g, cams[k % ncam], tiling, opts, buf, device_counts=True)
     torch.cuda.synchronize()
     ms = (C.c_double * 13)()
     cnt = (C.c_int64 * 13)()
     core.check(L.tdgs_profile_end(ms, cnt))
+    assert int(mon[2]) == overflows0, "a frame's keys did not fit the key arrays"
 
-    used = sorted({k % ncam for k in range(args.steps)})
     st = frame_stats(core, g, cams, tiling, opts, buf, used)
     n = len(g)
     nf, nb, m, evals, evals_live, evals_contrib, evals_back = st.mean(axis=0)
@@ -616,6 +639,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": w.name, "gaussians": n, "width": cam0.width, "height": cam0.height,
                    "sh_degree": deg, "tile": list(w.tile), "cameras": ncam, "outputs": "rgb+T"},
+        "host_sync_per_frame": False,
+        "frames_per_s_host_counts": round(fps_sync, 2),
         "frame_ms_p50": round(float(np.percentile(frame_ms, 50)), 4),
         "frame_ms_p99": round(float(np.percentile(frame_ms, 99)), 4),
         "mean_counts": {"filtered": round(nf), "nonempty": round(nb), "keys": round(m),

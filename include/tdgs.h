@@ -64,6 +64,16 @@ enum { TDGS_CLIP_CLAMP = 0, TDGS_CLIP_FILTER = 1 };  /* CovarianceBoundaryClamp 
  * docs/src/math.md:194-197): the derivative of f^2, not of f. That is reproduced by default; this
  * flag uses the derivative of f instead (d(f^2)/dSigma / (2 f), zero where f is clamped to aa_min). */
 #define TDGS_FLAG_EXACT_AA_GRADIENT 0x2
+/* tdgs_render without host synchronisation (no counterpart in the reference, which reads the
+ * filtered and key counts on the host every frame, forward_core.jl:231-233, 259-264): the
+ * launches after the count scan are sized by buf->key_capacity and read the counts on the
+ * device; *nb_fgaussians_out and *nb_keys_out are set to -1 and the frame's counts stay in
+ * device memory (tdgs_render_counts reads them; the entry points below that take
+ * nb_fgaussians accept -1 with the render buffers and read them there). A key count above
+ * buf->key_capacity renders the frame as render_void! would and sets the frame status to
+ * TDGS_FRAME_KEY_CAPACITY (nb_keys still says how many keys are needed); the fused backward
+ * projection + Adam then leaves the parameters untouched. Needs at most 65535 tiles. */
+#define TDGS_FLAG_DEVICE_COUNTS 0x4
 
 /* PinholeCamera (src/cameras.jl:50-106): P = K [R^T | -R^T t] cached as 3x4, row-major here. */
 typedef struct tdgs_camera {
@@ -348,6 +358,21 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
                 tdgs_render_buffers* buf, const tdgs_render_outputs* out,
                 int32_t* nb_fgaussians_out, int64_t* nb_keys_out);
 
+/* Frame status of a render with TDGS_FLAG_DEVICE_COUNTS. */
+enum { TDGS_FRAME_OK = 0, TDGS_FRAME_KEY_CAPACITY = 1, TDGS_FRAME_KEY_RANGE = 2 /* M >= 2^31 */ };
+
+/* The counts of the last tdgs_render with TDGS_FLAG_DEVICE_COUNTS into these buffers:
+ * counts_out[0..3] = nb_fgaussians, nb_keys, non-empty Gaussians, frame status. Synchronises
+ * the stream. (They live in the first 32 bytes of buf->temp.) No reference counterpart. */
+int tdgs_render_counts(void* stream, const tdgs_render_buffers* buf, int64_t* counts_out);
+
+/* Frame monitor of the context's TDGS_FLAG_DEVICE_COUNTS renders, in pinned host memory that
+ * the device updates at every such frame: [frames, largest key count, frames whose keys did
+ * not fit the key arrays, last key count]. Readable at any time without synchronisation (the
+ * frames still in flight are not counted yet); lets a training loop grow its key arrays ahead
+ * of need. No reference counterpart. */
+int tdgs_ctx_frame_monitor(tdgs_ctx* ctx, const int64_t** monitor_out);
+
 /* The sorted keys of the last tdgs_render with these buffers and tiling (nb_keys keys), as
  * the reference's RenderBuffers hold them after sort_keys_and_sdfgidx!
  * (forward_core.jl:641-659): (tile << 32) | depth bits, ascending, into buf->sorted_keys.
@@ -359,7 +384,10 @@ int tdgs_render_sorted_keys(void* stream, const tdgs_tiling* tiling, const tdgs_
 
 /* backward! (backward_core.jl:37-72): zero the 2D gradients, replay the tiles back to
  * front, then the backward projection to 3D gradients. Uses the buffers of the preceding
- * tdgs_render call with the same arguments; out must hold T and last. */
+ * tdgs_render call with the same arguments; out must hold T and last. nb_fgaussians < 0
+ * (here and in tdgs_backward_project / tdgs_backward_project_adam) takes the filtered count
+ * of a TDGS_FLAG_DEVICE_COUNTS render from buf on the device (grads->capacity must then be at
+ * least buf->capacity; the 2D gradients are zeroed over the whole capacity). */
 int tdgs_backward(void* stream, tdgs_gradients* grads, const float* rgb_grad,
                   const tdgs_render_outputs* out, const tdgs_gaussians* g,
                   const tdgs_camera* cam, const tdgs_tiling* tiling,
@@ -404,6 +432,12 @@ int tdgs_adam_step(void* stream, tdgs_gaussians* g, tdgs_adam_state* st,
 int tdgs_adc_stats(void* stream, tdgs_adc_buffers* adc, const tdgs_gradients* grads,
                    const int32_t* fgidx_to_gidx, int32_t nb_fgaussians, int32_t width,
                    int32_t height);
+
+/* tdgs_adc_stats for a render with TDGS_FLAG_DEVICE_COUNTS: fgidx_to_gidx from the render
+ * buffers and the filtered count from the frame counts on the device (nothing for a frame
+ * whose keys did not fit). */
+int tdgs_adc_stats_frame(void* stream, tdgs_adc_buffers* adc, const tdgs_gradients* grads,
+                         const tdgs_render_buffers* buf, int32_t width, int32_t height);
 
 /* Masks, counts, scan and ngidx_to_gidx (training.jl:325-397). Thresholds are in feature
  * space: prune if logit < prune_logit or (use_max_scale and max log-scale > log_max_scale);

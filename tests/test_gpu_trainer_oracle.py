@@ -1,7 +1,8 @@
 """training_step! on the GPU against the same steps driven through the CPU oracle.
 
 The Trainer (training.jl:173-244) runs eight iterations across a density-control step (the
-ADC at iteration 600) with the optimiser fused into the backward projection and without.
+ADC at iteration 600) with the optimiser fused into the backward projection and without (fused,
+the steps without density control render with device-side counts: no host synchronisation).
 Each iteration is replayed on the CPU with the oracle's functions in the reference's order:
 render! (checked bit for bit against the GPU's image), the backward projection from the GPU's
 2D gradients of that iteration, the ADC statistics, at iteration 600 the masks, compaction
@@ -47,14 +48,24 @@ def test_trainer_steps_match_oracle_driven_steps(gpu, oracle, monkeypatch, fuse)
     captured = []
     orig_b2, orig_b = training.backward_render_tiles_, training.backward_
 
+    def nbf_of(buf):
+        if buf.nb_fgaussians >= 0:
+            return buf.nb_fgaussians
+        # a device-count step: read the count (a synchronisation the trainer does not make)
+        # and leave the buffers as the step left them, so that the rest of the step still
+        # takes the count from the device
+        n = buf.frame_counts()[0]
+        buf.nb_fgaussians = buf.nb_keys = -1
+        return n
+
     def cap_b2(fg, grad, out, cam, t, o, buf):
         r = orig_b2(fg, grad, out, cam, t, o, buf)
-        captured.append(fg.grads2d_matrix(buf.nb_fgaussians).cpu().numpy().copy())
+        captured.append(fg.grads2d_matrix(nbf_of(buf)).cpu().numpy().copy())
         return r
 
     def cap_b(fg, grad, out, g, cam, t, o, buf):
         r = orig_b(fg, grad, out, g, cam, t, o, buf)
-        captured.append(fg.grads2d_matrix(buf.nb_fgaussians).cpu().numpy().copy())
+        captured.append(fg.grads2d_matrix(nbf_of(buf)).cpu().numpy().copy())
         return r
 
     monkeypatch.setattr(training, "backward_render_tiles_", cap_b2)
@@ -72,6 +83,9 @@ def test_trainer_steps_match_oracle_driven_steps(gpu, oracle, monkeypatch, fuse)
         torch.cuda.synchronize()
         it = tr.iteration_nb
         cam = tr.last_camera
+        # fused steps without density control render with device-side counts
+        is_adc = it % to.adc_interval == 0 and to.adc_start_iteration_nb <= it <= to.adc_final_iteration_nb
+        assert (tr.render_buffers.nb_fgaussians == -1) == (fuse and not is_adc)
         assert len(captured) == step + 1
         g2 = captured[-1]
         fwd = oracle.render(g, cam, tiling, ropts)

@@ -18,6 +18,10 @@ TDGS_CLIP_CLAMP = 0
 TDGS_CLIP_FILTER = 1
 TDGS_FLAG_EXACT_SH_JACOBIAN = 0x1
 TDGS_FLAG_EXACT_AA_GRADIENT = 0x2
+TDGS_FLAG_DEVICE_COUNTS = 0x4
+TDGS_FRAME_OK = 0
+TDGS_FRAME_KEY_CAPACITY = 1
+TDGS_FRAME_KEY_RANGE = 2
 TDGS_IMAGE_RGB = 0
 TDGS_IMAGE_TRANSMITTANCE = 1
 TDGS_IMAGE_DEPTH = 2

@@ -240,7 +240,9 @@ class RenderBuffers:
         """The sorted 64-bit keys of the last render (int64, key_capacity entries, the first
         nb_keys valid). The render sorts 16-bit tile ids when the tiling has at most 65535 tiles;
         the keys are then assembled here on first access (on the current stream)."""
-        if self._keys_pending:
+        if self._keys_pending and self.nb_keys < 0:
+            self.frame_counts()
+        if self._keys_pending and self.nb_keys > 0:
             check(lib().tdgs_render_sorted_keys(stream_ptr(self.device.index), C.byref(self._keys_pending),
                                                 C.byref(self.struct()), self.nb_keys))
             self._keys_pending = None
@@ -257,6 +259,20 @@ class RenderBuffers:
         self.sorted_values = torch.empty(kc, dtype=torch.int32, device=d)
         tb = lib().tdgs_render_temp_bytes(self.capacity, kc, C.byref(self.tiling.to_c()))
         self.temp = torch.empty(int(tb), dtype=torch.uint8, device=d)
+
+    def frame_counts(self):
+        """The counts of the last render with device_counts=True (tdgs_render_counts;
+        synchronises): sets nb_fgaussians and nb_keys, returns (nb_fgaussians, nb_keys,
+        non-empty count, frame status)."""
+        c = (C.c_int64 * 4)()
+        check(lib().tdgs_render_counts(stream_ptr(self.device.index), C.byref(self.struct()), c))
+        self.nb_fgaussians, self.nb_keys = int(c[0]), int(c[1])
+        return int(c[0]), int(c[1]), int(c[2]), int(c[3])
+
+    def frame_counts_view(self):
+        """The device-side frame counts (int64 x 4: nb_fgaussians, nb_keys, non-empty count,
+        status) of a device-count render, as a view of temp (for an asynchronous copy)."""
+        return self.temp[:32].view(torch.int64)
 
     def ensure_capacity(self, n):
         if n > self.capacity:
@@ -287,13 +303,27 @@ class RenderBuffers:
 # ------------------------------------------------------------------------------------
 
 def render_(outputs: RenderOutputs, gaussians, camera: PinholeCamera, tiling: Tiling,
-            options: RenderOptions, buffers: RenderBuffers):
-    """render! (src/forward_core.jl:196-314). Grows the key buffers when needed."""
+            options: RenderOptions, buffers: RenderBuffers, device_counts: bool = False):
+    """render! (src/forward_core.jl:196-314). Grows the key buffers when needed.
+
+    device_counts=True renders without synchronising with the host (TDGS_FLAG_DEVICE_COUNTS):
+    buffers.nb_fgaussians and nb_keys become -1 and the counts stay on the device
+    (buffers.frame_counts() reads them); the key arrays are not grown, and a frame whose keys
+    do not fit renders as render_void! with the status TDGS_FRAME_KEY_CAPACITY."""
     dev = gaussians.device.index
     buffers.ensure_capacity(len(gaussians))
     g = gaussians.struct()
     cam, t, o = camera.to_c(), tiling.to_c(), options.to_c()
     out = outputs.struct()
+    if device_counts:
+        o.flags |= abi.TDGS_FLAG_DEVICE_COUNTS
+        nbf, m = C.c_int32(0), C.c_int64(0)
+        check(lib().tdgs_render(context(dev), stream_ptr(dev), C.byref(g), C.byref(cam), C.byref(t), C.byref(o),
+                                C.byref(buffers.struct()), C.byref(out), C.byref(nbf), C.byref(m)))
+        buffers.nb_fgaussians = -1
+        buffers.nb_keys = -1
+        buffers._keys_pending = t
+        return outputs
     nbf = C.c_int32(0)
     m = C.c_int64(0)
     for _ in range(2):
@@ -488,9 +518,10 @@ def backward_render_tiles_(fgradients: FilteredGaussiansGradientsVector, rgb_ima
     dev = rgb_image_grad.device.index
     assert rgb_image_grad.dtype == torch.float32 and rgb_image_grad.is_contiguous()
     nbf = buffers.nb_fgaussians
-    if nbf <= 0:
+    if nbf == 0:
         return fgradients
-    fgradients.zero_2d_(nbf)
+    # (a device-count render: the count is not known here, zero the whole capacity)
+    fgradients.zero_2d_(nbf if nbf > 0 else None)
     check(lib().tdgs_backward_render_tiles(stream_ptr(dev), C.byref(fgradients.struct()),
                                            C.c_void_p(dptr(rgb_image_grad)), C.byref(outputs.struct()),
                                            C.byref(camera.to_c()), C.byref(tiling.to_c()), C.byref(options.to_c()),

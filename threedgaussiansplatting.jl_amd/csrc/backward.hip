@@ -86,8 +86,8 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 
 // backward_pair (backward_core.jl:249-272) in the form the wavefront sums. The partial colour
 // psi enters only through g . psi, kept as one scalar gpsi; the terms linear in the entry's M
-// or carrying a constant factor are summed over the pixels without it, and the flush applies
-// M and the factors once per (tile, Gaussian):
+// or carrying a constant factor are summed over the pixels without it, and M and the factors
+// are applied to the wavefront's sums after the transpose-sum:
 //   dmu = M (sum out[0], sum out[1]),  dM11 = -sum out[3] / 2,  dM21 = -sum out[4],
 //   dM22 = -sum out[5] / 2.
 // out += [aa du, aa dv, G dalpha, aa du du, aa du dv, aa dv dv, T alpha g] with aa = alpha dalpha
@@ -205,6 +205,9 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
         cu[p] = (float)U - 0.5f;
         cv[p] = (float)V - 0.5f;
     }
+    const int slot = lane / 9, comp = lane - 9 * slot;
+    const int partner = comp == 0 ? lane + 1 : comp == 1 ? lane - 1 : lane;
+    const float scale = comp == 4 ? -1.0f : (comp == 3 || comp == 5) ? -0.5f : 1.0f;
     // entries past the last contributor of every pixel of the wavefront / tile are skipped
     const int wave_last = wave_max_i32(last[0] > last[1] ? last[0] : last[1]);
     if (t == 0) s_max_last = 0;
@@ -249,6 +252,7 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
         // entries are kept per lane and summed over the wavefront in one transpose-sum, after
         // which lane l holds component l % 9 of slot l / 9 and adds it to the tile's LDS sum.
         int j = __builtin_amdgcn_readfirstlane(jtop - 1);   // wave-uniform: scalar loop control
+        // after a transpose-sum lane l holds component comp = l % 9 of slot l / 9
         const float max_alpha = a.max_alpha;
         while (j >= 0) {
             float v[64];
@@ -309,34 +313,35 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
             if (js[0] < 0) break;
             v[63] = 0.0f;
             const float sum = wave_transpose_sum64(v);
-            const int slot = lane / 9;
             int jl = -1;
 #pragma unroll
             for (int e = 0; e < kSlots; ++e) jl = slot == e ? js[e] : jl;
-            if (lane < 9 * kSlots && jl >= 0) atomicAdd(&s_acc[9 * jl + (lane - 9 * slot)], sum);
+            // The sums become gradient components: dmu = M (sum 0, sum 1) takes the partner
+            // lane's sum of the same slot, dM11, dM21, dM22 their factors.
+            const float other = __shfl(sum, partner, kWave);
+            const int je = jl < 0 ? 0 : jl;
+            const float m11 = s_rec[je].c.w;
+            const float2 m2 = *reinterpret_cast<const float2*>(&s_rec[je].d);   // M21 M22
+            const float mixed = fmaf(comp == 0 ? m11 : m2.y, sum, m2.x * other);
+            const float val = comp < 2 ? mixed : sum * scale;
+            if (lane < 9 * kSlots && jl >= 0) atomicAdd(&s_acc[9 * jl + comp], val);
         }
         __syncthreads();
         // Flush with lane i on component i % 9 of entry i / 9: one atomic instruction covers
-        // the 36-byte slots of ~7 Gaussians instead of one scattered word of 64.
-        // The sums of backward_pair_sums become the gradient components here.
+        // the 36-byte slots of ~7 Gaussians instead of one scattered word of 64. Each element
+        // is cleared for the next batch by the thread that reads it.
         for (int i = t; i < 9 * nb; i += NB) {
-            const int e = i / 9, k = i - 9 * e;
-            const int64_t f = __builtin_bit_cast(int32_t, s_rec[e].c.z);
-            float v = s_acc[i];
-            if (k < 2) {
-                const float4 rd = s_rec[e].d;
-                const float m_a = k == 0 ? s_rec[e].c.w : rd.x;   // M11 or M21
-                const float m_b = k == 0 ? rd.x : rd.y;           // M21 or M22
-                v = fmaf(m_a, s_acc[9 * e], m_b * s_acc[9 * e + 1]);
-            } else if (k == 3 || k == 5) {
-                v *= -0.5f;
-            } else if (k == 4) {
-                v = -v;
+            int ii = i;
+            asm volatile("" : "+v"(ii));   // (keeps the element index 32-bit: no 64-bit induction variables)
+            const float v = s_acc[ii];
+            if (v != 0.0f) {
+                s_acc[ii] = 0.0f;
+                const int e = ii / 9, k = ii - 9 * e;
+                const int32_t f = __builtin_bit_cast(int32_t, s_rec[e].c.z);
+                unsafeAtomicAdd(SEP ? a.g2.at_dynamic(k, f) : a.g2.base[0] + (9 * (int64_t)f + k), v);
             }
-            if (v != 0.0f) unsafeAtomicAdd(SEP ? a.g2.at_dynamic(k, f) : a.g2.base[0] + 9 * f + k, v);
         }
         __syncthreads();
-        for (int i = t; i < 9 * nb; i += NB) s_acc[i] = 0.0f;   // the next batch sums after its barrier
         hi = lo;
     }
 }
@@ -363,6 +368,7 @@ struct BackProjectArgs {
     tdgs_camera cam;
     tdgs_render_options opt;
     int64_t nbf;
+    const int64_t* frame;   // device counts (nbf is then the capacity bound): N_f, status
     const int32_t* fgidx_to_gidx;
     const float* f2d;
     const int32_t* counts;
@@ -436,8 +442,14 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
     __shared__ int32_t s_wcnt[kBpThreads / kWave];
     const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
     const int64_t f0 = (int64_t)blockIdx.x * kBpThreads;
+    int64_t nbf = a.nbf;
+    if (a.frame) {   // device counts; nothing to do for a frame whose keys did not fit
+        const int64_t fc = a.frame[0];
+        nbf = a.frame[3] != kFrameOk ? 0 : fc < nbf ? fc : nbf;
+    }
+    if (f0 >= nbf) return;   // (uniform over the workgroup)
     const int64_t fz = f0 + t;
-    const bool valid = fz < a.nbf;
+    const bool valid = fz < nbf;
     const bool active = valid && a.counts[fz] != 0;
     const int32_t gz = valid ? a.fgidx_to_gidx[fz] - 1 : -1;
     s_gi[t] = active ? gz : -1;
@@ -557,7 +569,7 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
         for (int c = 0; c < 3; ++c)
             for (int k = 0; k < hr; ++k) s_sh[t * kShRow + c * hg + k] = 0.0f;
     __syncthreads();
-    const int nrows = (int)(a.nbf - f0 < kBpThreads ? a.nbf - f0 : kBpThreads);
+    const int nrows = (int)(nbf - f0 < kBpThreads ? nbf - f0 : kBpThreads);
     if constexpr (ADAM) {
         // update! on the SH coefficients k < hr of every row (k_adam's SH items)
         const AdamInPlace& d = a.adam;
@@ -702,22 +714,41 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
     return TDGS_OK;
 }
 
+// The filtered count of a backward entry point: nb_fgaussians, or with nb_fgaussians < 0 the
+// capacity bound of a device-count render (*frame then points at its counts).
+static int filtered_count(int32_t nb_fgaussians, const tdgs_render_buffers* buf, const tdgs_gradients* grads,
+                          int64_t* nbf, const int64_t** frame) {
+    *frame = nullptr;
+    *nbf = nb_fgaussians;
+    if (nb_fgaussians >= 0) return TDGS_OK;
+    TDGS_REQUIRE(buf && buf->temp && buf->temp_bytes >= 4 * sizeof(int64_t),
+                 "nb_fgaussians < 0 reads the counts of a device-count render from its buffers");
+    TDGS_REQUIRE(!grads || grads->capacity >= buf->capacity, "gradient buffers hold %d, the render buffers %d",
+                 grads ? grads->capacity : 0, buf->capacity);
+    *nbf = buf->capacity;
+    *frame = frame_counts(buf);
+    return TDGS_OK;
+}
+
 int tdgs_backward_project(void* stream, tdgs_gradients* grads, const tdgs_gaussians* g,
                           const tdgs_camera* cam, const tdgs_render_options* opt,
                           const tdgs_render_buffers* buf, int32_t nb_fgaussians) {
     TDGS_TRY(check_gaussians(g, true));
     TDGS_TRY(check_options(opt, g->sh_degree));
-    TDGS_TRY(check_gradients(grads, nb_fgaussians, g->sh_degree));
+    int64_t nbf;
+    const int64_t* frame;
+    TDGS_TRY(filtered_count(nb_fgaussians, buf, grads, &nbf, &frame));
+    TDGS_TRY(check_gradients(grads, nbf, g->sh_degree));
     TDGS_REQUIRE(grads->sh_degree >= opt->sh_degree, "gradient SH storage below the render degree");
     TDGS_REQUIRE(cam && buf && buf->fgidx_to_gidx && buf->f2d && buf->counts, "null arguments");
-    if (nb_fgaussians <= 0) return TDGS_OK;
+    if (nbf <= 0) return TDGS_OK;
     hipStream_t s = (hipStream_t)stream;
     StageScope sc(TDGS_STAGE_BACKWARD_PROJECT, s);
     BackProjectArgs a;
-    a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nb_fgaussians;
+    a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nbf; a.frame = frame;
     a.fgidx_to_gidx = buf->fgidx_to_gidx; a.f2d = buf->f2d; a.counts = buf->counts; a.gr = *grads;
     TDGS_TRY(grads2d_view(grads, &a.g2));
-    k_backward_project<false><<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(a);
+    k_backward_project<false><<<(unsigned)ceil_div(nbf, kBpThreads), kBpThreads, 0, s>>>(a);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
@@ -727,18 +758,21 @@ int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_g
                                const tdgs_render_buffers* buf, int32_t nb_fgaussians) {
     TDGS_TRY(check_gaussians(g, true));
     TDGS_TRY(check_options(opt, g->sh_degree));
-    TDGS_REQUIRE(grads && grads->capacity >= nb_fgaussians && grads->sh_degree >= 0 && grads->sh_degree <= 3,
+    int64_t nbf;
+    const int64_t* frame;
+    TDGS_TRY(filtered_count(nb_fgaussians, buf, grads, &nbf, &frame));
+    TDGS_REQUIRE(grads && grads->capacity >= nbf && grads->sh_degree >= 0 && grads->sh_degree <= 3,
                  "bad gradient buffers");
     TDGS_REQUIRE(grads->sh_degree >= opt->sh_degree, "gradient SH storage below the render degree");
     TDGS_REQUIRE(st && cam && buf && buf->fgidx_to_gidx && buf->f2d && buf->counts, "null arguments");
-    if (nb_fgaussians > 0) {
+    if (nbf > 0) {
         TDGS_REQUIRE(st->means_moments && st->opacity_moments && st->scaling_moments && st->rotation_moments &&
                          st->sh_moments,
                      "null arrays");
         hipStream_t s = (hipStream_t)stream;
         StageScope sc(TDGS_STAGE_BACKWARD_PROJECT, s);
         BackProjectArgs a;
-        a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nb_fgaussians;
+        a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nbf; a.frame = frame;
         a.fgidx_to_gidx = buf->fgidx_to_gidx; a.f2d = buf->f2d; a.counts = buf->counts; a.gr = *grads;
         TDGS_TRY(grads2d_view(grads, &a.g2));
         AdamInPlace& d = a.adam;
@@ -752,7 +786,7 @@ int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_g
         d.bc1 = (float)(1.0 - pow((double)st->beta1, tt));
         d.bc2 = (float)(1.0 - pow((double)st->beta2, tt));
         d.eps = st->epsilon;
-        k_backward_project<true><<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(a);
+        k_backward_project<true><<<(unsigned)ceil_div(nbf, kBpThreads), kBpThreads, 0, s>>>(a);
         TDGS_LAUNCHED();
     }
     st->update_count += 1;
@@ -762,10 +796,13 @@ int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_g
 int tdgs_backward(void* stream, tdgs_gradients* grads, const float* rgb_grad, const tdgs_render_outputs* out,
                   const tdgs_gaussians* g, const tdgs_camera* cam, const tdgs_tiling* tiling,
                   const tdgs_render_options* opt, const tdgs_render_buffers* buf, int32_t nb_fgaussians) {
-    TDGS_TRY(check_gradients(grads, nb_fgaussians, g ? g->sh_degree : 0));
-    if (nb_fgaussians <= 0) return TDGS_OK;
+    int64_t nbf;
+    const int64_t* frame;
+    TDGS_TRY(filtered_count(nb_fgaussians, buf, grads, &nbf, &frame));
+    TDGS_TRY(check_gradients(grads, nbf, g ? g->sh_degree : 0));
+    if (nbf <= 0) return TDGS_OK;
     hipStream_t s = (hipStream_t)stream;
-    TDGS_TRY(zero_grads2d(s, grads, nb_fgaussians));
+    TDGS_TRY(zero_grads2d(s, grads, nbf));   // (with device counts: the whole capacity)
     TDGS_TRY(tdgs_backward_render_tiles(stream, grads, rgb_grad, out, cam, tiling, opt, buf));
     return tdgs_backward_project(stream, grads, g, cam, opt, buf, nb_fgaussians);
 }

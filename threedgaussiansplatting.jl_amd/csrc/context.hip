@@ -90,15 +90,20 @@ int tdgs_ctx_create(int device, tdgs_ctx** ctx_out) {
     TDGS_HIP(hipSetDevice(device));
     tdgs_ctx* c = new tdgs_ctx();
     c->device = device;
-    hipError_t e = hipMalloc((void**)&c->d_counters, sizeof(int64_t) * kCounters);
+    hipError_t e = hipMalloc((void**)&c->d_counters, sizeof(int64_t) * (kCounters + kMonitor));
     if (e == hipSuccess) e = hipHostMalloc((void**)&c->h_counters, sizeof(int64_t) * kCounters);
-    if (e == hipSuccess) e = hipMemset(c->d_counters, 0, sizeof(int64_t) * kCounters);
+    if (e == hipSuccess) e = hipMemset(c->d_counters, 0, sizeof(int64_t) * (kCounters + kMonitor));
+    if (e == hipSuccess)
+        e = hipHostMalloc((void**)&c->h_monitor, sizeof(int64_t) * kMonitor, hipHostMallocCoherent | hipHostMallocMapped);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void**)&c->h_monitor_dev, c->h_monitor, 0);
     if (e != hipSuccess) {
         if (c->d_counters) (void)hipFree(c->d_counters);
         if (c->h_counters) (void)hipHostFree(c->h_counters);
+        if (c->h_monitor) (void)hipHostFree(c->h_monitor);
         delete c;
         return hip_fail(e, "tdgs_ctx_create", __FILE__, __LINE__);
     }
+    for (int k = 0; k < kMonitor; ++k) c->h_monitor[k] = 0;
     *ctx_out = c;
     return TDGS_OK;
 }
@@ -108,6 +113,7 @@ int tdgs_ctx_destroy(tdgs_ctx* ctx) {
     TDGS_HIP(hipDeviceSynchronize());
     TDGS_HIP(hipFree(ctx->d_counters));
     TDGS_HIP(hipHostFree(ctx->h_counters));
+    TDGS_HIP(hipHostFree(ctx->h_monitor));
     delete ctx;
     return TDGS_OK;
 }
@@ -246,6 +252,12 @@ int tdgs_host_free(void* ptr) {
 int tdgs_ctx_check(tdgs_ctx* ctx, void* stream) {
     TDGS_REQUIRE(ctx, "null ctx");
     return read_counters(ctx, (hipStream_t)stream);
+}
+
+int tdgs_ctx_frame_monitor(tdgs_ctx* ctx, const int64_t** monitor_out) {
+    TDGS_REQUIRE(ctx && monitor_out, "null arguments");
+    *monitor_out = ctx->h_monitor;
+    return TDGS_OK;
 }
 
 }  // extern "C"

@@ -577,11 +577,27 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
                                                                  const int32_t* __restrict__ blk_first,
                                                                  const int32_t* __restrict__ ranges, int32_t ntx,
                                                                  int nbits0, uint32_t* __restrict__ counts0,
-                                                                 int64_t count_tiles) {
+                                                                 int64_t count_tiles, int64_t* dc, int64_t key_cap) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
     __shared__ uint32_t s_h[kRsBins];
     const int t = threadIdx.x;
+    if (dc) {
+        // device counts: the grid covers key_cap keys; the key passes use M, or none when M does
+        // not fit (the status says why)
+        nb = dc[4];
+        m = dc[1];
+        const int64_t st = m > key_cap ? kFrameKeyCapacity : m >= (int64_t)INT32_MAX ? kFrameKeyRange : kFrameOk;
+        if (st != kFrameOk) m = 0;
+        if (blockIdx.x == 0 && t == 0) {
+            dc[kCntKeysUsed] = m;
+            dc[kCntStatus] = st;
+        }
+        if ((int64_t)blockIdx.x * kEmitTile >= m) {   // past the keys: an empty column of counts
+            if (t < kRsBins) counts0[(int64_t)t * count_tiles + blockIdx.x] = 0;
+            return;
+        }
+    }
     if (t < kRsBins) s_h[t] = 0;
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
     emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf,
@@ -607,11 +623,16 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
     const int32_t* __restrict__ blk_first, const int32_t* __restrict__ ranges, int32_t ntx, int nbits0,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, int64_t count_tiles,
-    uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err) {
+    uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err, const int64_t* dc) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
+    if (dc) {   // device counts (k_emit_count set the key count used)
+        nb = dc[4];
+        m = dc[kCntKeysUsed];
+        if (d0 >= m) return;
+    }
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
     emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf,
                                                     s_range, tile, val);
@@ -670,8 +691,13 @@ __device__ __forceinline__ int32_t tile_of(const uint16_t* st, int64_t i) { retu
 // [1, nb_tiles] so that a malformed key cannot write out of bounds.
 template <class K>
 __global__ __launch_bounds__(256) void k_tile_ranges(int64_t m, const K* __restrict__ sk, int32_t nb_tiles,
-                                                     int32_t* __restrict__ te) {
+                                                     int32_t* __restrict__ te, const int64_t* dm = nullptr) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (dm) {   // device key count (the grid covers the key capacity); no keys: empty tiles
+        m = *dm;
+        if (m == 0)
+            for (int64_t k = i; k < nb_tiles; k += (int64_t)gridDim.x * blockDim.x) te[k] = 0;
+    }
     if (i >= m) return;
     const int32_t cur = tile_of(sk, i);
     if (i == 0) {
@@ -691,8 +717,13 @@ __global__ __launch_bounds__(256) void k_tile_ranges(int64_t m, const K* __restr
 // The same on 16-bit tile ids, eight sorted entries per thread (one 16-byte load, plus the id
 // that follows them).
 __global__ __launch_bounds__(256) void k_tile_ranges16(int64_t m, const uint16_t* __restrict__ st, int32_t nb_tiles,
-                                                       int32_t* __restrict__ te) {
+                                                       int32_t* __restrict__ te, const int64_t* dm = nullptr) {
     const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (dm) {   // device key count (the grid covers the key capacity); no keys: empty tiles
+        m = *dm;
+        if (m == 0)
+            for (int64_t k = i0 / 8; k < nb_tiles; k += (int64_t)gridDim.x * blockDim.x) te[k] = 0;
+    }
     if (i0 >= m) return;
     int32_t id[9];
     if (i0 + 8 < m) {
@@ -842,6 +873,12 @@ struct BlendArgs {
     float* depth;
     int32_t* last;
     unsigned long long* evaluations;  // COUNT variant: [evaluations, live, contributing]
+    // device-count render: the context's counters (key count used, N_f), and the frame counts
+    // of the render buffers, which workgroup (0, 0) fills in
+    const int64_t* dcount;
+    int64_t* frame;
+    int64_t* mon;        // frame monitor state (device) and its host copy
+    int64_t* mon_host;
 };
 
 // The blending steps of one batch of nb staged records, written out instruction by instruction.
@@ -1035,9 +1072,29 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     const float cu = (float)u_in - 0.5f, cv = (float)v_in - 0.5f;
     const float uu = cu * cu, uv = cu * cv, vv = cv * cv;
     const float u0 = (float)((tx - 1) * a.TW), v0 = (float)((ty - 1) * a.TH);
+    int64_t m = a.m;
+    bool nothing = false;   // render_void!'s outputs (a device-count render with no keys)
+    if (!COUNT && a.dcount) {
+        m = a.dcount[kCntKeysUsed];
+        nothing = m == 0 || a.dcount[0] == 0;
+        if (tile == 1 && t == 0) {
+            const int64_t keys = a.dcount[1], status = a.dcount[kCntStatus];
+            a.frame[0] = a.dcount[0];
+            a.frame[1] = keys;
+            a.frame[2] = a.dcount[4];
+            a.frame[3] = status;
+            const int64_t mon[kMonitor] = {a.mon[0] + 1, a.mon[1] > keys ? a.mon[1] : keys,
+                                           a.mon[2] + (status != kFrameOk ? 1 : 0), keys};
+#pragma unroll
+            for (int k = 0; k < kMonitor; ++k) {
+                a.mon[k] = mon[k];
+                __hip_atomic_store(a.mon_host + k, mon[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+    }
     int64_t end = a.tiles_end[tile - 1];
     int64_t beg = tile == 1 ? 0 : a.tiles_end[tile - 2];
-    if (end > a.m) end = a.m;
+    if (end > m) end = m;
     if (beg < 0) beg = 0;
     if (beg > end) beg = end;
 
@@ -1137,7 +1194,7 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
         a.rgb[3 * px + 2] = fmaf(T, a.bg2, C2);
     }
     if (a.T) a.T[px] = T;
-    if (DEPTH && a.depth) a.depth[px] = D;
+    if (DEPTH && a.depth) a.depth[px] = nothing ? kInf : D;
     if (a.last) a.last[px] = last;
 }
 
@@ -1169,7 +1226,9 @@ static int launch_render_void(hipStream_t s, const tdgs_camera* cam, const tdgs_
 static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs_tiling* t,
                                const tdgs_render_options* o, int64_t m, const int32_t* tiles_end,
                                const int32_t* sorted_f, const float* f2d, const float* depths,
-                               const tdgs_render_outputs* out, unsigned long long* evaluations = nullptr) {
+                               const tdgs_render_outputs* out, unsigned long long* evaluations = nullptr,
+                               const int64_t* dcount = nullptr, int64_t* frame = nullptr,
+                               int64_t* mon = nullptr, int64_t* mon_host = nullptr) {
     BlendArgs a;
     a.W = cam->width; a.H = cam->height; a.TW = t->tile_width; a.TH = t->tile_height;
     a.ntx = t->nb_tiles_x;
@@ -1180,6 +1239,10 @@ static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs
     a.m = m; a.tiles_end = tiles_end; a.sorted_f = sorted_f; a.f2d = f2d; a.depths = depths;
     a.rgb = out->rgb; a.T = out->T; a.depth = out->depth; a.last = out->last;
     a.evaluations = evaluations;
+    a.dcount = dcount;
+    a.frame = frame;
+    a.mon = mon;
+    a.mon_host = mon_host;
     const int nt = t->tile_width * t->tile_height;
     const dim3 grid(t->nb_tiles_x, t->nb_tiles_y);
     const size_t lds = (size_t)(nt + 1) * sizeof(BlendRec);   // + the record blend_batch prefetches past a batch
@@ -1335,6 +1398,68 @@ static int launch_keep_and_project(hipStream_t s, const tdgs_gaussians* g, const
 
 using namespace tdgs;
 
+// Steps 6-9 of tdgs_render with TDGS_FLAG_DEVICE_COUNTS: no host synchronisation. The launches
+// are sized by the key capacity and every kernel reads N_f, the non-empty count and M from the
+// context's counters; k_emit_count records the key count the passes use (0 when M does not
+// fit the key arrays, with the frame status saying so), and the blend copies the counts to the
+// frame counts of the buffers. At most 65535 tiles (16-bit tile ids); the tile ranges come
+// from the sorted ids.
+static int render_keys_device_counts(tdgs_ctx* ctx, hipStream_t s, const tdgs_camera* cam,
+                                     const tdgs_tiling* tiling, const tdgs_render_options* opt,
+                                     tdgs_render_buffers* buf, const tdgs_render_outputs* out,
+                                     const RenderScratch& r, int64_t n) {
+    int64_t* dc = ctx->d_counters;
+    uint32_t* d_err = ctx_error_word(ctx);
+    const int64_t kc = buf->key_capacity;
+    const int eb = end_bit_of(tiling);
+    const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
+    const int te_bit = eb - 32;
+    const int passes = radix_passes(0, te_bit);
+    const int nbits0 = radix_digit_bits(0, te_bit);
+    uint16_t* t16_out = reinterpret_cast<uint16_t*>(buf->keys);
+    uint16_t* t16_alt = t16_out + kc;
+    const unsigned egrid = (unsigned)ceil_div(kc, kEmitTile);
+    const int64_t count_tiles = radix_tiles<uint16_t>(kc);
+    uint32_t* table = radix_count_table(r.rtemp);
+    uint32_t* totals = radix_totals(r.rtemp, kc);
+    const bool one_pass = passes == 1;
+    (void)n;
+    {
+        StageScope sc(TDGS_STAGE_EMIT, s);
+        k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(0, 0, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges,
+                                                        tiling->nb_tiles_x, nbits0, table, count_tiles, dc, kc);
+        TDGS_LAUNCHED();
+    }
+    {
+        StageScope sc(TDGS_STAGE_TILE_SORT, s);
+        k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals);
+        TDGS_LAUNCHED();
+        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(0, 0, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges,
+                                                          tiling->nb_tiles_x, nbits0, table, totals, count_tiles,
+                                                          one_pass ? t16_out : t16_alt,
+                                                          one_pass ? buf->sorted_values : buf->values, d_err, dc);
+        TDGS_LAUNCHED();
+        if (!one_pass)
+            TDGS_TRY(radix_sort_pairs<uint16_t>(t16_alt, t16_out, buf->values, buf->sorted_values, t16_alt,
+                                                buf->values, kc, nbits0, te_bit, r.rtemp, r.rbytes, s, nullptr, d_err,
+                                                nullptr, dc + kCntKeysUsed));
+    }
+    {
+        StageScope sc(TDGS_STAGE_TILE_RANGES, s);
+        const int64_t threads = ceil_div(kc, 8) > nb_tiles ? ceil_div(kc, 8) : nb_tiles;
+        if (((uintptr_t)t16_out & 15) == 0)
+            k_tile_ranges16<<<(unsigned)ceil_div(threads, 256), 256, 0, s>>>(kc, t16_out, nb_tiles, buf->tiles_end,
+                                                                              dc + kCntKeysUsed);
+        else
+            k_tile_ranges<uint16_t><<<(unsigned)ceil_div(kc > nb_tiles ? kc : nb_tiles, 256), 256, 0, s>>>(
+                kc, t16_out, nb_tiles, buf->tiles_end, dc + kCntKeysUsed);
+        TDGS_LAUNCHED();
+    }
+    StageScope sc(TDGS_STAGE_BLEND, s);
+    return launch_render_tiles(s, cam, tiling, opt, kc, buf->tiles_end, buf->sorted_values, buf->f2d, buf->depths,
+                               out, nullptr, dc, frame_counts(buf), ctx->d_counters + kCounters, ctx->h_monitor_dev);
+}
+
 extern "C" {
 
 int tdgs_project(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
@@ -1460,6 +1585,14 @@ int tdgs_tile_ranges(void* stream, int64_t nb_keys, const int64_t* sorted_keys, 
     return TDGS_OK;
 }
 
+int tdgs_render_counts(void* stream, const tdgs_render_buffers* buf, int64_t* counts_out) {
+    TDGS_REQUIRE(buf && buf->temp && buf->temp_bytes >= 4 * sizeof(int64_t) && counts_out, "null arguments");
+    hipStream_t s = (hipStream_t)stream;
+    TDGS_HIP(hipMemcpyAsync(counts_out, frame_counts(buf), 4 * sizeof(int64_t), hipMemcpyDeviceToHost, s));
+    TDGS_HIP(hipStreamSynchronize(s));
+    return TDGS_OK;
+}
+
 int tdgs_render_sorted_keys(void* stream, const tdgs_tiling* tiling, const tdgs_render_buffers* buf,
                             int64_t nb_keys) {
     TDGS_REQUIRE(tiling && tiling->nb_tiles_x > 0 && tiling->nb_tiles_y > 0, "bad tiling");
@@ -1510,9 +1643,22 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     TDGS_REQUIRE(ctx && buf && out && nb_fgaussians_out && nb_keys_out, "null arguments");
     TDGS_TRY(check_render_args(g, cam, tiling, opt, buf));
     hipStream_t s = (hipStream_t)stream;
-    *nb_fgaussians_out = 0;
-    *nb_keys_out = 0;
+    const bool device_counts = (opt->flags & TDGS_FLAG_DEVICE_COUNTS) != 0;
+    *nb_fgaussians_out = device_counts ? -1 : 0;
+    *nb_keys_out = device_counts ? -1 : 0;
     const int64_t n = g->n;
+    if (device_counts) {
+        TDGS_REQUIRE((int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y <= 65535,
+                     "device counts need at most 65535 tiles (the tiling has %lld)",
+                     (long long)tiling->nb_tiles_x * tiling->nb_tiles_y);
+        TDGS_REQUIRE(buf->key_capacity >= 1 && buf->keys && buf->values && buf->sorted_values,
+                     "device counts need allocated key arrays");
+        if (n == 0) {
+            // the frame counts of an empty frame
+            static const int64_t zeros[4] = {0, 0, 0, 0};
+            TDGS_HIP(hipMemcpyAsync(frame_counts(buf), zeros, sizeof(zeros), hipMemcpyHostToDevice, s));
+        }
+    }
     if (n == 0) return launch_render_void(s, cam, opt, out);
     const RenderScratch r = carve_render_scratch(buf, tiling);
     uint32_t* dkey = r.dkey;
@@ -1551,6 +1697,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
                              SortedCounts{sorted_f, buf->counts, d_nb}, WriteScanAndBlocks{cs, blk_first, nblk}, n, stemp,
                              sbytes, d_m, s, d_nb));
     }
+    if (opt->flags & TDGS_FLAG_DEVICE_COUNTS)
+        return render_keys_device_counts(ctx, s, cam, tiling, opt, buf, out, r, n);
     TDGS_TRY(read_counters(ctx, s));
     const int64_t nbf = ctx->h_counters[0];
     const int64_t m = ctx->h_counters[1];
@@ -1590,7 +1738,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         {
             StageScope sc(TDGS_STAGE_EMIT, s);
             k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->tile_ranges,
-                                                            tiling->nb_tiles_x, nbits0, table, count_tiles);
+                                                            tiling->nb_tiles_x, nbits0, table, count_tiles, nullptr, 0);
             TDGS_LAUNCHED();
         }
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
@@ -1599,7 +1747,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->tile_ranges,
                                                           tiling->nb_tiles_x, nbits0, table, totals, count_tiles,
                                                           one_pass ? t16_out : t16_alt,
-                                                          one_pass ? buf->sorted_values : buf->values, d_err);
+                                                          one_pass ? buf->sorted_values : buf->values, d_err,
+                                                          nullptr);
         TDGS_LAUNCHED();
         if (!one_pass)
             TDGS_TRY(radix_sort_pairs<uint16_t>(t16_alt, t16_out, buf->values, buf->sorted_values, t16_alt,

@@ -7,19 +7,35 @@
 
 struct tdgs_ctx {
     int device;
-    int64_t* d_counters;   // device scratch for counts reported to the host
+    int64_t* d_counters;   // device scratch for counts reported to the host (+ the monitor state)
     int64_t* h_counters;   // pinned host mirror of d_counters
+    int64_t* h_monitor;    // pinned, coherent host memory the device writes the frame monitor to
+    int64_t* h_monitor_dev;   // its device address
 };
 
 namespace tdgs {
 
 constexpr int kCounters = 8;
+// Frame monitor of device-count renders: [frames, largest M, frames whose keys did not fit,
+// last M], kept on the device after the counters (d_counters + kCounters) and copied to the
+// host (h_monitor) by every such frame.
+constexpr int kMonitor = 4;
 // Slot of ctx->d_counters holding the sticky device error flags (low 32 bits): kernels OR
 // kErr* bits into it; every host synchronisation through read_counters reports and clears it.
 constexpr int kErrSlot = 7;
 constexpr uint32_t kErrSortCounts = 1u;   // radix-sort counts disagreed with the keys
 
 inline uint32_t* ctx_error_word(tdgs_ctx* ctx) { return reinterpret_cast<uint32_t*>(ctx->d_counters + kErrSlot); }
+
+// Other slots of ctx->d_counters: 0 filtered count N_f, 1 key count M, 2 ADC count, 4 count of
+// non-empty Gaussians; in a render with TDGS_FLAG_DEVICE_COUNTS, 5 the key count the key
+// passes use (M, or 0 when M does not fit the key arrays) and 6 the frame status.
+constexpr int kCntKeysUsed = 5, kCntStatus = 6;
+// Frame status: the keys fit, M > key_capacity, M >= 2^31.
+constexpr int64_t kFrameOk = 0, kFrameKeyCapacity = 1, kFrameKeyRange = 2;
+// A device-count render leaves [N_f, M, non-empty count, status] in the first four int64 of
+// the render buffers' temp, for the entry points that read the counts on the device.
+inline int64_t* frame_counts(const tdgs_render_buffers* buf) { return reinterpret_cast<int64_t*>(buf->temp); }
 
 // Copy the device counters to the host and wait for the stream; returns TDGS_ERR_DEVICE (and
 // clears the flags) when a kernel has raised an error flag since the last check.

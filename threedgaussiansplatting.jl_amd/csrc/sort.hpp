@@ -105,14 +105,15 @@ __device__ __forceinline__ void tile_digit_histogram(const K* __restrict__ keys,
     __syncthreads();
 }
 
-// d_n, when not null, replaces n by a count computed on the device (the grid still covers n);
+// d_n, when not null, replaces n by a count computed on the device, min(*d_n, n) (the grid
+// still covers n);
 // drop_max leaves keys equal to the all-ones key out of the count (and of the sort).
 template <class K>
 __global__ __launch_bounds__(kRsThreads) void k_rs_count(const K* __restrict__ keys, int64_t n, int shift,
                                                          int nbits, uint32_t* __restrict__ counts, int64_t tiles,
                                                          const int64_t* d_n, int drop_max) {
     __shared__ uint32_t s_h[kRsBins];
-    tile_digit_histogram(keys, d_n ? *d_n : n, blockIdx.x, shift, nbits, s_h, drop_max != 0);
+    tile_digit_histogram(keys, d_n ? (*d_n < n ? *d_n : n) : n, blockIdx.x, shift, nbits, s_h, drop_max != 0);
     if (threadIdx.x < kRsBins) counts[(int64_t)threadIdx.x * tiles + blockIdx.x] = s_h[threadIdx.x];
 }
 
@@ -288,7 +289,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     __shared__ uint32_t s_raw[rs_stage_words<K>()];
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const int64_t tile = blockIdx.x;
-    if (d_n) n = *d_n;
+    if (d_n && *d_n < n) n = *d_n;
     const int32_t base = (int32_t)(tile * kRsTile);
     const int32_t wbase = base + w * (kRsItems * kWave) + lane;
     const int32_t nn = (int32_t)n;
@@ -352,11 +353,14 @@ inline size_t radix_temp_bytes(int64_t n) {
 // kept pairs (their count read on the device, so the host needs no synchronisation), and the
 // count of kept pairs is written to *kept_out. The output then holds the kept pairs, stably
 // sorted, in its first *kept_out entries.
+//
+// d_count (device word, may be null; not with kept_out) holds the number of pairs to sort,
+// min(*d_count, n): n only sizes the launches, so the host needs no synchronisation.
 template <class K>
 int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K* alt_k,
                      int32_t* alt_v, int64_t n, int begin_bit, int end_bit, void* temp,
                      size_t temp_bytes, hipStream_t stream, uint32_t* first_counts = nullptr,
-                     uint32_t* err = nullptr, int64_t* kept_out = nullptr) {
+                     uint32_t* err = nullptr, int64_t* kept_out = nullptr, const int64_t* d_count = nullptr) {
     const int passes = radix_passes(begin_bit, end_bit);
     const int width = radix_digit_bits(begin_bit, end_bit);
     if (n <= 0) return TDGS_OK;
@@ -365,8 +369,8 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
         return TDGS_ERR_INVALID;
     }
     if (passes == 0) {
-        if (kept_out) {
-            set_error("radix sort: dropping keys needs at least one pass");
+        if (kept_out || d_count) {
+            set_error("radix sort: dropping keys or a device count needs at least one pass");
             return TDGS_ERR_INVALID;
         }
         if (kout != kin) TDGS_HIP(hipMemcpyAsync(kout, kin, n * sizeof(K), hipMemcpyDeviceToDevice, stream));
@@ -390,7 +394,7 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
         K* dk = to_out ? kout : alt_k;
         int32_t* dv = to_out ? vout : alt_v;
         uint32_t* table = counts;
-        const int64_t* d_n = (kept_out && p > 0) ? kept_out : nullptr;
+        const int64_t* d_n = kept_out ? (p > 0 ? kept_out : nullptr) : d_count;
         const int drop = (kept_out && p == 0) ? 1 : 0;
         if (p == 0 && first_counts) {
             if (kept_out) {

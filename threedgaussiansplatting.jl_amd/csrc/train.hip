@@ -133,9 +133,13 @@ __global__ __launch_bounds__(256) void k_adam(AdamArgs a) {
 // so the norm is formed in double precision.)
 // mean2d: the x component of the first mean gradient, the y component follows it; stride
 // floats from one filtered Gaussian to the next (9 interleaved, 2 for the reference's array).
+// frame (device counts, may be null): N_f and the frame status of a device-count render; nbf
+// is then the capacity bound.
 __global__ void k_adc_stats(const float* __restrict__ mean2d, int32_t stride, const int32_t* __restrict__ f2g,
-                            int64_t nbf, double sw, double sh, float* __restrict__ acc, int32_t* __restrict__ cnt) {
+                            int64_t nbf, double sw, double sh, float* __restrict__ acc, int32_t* __restrict__ cnt,
+                            const int64_t* frame) {
     const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (frame) nbf = frame[3] != kFrameOk ? 0 : frame[0] < nbf ? frame[0] : nbf;
     if (f >= nbf) return;
     const float gx = mean2d[stride * f], gy = mean2d[stride * f + 1];
     if (gx != 0.0f || gy != 0.0f) {
@@ -411,7 +415,27 @@ int tdgs_adc_stats(void* stream, tdgs_adc_buffers* adc, const tdgs_gradients* gr
     k_adc_stats<<<(unsigned)ceil_div(nb_fgaussians, 256), 256, 0, s>>>(g2.base[0], g2.stride[0], fgidx_to_gidx,
                                                                        nb_fgaussians,
                                                                        sw, sh, adc->accum_grad_norms,
-                                                                       adc->contribution_counts);
+                                                                       adc->contribution_counts, nullptr);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+int tdgs_adc_stats_frame(void* stream, tdgs_adc_buffers* adc, const tdgs_gradients* grads,
+                         const tdgs_render_buffers* buf, int32_t width, int32_t height) {
+    TDGS_REQUIRE(adc && grads && buf && buf->fgidx_to_gidx && buf->temp && buf->temp_bytes >= 4 * sizeof(int64_t),
+                 "null arguments");
+    TDGS_REQUIRE(adc->accum_grad_norms && adc->contribution_counts, "null arrays");
+    TDGS_REQUIRE(grads->capacity >= buf->capacity, "gradient buffers hold %d, the render buffers %d",
+                 grads->capacity, buf->capacity);
+    if (buf->capacity <= 0) return TDGS_OK;
+    Grads2D g2;
+    TDGS_TRY(grads2d_view(grads, &g2));
+    hipStream_t s = (hipStream_t)stream;
+    StageScope sc(TDGS_STAGE_ADC, s);
+    const double sw = (double)width * width / 4.0, sh = (double)height * height / 4.0;
+    k_adc_stats<<<(unsigned)ceil_div(buf->capacity, 256), 256, 0, s>>>(g2.base[0], g2.stride[0], buf->fgidx_to_gidx,
+                                                                       buf->capacity, sw, sh, adc->accum_grad_norms,
+                                                                       adc->contribution_counts, frame_counts(buf));
     TDGS_LAUNCHED();
     return TDGS_OK;
 }

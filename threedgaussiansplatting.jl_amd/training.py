@@ -188,9 +188,15 @@ class AdaptiveDensityControlBuffers:
         return s
 
 
-def adc_stats_(adc: AdaptiveDensityControlBuffers, fgradients, fgidx_to_gidx, nb_fgaussians, camera):
-    """update_adc_stats_kernel! (training.jl:472-497)."""
+def adc_stats_(adc: AdaptiveDensityControlBuffers, fgradients, fgidx_to_gidx, nb_fgaussians, camera, buffers=None):
+    """update_adc_stats_kernel! (training.jl:472-497). nb_fgaussians < 0: the counts of a
+    device-count render, read on the device from `buffers` (tdgs_adc_stats_frame)."""
     dev = adc.accum.device.index
+    if nb_fgaussians < 0:
+        check(lib().tdgs_adc_stats_frame(stream_ptr(dev), C.byref(adc.struct()), C.byref(fgradients.struct()),
+                                         C.byref(buffers.struct()), C.c_int32(camera.width),
+                                         C.c_int32(camera.height)))
+        return
     check(lib().tdgs_adc_stats(stream_ptr(dev), C.byref(adc.struct()), C.byref(fgradients.struct()),
                                C.c_void_p(dptr(fgidx_to_gidx)), C.c_int32(nb_fgaussians),
                                C.c_int32(camera.width), C.c_int32(camera.height)))
@@ -353,8 +359,20 @@ class Trainer:
 
     def __init__(self, gaussians: TrainableGaussiansVector, cameras, images, render_options: RenderOptions,
                  tiling: Tiling, training_options: TrainingOptions, optimizer: AdamOptimizer | None = None,
-                 seed: int = 0, device=0, fuse_optimizer: bool = True, record_adc: bool = False):
+                 seed: int = 0, device=0, fuse_optimizer: bool = True, record_adc: bool = False,
+                 device_counts: bool = True):
         self.device = _dev(device)
+        # device_counts: steps without density control (with the fused optimiser) render with
+        # TDGS_FLAG_DEVICE_COUNTS, so they issue no host synchronisation; the key arrays are
+        # grown ahead of need from the context's frame monitor (pinned memory the device
+        # updates), and a step whose keys did not fit is skipped by the device and counted in
+        # skipped_steps
+        self.device_counts = device_counts
+        self.skipped_steps = 0
+        self._monitor = None
+        # the monitor's frames and overflow frames before this trainer's first frame
+        self._monitor_frames0, _, self._monitor_seen, _ = self.frame_monitor() if device_counts else (0, 0, 0, 0)
+        self._largest_keys = 0   # largest key count of this trainer's frames seen on the monitor
         # record_adc: keep per density-control step the counts of pruned, cloned and split
         # Gaussians in adc_history (three reductions and a synchronisation per ADC step)
         self.record_adc = record_adc
@@ -408,7 +426,13 @@ class Trainer:
         self.images.prefetch(self.peek_next_camera())
         cam = self.cameras[k]
         self.last_camera = cam
-        render_(self.render_outputs, self.gaussians, cam, self.tiling, self.render_options, self.render_buffers)
+        dev_counts = (self.device_counts and self.fuse_optimizer and not self.adc_step_due()
+                      and self.fgradients.capacity >= self.render_buffers.capacity
+                      and self.tiling.nb_tiles <= 65535)
+        if dev_counts:
+            self._grow_keys_from_monitor()
+        render_(self.render_outputs, self.gaussians, cam, self.tiling, self.render_options, self.render_buffers,
+                device_counts=dev_counts)
         self.loss_sums.zero_()
         gt = self.images.acquire(k)
         loss_grad_(self.render_outputs.rgb, gt, self.rgb_image_grad,
@@ -432,6 +456,34 @@ class Trainer:
         if in_adc:
             self.complete_adc_step_()
         self.maybe_opacity_reset_()
+
+    def frame_monitor(self):
+        """The context's frame monitor (tdgs_ctx_frame_monitor): [frames, largest key count,
+        frames whose keys did not fit, last key count] of the device-count renders so far, read
+        without synchronisation."""
+        if self._monitor is None:
+            p = C.POINTER(C.c_int64)()
+            check(lib().tdgs_ctx_frame_monitor(context(self.device.index), C.byref(p)))
+            self._monitor = p
+        return [int(self._monitor[i]) for i in range(4)]
+
+    def _grow_keys_from_monitor(self):
+        """Grows the key arrays to 1.5x the largest key count seen once it passes 80% of the
+        capacity (at least doubling them after a frame whose keys did not fit), and counts the
+        device-count frames whose keys did not fit (their steps were skipped on the device).
+        The monitor shows the frames completed so far, so the count of the last step may only
+        show at a later one."""
+        frames, _, overflows, last = self.frame_monitor()
+        if frames > self._monitor_frames0:
+            self._largest_keys = max(self._largest_keys, last)
+        b = self.render_buffers
+        want = int(1.5 * self._largest_keys) + 1024 if self._largest_keys > 0.8 * b.key_capacity else 0
+        if overflows > self._monitor_seen:
+            self.skipped_steps += overflows - self._monitor_seen
+            self._monitor_seen = overflows
+            want = max(want, 2 * b.key_capacity)
+        if want > b.key_capacity:
+            b._alloc_keys(want)
 
     def adc_step_due(self):
         """Whether maybe_densify_and_prune! densifies and prunes at this iteration."""
@@ -484,7 +536,8 @@ class Trainer:
         if it > o.adc_final_iteration_nb:
             return False
         nbf = self.render_buffers.nb_fgaussians
-        adc_stats_(self.adc, self.fgradients, self.render_buffers.fgidx_to_gidx, nbf, self.last_camera)
+        adc_stats_(self.adc, self.fgradients, self.render_buffers.fgidx_to_gidx, nbf, self.last_camera,
+                   self.render_buffers)
         if not (it >= o.adc_start_iteration_nb and it % o.adc_interval == 0):
             return False
         n_new = adc_plan_(self.adc, self.gaussians, float(logit32(o.pruning_min_opacity)),
@@ -509,5 +562,7 @@ class Trainer:
     def complete_adc_step_(self):
         """complete_adc_step! (training.jl:455-459): resize gradients and render buffers."""
         n = len(self.gaussians)
-        self.fgradients = FilteredGaussiansGradientsVector(n, self.gaussians.sh_degree, self.device.index)
         self.render_buffers.ensure_capacity(n)
+        # (at least the render buffers' capacity, which device-count steps need)
+        self.fgradients = FilteredGaussiansGradientsVector(max(n, self.render_buffers.capacity),
+                                                           self.gaussians.sh_degree, self.device.index)
