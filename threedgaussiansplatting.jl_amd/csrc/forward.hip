@@ -557,7 +557,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
         }
     }
     __syncthreads();
-    counts0[(int64_t)t * count_tiles + blockIdx.x] = s_h[t];
+    counts0[rs_entry(t, blockIdx.x, count_tiles)] = s_h[t];
 }
 
 // The 16-bit tile sort's first pass fused with key emission: emission blocks are radix tiles
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
             dc[kCntStatus] = st;
         }
         if ((int64_t)blockIdx.x * kEmitTile >= m) {   // past the keys: an empty column of counts
-            if (t < kRsBins) counts0[(int64_t)t * count_tiles + blockIdx.x] = 0;
+            if (t < kRsBins) counts0[rs_entry(t, blockIdx.x, count_tiles)] = 0;
             return;
         }
     }
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
     for (int i = 0; i < kEmitSortItems; ++i)
         if (first + i < m) atomicAdd(&s_h[(uint32_t)tile[i] & mask0], 1u);
     __syncthreads();
-    if (t < kRsBins) counts0[(int64_t)t * count_tiles + blockIdx.x] = s_h[t];
+    if (t < kRsBins) counts0[rs_entry(t, blockIdx.x, count_tiles)] = s_h[t];
 }
 
 // Slot of key k of the block in k_emit_scatter's transpose (thread k / 8 writes item k % 8,

@@ -51,6 +51,22 @@ static_assert(RsTile<uint16_t>::kTile >= kRsMinTile && RsTile<uint32_t>::kTile >
 constexpr int kRsWaves = kRsThreads / kWave;
 static_assert(kRsThreads >= kRsBins && kRsThreads % kRsBins == 0, "digit owners");
 
+// Column of radix tile `tile` in a row of the digit-major count table. Workgroups are dealt
+// round-robin to the 8 XCDs (each with its own L2), so tile t runs on XCD t % 8; the columns
+// are grouped by XCD (tile t at (t % 8) * (pitch / 8) + t / 8) so that the cache lines one
+// XCD's count workgroups write, and its scatter workgroups read, are not shared with another
+// XCD's L2 (partial lines merged across XCDs cost 7x the table in write traffic). Rows are
+// rs_pitch(tiles) words apart.
+constexpr int kXcds = 8;
+__host__ __device__ inline int64_t rs_pitch(int64_t tiles) { return (tiles + kXcds - 1) / kXcds * kXcds; }
+__host__ __device__ inline int64_t rs_col(int64_t tile, int64_t tiles) {
+    return (tile % kXcds) * (rs_pitch(tiles) / kXcds) + tile / kXcds;
+}
+// Entry of digit d and radix tile `tile` in the count table.
+__host__ __device__ inline int64_t rs_entry(int d, int64_t tile, int64_t tiles) {
+    return (int64_t)d * rs_pitch(tiles) + rs_col(tile, tiles);
+}
+
 // Lanes of the wavefront holding the same digit as this lane (among lanes with valid).
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, int nbits, bool valid) {
     uint64_t peers = __ballot(valid);
@@ -114,14 +130,18 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_count(const K* __restrict__ k
                                                          const int64_t* d_n, int drop_max) {
     __shared__ uint32_t s_h[kRsBins];
     tile_digit_histogram(keys, d_n ? (*d_n < n ? *d_n : n) : n, blockIdx.x, shift, nbits, s_h, drop_max != 0);
-    if (threadIdx.x < kRsBins) counts[(int64_t)threadIdx.x * tiles + blockIdx.x] = s_h[threadIdx.x];
+    if (threadIdx.x < kRsBins) counts[rs_entry(threadIdx.x, blockIdx.x, tiles)] = s_h[threadIdx.x];
 }
 
-// Workgroup d: exclusive prefix of counts[d][0..tiles) in place, total to totals[d].
+// Workgroup d: exclusive prefix of digit d's counts over the tiles (in tile order), in place,
+// total to totals[d].
 static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restrict__ counts, int64_t tiles,
                                                              uint32_t* __restrict__ totals) {
     __shared__ uint32_t s_tmp[4];
-    uint32_t* row = counts + (int64_t)blockIdx.x * tiles;
+    uint32_t* const row0 = counts + (int64_t)blockIdx.x * rs_pitch(tiles);
+    const int64_t per = rs_pitch(tiles) / kXcds;
+    // entry of tile i in the row
+    auto at = [&](int64_t i) -> uint32_t& { return row0[(i % kXcds) * per + i / kXcds]; };
     const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
     constexpr int IT = 8;
     uint32_t carry = 0;
@@ -131,7 +151,7 @@ static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restric
         uint32_t acc = 0;
 #pragma unroll
         for (int k = 0; k < IT; ++k) {
-            v[k] = b + k < tiles ? row[b + k] : 0u;
+            v[k] = b + k < tiles ? at(b + k) : 0u;
             acc += v[k];
         }
         uint32_t incl = acc;
@@ -150,7 +170,7 @@ static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restric
         off += incl - acc;
 #pragma unroll
         for (int k = 0; k < IT; ++k) {
-            if (b + k < tiles) row[b + k] = off;
+            if (b + k < tiles) at(b + k) = off;
             off += v[k];
         }
         carry += blk;
@@ -188,7 +208,7 @@ __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const bool owner = t < kRsBins;
     const uint32_t total_t = owner ? totals[t] : 0u;
-    const uint32_t off_t = owner ? offsets[(int64_t)t * tiles + tile] : 0u;
+    const uint32_t off_t = owner ? offsets[rs_entry(t, tile, tiles)] : 0u;
     for (int i = t; i < kRsWaves * kRsBins; i += kRsThreads) (&s_wh[0][0])[i] = 0;
     __syncthreads();
     const uint32_t mask = (1u << nbits) - 1u;
@@ -329,14 +349,15 @@ inline uint32_t* radix_count_table(void* temp) { return (uint32_t*)temp; }
 
 // The digit totals inside radix_sort_pairs' scratch for n keys (after the count table).
 inline uint32_t* radix_totals(void* temp, int64_t n) {
-    return (uint32_t*)((char*)temp + align_up((size_t)ceil_div(n > 0 ? n : 1, kRsMinTile) * kRsBins * sizeof(uint32_t)));
+    return (uint32_t*)((char*)temp +
+                       align_up((size_t)rs_pitch(ceil_div(n > 0 ? n : 1, kRsMinTile)) * kRsBins * sizeof(uint32_t)));
 }
 
 // Scratch for radix_sort_pairs, excluding the ping-pong buffers: the digit-major count
-// table, the digit totals and an error word.
+// table (rows padded to a multiple of kXcds tiles), the digit totals and an error word.
 // (Sized for the smallest tile, so it serves every key width.)
 inline size_t radix_temp_bytes(int64_t n) {
-    return align_up((size_t)ceil_div(n > 0 ? n : 1, kRsMinTile) * kRsBins * sizeof(uint32_t)) +
+    return align_up((size_t)rs_pitch(ceil_div(n > 0 ? n : 1, kRsMinTile)) * kRsBins * sizeof(uint32_t)) +
            align_up((kRsBins + 64) * 4);
 }
 
@@ -344,7 +365,7 @@ inline size_t radix_temp_bytes(int64_t n) {
 // (alt_k, alt_v) is the ping-pong buffer. The first pass writes (kout) when the pass count is
 // odd and (alt) when it is even, so kin may alias whichever of the two the first pass does
 // not write (and it is never written otherwise). first_counts, when not null, is the count
-// table of the first pass ([256][radix_tiles<K>(n)] digit-major, from the producer of the
+// table of the first pass (256 rows of radix_tiles<K>(n) tiles at rs_entry, from the producer of the
 // keys); it is consumed (scanned in place). `err` (device word, may be null) is set nonzero
 // if the counts disagree with the keys (the affected keys are not written).
 //
