@@ -351,7 +351,9 @@ size_t tdgs_render_temp_bytes(int32_t capacity, int64_t key_capacity, const tdgs
  * raster. Synchronises once to learn the filtered count and the key count. When the key
  * count exceeds buf->key_capacity it returns TDGS_ERR_CAPACITY with *nb_keys_out set and
  * leaves the outputs untouched; grow the key arrays (and temp) and call again.
- * With at most 65535 tiles the sort by tile moves 16-bit tile ids, not the 64-bit keys, and
+ * With at most 65535 tiles the keys are not materialised: the tile lists (sorted_values,
+ * tiles_end) are built by binning the depth-ordered Gaussians to coarse blocks of tiles (the
+ * blocks' lists go through buf->keys and buf->values), with the same result as the sort, and
  * buf->sorted_keys is not written: tdgs_render_sorted_keys assembles it on request. */
 int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs_camera* cam,
                 const tdgs_tiling* tiling, const tdgs_render_options* opt,

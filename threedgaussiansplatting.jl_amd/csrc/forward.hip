@@ -395,6 +395,18 @@ __device__ void WriteScanAndBlocks::operator()(int64_t j, int64_t incl, int32_t 
 // and rectangle width are staged in LDS too (in the part of the scan buffer that a span of
 // that size leaves free); otherwise the walk reads them from global memory.
 constexpr int kEmitStage = 1024;
+
+// The grid the emission walks: the tiles (sx = sy = 0), or the coarse blocks of 2^sx x 2^sy
+// tiles (ntx blocks per row); a Gaussian's rectangle of tiles covers the rectangle of blocks
+// from the block of its first tile to the block of its last.
+struct EmitGrid {
+    int32_t ntx, sx, sy;
+    __device__ __forceinline__ void rect(const int4 r, int32_t* t0, int32_t* wx) const {
+        const int32_t x0 = (r.x - 1) >> sx, y0 = (r.y - 1) >> sy, x1 = (r.z - 1) >> sx;
+        *t0 = x0 + 1 + y0 * ntx;
+        *wx = x1 - x0 + 1;
+    }
+};
 static_assert(kEmitStage + 1 + 3 * kEmitStage <= kEmitTile + 1, "staging fits the scan buffer");
 
 // Slot of key k (0 <= k < kEmitTile) of the block in the LDS transpose: thread k / kEmitItems
@@ -412,7 +424,7 @@ __device__ __forceinline__ int emit_slot(int k) {
 template <int THREADS, int ITEMS>
 __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t block, const int32_t* __restrict__ sorted_f,
                                               const int32_t* __restrict__ cs, const int32_t* __restrict__ blk_first,
-                                              const int32_t* __restrict__ ranges, int32_t ntx, int32_t* s_buf,
+                                              const int32_t* __restrict__ ranges, EmitGrid grid, int32_t* s_buf,
                                               int64_t* s_range, int32_t (&tile)[ITEMS], int32_t (&val)[ITEMS]) {
     constexpr int kBlock = THREADS * ITEMS;
     static_assert(kBlock == kEmitTile, "emission blocks of kEmitTile keys");
@@ -453,8 +465,7 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
                 const int32_t f = sorted_f[j + 1];
                 const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
                 s_f[k] = f;
-                s_t0[k] = r.x + (r.y - 1) * ntx;
-                s_wx[k] = r.z - r.x + 1;
+                grid.rect(r, &s_t0[k], &s_wx[k]);
             }
         }
     }
@@ -479,9 +490,7 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
                 f = s_f[k]; t0 = s_t0[k]; wx = s_wx[k];
             } else {
                 f = sorted_f[j_lo + k];
-                const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
-                t0 = r.x + (r.y - 1) * ntx;
-                wx = r.z - r.x + 1;
+                grid.rect(reinterpret_cast<const int4*>(ranges)[f - 1], &t0, &wx);
             }
         };
         load(lo);
@@ -497,7 +506,7 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
                 q = 0;
                 rx = 0;
             }
-            tile[i] = t0 + q * ntx + rx;
+            tile[i] = t0 + q * grid.ntx + rx;
             val[i] = f;
             if (++rx == wx) {
                 rx = 0;
@@ -515,7 +524,7 @@ template <bool TILE16>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
     const int32_t* __restrict__ blk_first, const float* __restrict__ depths, const int32_t* __restrict__ ranges,
-    int32_t ntx, void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0,
+    EmitGrid grid, void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0,
     uint32_t* __restrict__ counts0, int64_t count_tiles) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
@@ -524,7 +533,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     s_h[t] = 0;
     const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
     int32_t tile[kEmitItems], val[kEmitItems];
-    emit_generate<kEmitThreads, kEmitItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf, s_range,
+    emit_generate<kEmitThreads, kEmitItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, grid, s_buf, s_range,
                                             tile, val);
     // values, then tile ids (or keys), through LDS to coalesced stores
     const int64_t nk = m - d0 < kEmitTile ? m - d0 : kEmitTile;
@@ -575,7 +584,7 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
                                                                  const int32_t* __restrict__ sorted_f,
                                                                  const int32_t* __restrict__ cs,
                                                                  const int32_t* __restrict__ blk_first,
-                                                                 const int32_t* __restrict__ ranges, int32_t ntx,
+                                                                 const int32_t* __restrict__ ranges, EmitGrid grid,
                                                                  int nbits0, uint32_t* __restrict__ counts0,
                                                                  int64_t count_tiles, int64_t* dc, int64_t key_cap) {
     __shared__ int32_t s_buf[kEmitTile + 1];
@@ -583,24 +592,27 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
     __shared__ uint32_t s_h[kRsBins];
     const int t = threadIdx.x;
     if (dc) {
-        // device counts: the grid covers key_cap keys; the key passes use M, or none when M does
-        // not fit (the status says why)
+        // device counts: the grid covers key_cap entries; when the M keys fit the key arrays the
+        // passes emit the blocks' entries (at most M), else none (the status says why)
         nb = dc[4];
-        m = dc[1];
-        const int64_t st = m > key_cap ? kFrameKeyCapacity : m >= (int64_t)INT32_MAX ? kFrameKeyRange : kFrameOk;
-        if (st != kFrameOk) m = 0;
+        const int64_t packed = dc[kCntCoarse];   // (M << 32) | coarse entries, from the scan
+        const int64_t keys = packed >> 32;
+        const int64_t st = keys > key_cap ? kFrameKeyCapacity : keys >= (int64_t)INT32_MAX ? kFrameKeyRange : kFrameOk;
+        m = st == kFrameOk ? (packed & kLow32) : 0;
         if (blockIdx.x == 0 && t == 0) {
-            dc[kCntKeysUsed] = m;
+            dc[1] = keys;
+            dc[kCntKeysUsed] = st == kFrameOk ? keys : 0;
+            dc[kCntCoarseUsed] = m;
             dc[kCntStatus] = st;
         }
-        if ((int64_t)blockIdx.x * kEmitTile >= m) {   // past the keys: an empty column of counts
+        if ((int64_t)blockIdx.x * kEmitTile >= m) {   // past the entries: an empty column of counts
             if (t < kRsBins) counts0[rs_entry(t, blockIdx.x, count_tiles)] = 0;
             return;
         }
     }
     if (t < kRsBins) s_h[t] = 0;
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
-    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf,
+    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, grid, s_buf,
                                                     s_range, tile, val);
     const int64_t first = (int64_t)blockIdx.x * kEmitTile + (int64_t)t * kEmitSortItems;
     const uint32_t mask0 = (1u << nbits0) - 1u;
@@ -621,20 +633,20 @@ __device__ __forceinline__ int emit_sort_slot(int k) {
 
 __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
-    const int32_t* __restrict__ blk_first, const int32_t* __restrict__ ranges, int32_t ntx, int nbits0,
+    const int32_t* __restrict__ blk_first, const int32_t* __restrict__ ranges, EmitGrid grid, int nbits0,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, int64_t count_tiles,
     uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err, const int64_t* dc) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
-    if (dc) {   // device counts (k_emit_count set the key count used)
+    if (dc) {   // device counts (k_emit_count set the entry count used)
         nb = dc[4];
-        m = dc[kCntKeysUsed];
+        m = dc[kCntCoarseUsed];
         if (d0 >= m) return;
     }
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
-    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, ntx, s_buf,
+    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, grid, s_buf,
                                                     s_range, tile, val);
     uint16_t key[kEmitSortItems];
     int32_t v[kEmitSortItems];
@@ -717,8 +729,11 @@ __global__ __launch_bounds__(256) void k_tile_ranges(int64_t m, const K* __restr
 // The same on 16-bit tile ids, eight sorted entries per thread (one 16-byte load, plus the id
 // that follows them).
 __global__ __launch_bounds__(256) void k_tile_ranges16(int64_t m, const uint16_t* __restrict__ st, int32_t nb_tiles,
-                                                       int32_t* __restrict__ te, const int64_t* dm = nullptr) {
+                                                       int32_t* __restrict__ te, const int64_t* dm = nullptr,
+                                                       int32_t* zero = nullptr, int64_t nzero = 0) {
     const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    // (also clears zero[0, nzero) for the next kernel)
+    for (int64_t k = i0 / 8; k < nzero; k += (int64_t)gridDim.x * blockDim.x) zero[k] = 0;
     if (dm) {   // device key count (the grid covers the key capacity); no keys: empty tiles
         m = *dm;
         if (m == 0)
@@ -755,6 +770,253 @@ __global__ __launch_bounds__(256) void k_tile_ranges16(int64_t m, const uint16_t
             for (int32_t t = lo; t <= nb_tiles; ++t) te[t - 1] = (int32_t)m;
         }
     }
+}
+
+// ------------------------------------------------------------------------------------
+// Tile lists by coarse binning (at most 65535 tiles)
+// ------------------------------------------------------------------------------------
+// The reference sorts the M (tile, depth) keys (forward_core.jl:605-660); its result is, for
+// every tile in id order, the Gaussians covering the tile in depth order. Here the non-empty
+// Gaussians, already in depth order, are binned to coarse blocks of 2^sx x 2^sy tiles: one
+// 16-bit block id per (Gaussian, block its tile rectangle touches), stably sorted by the radix
+// passes (emission fused with the first), far fewer entries than keys. Then one workgroup
+// per block walks the block's Gaussians in depth order and, for each of its tiles, keeps
+// those whose rectangle covers the tile: k_bin_tiles<COUNT> counts them, a scan turns the
+// counts into tiles_end (a scan), and k_bin_tiles<WRITE> writes each tile's Gaussians (wavefront
+// compaction, consecutive addresses) at the tile's place. Same lists as the sort, bit for
+// bit, with the M keys never written or moved.
+
+// Block geometry: the smallest of 8 x 8, 16 x 8, 16 x 16 tiles that leaves at most 255 blocks
+// (8-bit ids: one radix pass), else 16 x 16.
+struct BinGeom {
+    int sx, sy;
+    int32_t nbx, nby;
+    int32_t nblocks() const { return nbx * nby; }
+};
+static BinGeom bin_geom(const tdgs_tiling* t) {
+    const int shapes[3][2] = {{3, 3}, {4, 3}, {4, 4}};
+    BinGeom g{4, 4, 0, 0};
+    for (int k = 0; k < 3; ++k) {
+        g.sx = shapes[k][0];
+        g.sy = shapes[k][1];
+        g.nbx = (int32_t)ceil_div(t->nb_tiles_x, 1 << g.sx);
+        g.nby = (int32_t)ceil_div(t->nb_tiles_y, 1 << g.sy);
+        if (g.nblocks() <= 255) break;   // 1-based ids of at most 8 bits
+    }
+    return g;
+}
+
+// Tiles and blocks touched by each non-empty Gaussian in depth order, packed as
+// (tiles << 32) | blocks (entries past N_b count 0): one scan gives the blocks' emission
+// offsets in the low half and, in its total, the key count M in the high half (both below
+// 2^31, so the halves never carry into each other).
+struct SortedTileBlockCounts {
+    const int32_t* sorted_f;
+    const int32_t* counts;
+    const int32_t* ranges;
+    int sx, sy;
+    const int64_t* d_nb;
+    __device__ int64_t operator()(int64_t j) const {
+        if (j >= *d_nb) return 0;
+        const int32_t f = sorted_f[j] - 1;
+        const int4 r = reinterpret_cast<const int4*>(ranges)[f];
+        const int32_t blocks =
+            (((r.z - 1) >> sx) - ((r.x - 1) >> sx) + 1) * (((r.w - 1) >> sy) - ((r.y - 1) >> sy) + 1);
+        return ((int64_t)counts[f] << 32) | (int64_t)blocks;
+    }
+};
+// WriteScanAndBlocks on the blocks' half of the packed scan.
+struct WriteBlockScan {
+    WriteScanAndBlocks w;
+    __device__ void operator()(int64_t j, int64_t incl, int64_t item) const {
+        w(j, incl & kLow32, (int32_t)(item & kLow32));
+    }
+};
+
+// Each block's list is cut into `segs` consecutive segments, one workgroup each (more
+// workgroups in flight; the counts and offsets are per (segment, tile)).
+constexpr int kBinMaxSegs = 16;
+inline int bin_segments(int32_t nblocks) {
+    const int s = 1024 / (nblocks > 0 ? nblocks : 1);
+    return s < 1 ? 1 : s > kBinMaxSegs ? kBinMaxSegs : s;
+}
+
+struct BinArgs {
+    int32_t ntx, nty, nbx, sy, nblocks, segs;
+    const int32_t* cvals;      // the blocks' lists: fgidx (1-based), block by block, depth order within
+    const int32_t* cend;       // inclusive end of each block's run in cvals
+    int64_t mc;                // entries of cvals (launch bound)
+    const int64_t* dmc;        // entries used (device counts), or null
+    const int32_t* ranges;     // tile rectangles [x0, y0, x1, y1] (1-based, inclusive) by fgidx
+    int32_t* tile_counts;      // [tiles][segs]: COUNT writes the Gaussians of the segment covering each tile
+    int32_t* tile_totals;      // COUNT adds them up per tile (zeroed beforehand)
+    const int32_t* tiles_end;  // WRITE: inclusive ends of the tiles' lists
+    int32_t* out;              // WRITE: sdfgidx_to_fgidx
+    int32_t cap;               // WRITE: entries of out
+    uint32_t* err;
+};
+
+// Workgroup: one segment of one block of 2^SX x 2^sy tiles, 4 threads per tile; wavefront w
+// takes the block's tiles 16 w .. 16 w + 15 (row-major, 2^SX per row). The segment's Gaussians
+// go through LDS in chunks of kBinPer per thread, as the tile rectangle clipped to the block in
+// two bit masks (columns, rows); a wavefront then tests 64 of them at a time against each of
+// its tiles with one ballot.
+constexpr int kBinPer = 4;   // candidates each thread stages per chunk (their loads in flight together)
+
+template <int SX, bool WRITE>
+__global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
+    __shared__ int32_t s_f[1024 * kBinPer];
+    __shared__ uint32_t s_m[1024 * kBinPer];
+    constexpr int BW = 1 << SX;
+    const int BH = 1 << a.sy;
+    const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
+    const int nt = (int)blockDim.x * kBinPer;   // candidates per chunk
+    const int b = blockIdx.x % a.nblocks, seg = blockIdx.x / a.nblocks;
+    const int bx = b % a.nbx, by = b / a.nbx;
+    const int x0b = bx * BW, y0b = by * BH;   // 0-based first tile of the block
+    int64_t mc = a.mc;
+    if (a.dmc && *a.dmc < mc) mc = *a.dmc;
+    int64_t ce = a.cend[b], cb = b == 0 ? 0 : a.cend[b - 1];
+    if (ce > mc) ce = mc;
+    if (cb > ce) cb = ce;
+    {   // the segment
+        const int64_t len = ce - cb;
+        ce = cb + len * (seg + 1) / a.segs;
+        cb = cb + len * seg / a.segs;
+    }
+    int32_t* const seg_counts = a.tile_counts + seg;   // entry of tile t: seg_counts[t segs]
+    const int ly0 = (16 * w) >> SX;   // the wavefront's first local row
+    int32_t cnt[16];                  // COUNT: hits so far; WRITE: the next output index
+    int32_t start = 0;
+    if (WRITE) {
+        // lane i < 16: tile i's list start plus the earlier segments' Gaussians in it (all the
+        // loads in flight at once)
+        const int x = x0b + ((16 * w + lane) & (BW - 1)), y = y0b + ((16 * w + lane) >> SX);
+        if (lane < 16 && x < a.ntx && y < a.nty) {
+            const int tile = x + y * a.ntx;
+            int32_t c[kBinMaxSegs];
+#pragma unroll
+            for (int q = 0; q < kBinMaxSegs; ++q) c[q] = q < seg ? a.tile_counts[(int64_t)tile * a.segs + q] : 0;
+            start = tile > 0 ? a.tiles_end[tile - 1] : 0;
+#pragma unroll
+            for (int q = 0; q < kBinMaxSegs; ++q) start += c[q];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cnt[i] = WRITE ? __builtin_amdgcn_readlane(start, i) : 0;
+    for (int64_t base = cb; base < ce; base += nt) {
+        // candidates base + t + blockDim q (q < kBinPer): the loads of each stage issue together
+        int32_t f[kBinPer];
+#pragma unroll
+        for (int q = 0; q < kBinPer; ++q) {
+            const int64_t k = base + t + (int64_t)blockDim.x * q;
+            f[q] = k < ce ? a.cvals[k] : 0;
+        }
+        int4 r[kBinPer];
+#pragma unroll
+        for (int q = 0; q < kBinPer; ++q)
+            r[q] = f[q] > 0 ? reinterpret_cast<const int4*>(a.ranges)[f[q] - 1] : make_int4(1, 1, 0, 0);
+#pragma unroll
+        for (int q = 0; q < kBinPer; ++q) {
+            // columns in bits 0-15, rows in bits 16-31 (of the block); none for an empty slot
+            const int cx0 = max(r[q].x - 1 - x0b, 0), cx1 = min(r[q].z - 1 - x0b, BW - 1);
+            const int cy0 = max(r[q].y - 1 - y0b, 0), cy1 = min(r[q].w - 1 - y0b, BH - 1);
+            const uint32_t cm = cx1 >= cx0 ? (2u << cx1) - (1u << cx0) : 0u;
+            const uint32_t rm = cy1 >= cy0 ? (2u << cy1) - (1u << cy0) : 0u;
+            s_f[t + blockDim.x * q] = f[q];
+            s_m[t + blockDim.x * q] = cm | (rm << 16);
+        }
+        __syncthreads();
+        const int nk = (int)(ce - base < nt ? ce - base : nt);
+        for (int j0 = 0; j0 < nk; j0 += kWave) {
+            const uint32_t p = s_m[j0 + lane];   // (entries past nk are zero: no hits)
+            // the wavefront's 16 tiles as bits: 8 x 2 (SX = 3) or 16 x 1 (SX = 4)
+            uint32_t h;
+            if (SX == 3)
+                h = (((p >> (16 + ly0)) & 1u) ? (p & 0xffu) : 0u) | (((p >> (17 + ly0)) & 1u) ? (p & 0xffu) << 8 : 0u);
+            else
+                h = ((p >> (16 + ly0)) & 1u) ? (p & 0xffffu) : 0u;
+            int32_t fv = 0;
+            if (WRITE) fv = s_f[j0 + lane];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const bool hit = (h >> i) & 1u;
+                const uint64_t bal = __ballot(hit);
+                if (WRITE && hit) {
+                    // (the counts come from the same walk; the index is clamped all the same)
+                    const int32_t o = cnt[i] + (int32_t)__popcll(bal & lanemask_lt());
+                    a.out[o < a.cap ? o : a.cap - 1] = fv;
+                }
+                cnt[i] += __popcll(bal);
+            }
+        }
+        __syncthreads();
+    }
+    if (!WRITE) {
+        int32_t mine = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mine = lane == i ? cnt[i] : mine;
+        const int x = x0b + ((16 * w + lane) & (BW - 1)), y = y0b + ((16 * w + lane) >> SX);
+        if (lane < 16 && x < a.ntx && y < a.nty) {
+            seg_counts[(int64_t)(x + y * a.ntx) * a.segs] = mine;
+            if (mine != 0) atomicAdd(&a.tile_totals[x + y * a.ntx], mine);
+        }
+    }
+}
+
+// One workgroup: tiles_end = inclusive scan of the tiles' totals (each thread a contiguous run
+// of 4k tiles, read as int4). The total must equal the key count M (*expect, or
+// expect_value; else *err is set: the lists would be incomplete).
+__global__ __launch_bounds__(1024) void k_bin_scan(const int32_t* __restrict__ totals, int32_t nt,
+                                                   int32_t* __restrict__ tiles_end, const int64_t* expect,
+                                                   int64_t expect_value, uint32_t* err) {
+    __shared__ int64_t s_w[1024 / kWave];
+    const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
+    const int per = ((nt + 1023) / 1024 + 3) & ~3;
+    const int lo = t * per;
+    int64_t sum = 0;
+#pragma unroll 4
+    for (int k = 0; k < per; k += 4) {
+        if (lo + k < nt) {
+            const int4 v = *reinterpret_cast<const int4*>(totals + lo + k);   // (the array is padded to 4k)
+            sum += (int64_t)(lo + k < nt ? v.x : 0) + (lo + k + 1 < nt ? v.y : 0) + (lo + k + 2 < nt ? v.z : 0) +
+                   (lo + k + 3 < nt ? v.w : 0);
+        }
+    }
+    int64_t incl = sum;
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int64_t o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) s_w[w] = incl;
+    __syncthreads();
+    int64_t off = 0, total = 0;
+    for (int k = 0; k < 1024 / kWave; ++k) {
+        if (k < w) off += s_w[k];
+        total += s_w[k];
+    }
+    int64_t run = off + incl - sum;
+    for (int i = lo; i < lo + per && i < nt; ++i) {
+        run += totals[i];
+        tiles_end[i] = (int32_t)run;
+    }
+    if (t == 0 && total != (expect ? *expect : expect_value)) atomicOr(err, 1u);
+}
+
+// The sorted keys (tile << 32 | depth bits) of the tile lists: the tile of list entry i is the
+// first with tiles_end > i.
+__global__ __launch_bounds__(256) void k_assemble_keys_te(int64_t m, const int32_t* __restrict__ te, int32_t nt,
+                                                          const int32_t* __restrict__ sv,
+                                                          const float* __restrict__ depths,
+                                                          int64_t* __restrict__ sk) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    int lo = 0, hi = nt - 1;   // smallest tile index with te > i
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if ((int64_t)te[mid] > i) hi = mid; else lo = mid + 1;
+    }
+    sk[i] = ((int64_t)(lo + 1) << 32) | (int64_t)float_bits(depths[sv[i] - 1]);
 }
 
 // The 64-bit sorted keys (tile << 32 | depth bits of the Gaussian) from the 16-bit sorted
@@ -1278,6 +1540,11 @@ static int end_bit_of(const tdgs_tiling* t) {
 }
 
 // Scratch layout of tdgs_render.
+// Items of the largest scan: the Gaussians, or the tiles (tile lists).
+static int64_t scan_items(int64_t cap, const tdgs_tiling* t) {
+    const int64_t nt = t ? (int64_t)t->nb_tiles_x * t->nb_tiles_y : 0;
+    return cap > nt ? cap : nt;
+}
 static int64_t rect_diff_size(const tdgs_tiling* t) {
     return t ? (int64_t)(t->nb_tiles_x + 1) * (t->nb_tiles_y + 1) : 0;
 }
@@ -1292,13 +1559,16 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(cap);                       // depth values, ping-pong
     ar.template take<int32_t>(cap);                       // depth values, sorted (fgidx)
     ar.template take<int32_t>(cap);                       // counts scan in depth order
-    ar.template take<char>((int64_t)scan_temp_bytes_for(cap));
+    ar.template take<char>((int64_t)scan_temp_bytes_for(scan_items(cap, t)));
     ar.template take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub) * kKeepSub);   // keep counts per block
     ar.template take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub));   // and per kKeepSub blocks
     const int64_t big = cap > key_cap ? cap : key_cap;
     ar.template take<char>((int64_t)radix_temp_bytes(big));
     ar.template take<int32_t>(kRectCopies * rect_diff_size(t));   // tile-coverage difference arrays
     ar.template take<int32_t>(ceil_div(key_cap, kEmitTile) + 2);  // first Gaussian of each emission block
+    ar.template take<int32_t>(t ? (int64_t)kBinMaxSegs * t->nb_tiles_x * t->nb_tiles_y : 0);   // per (segment, tile)
+    ar.template take<int32_t>(t ? bin_geom(t).nblocks() : 0);                    // ends of the blocks' lists
+    ar.template take<int32_t>(t ? ((int64_t)t->nb_tiles_x * t->nb_tiles_y + 3) / 4 * 4 : 0);   // tiles' totals
 }
 
 // The scratch arrays of tdgs_render / tdgs_project inside buf->temp (render_layout's order).
@@ -1314,6 +1584,10 @@ struct RenderScratch {
     int64_t ndiff;
     int32_t* blk_first;
     int64_t nblk;
+    int32_t* tile_counts;
+    int32_t* block_end;
+    int32_t* tile_totals;
+    int64_t ntt;   // entries of tile_totals (tiles, padded to 4)
 };
 
 static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const tdgs_tiling* tiling) {
@@ -1328,7 +1602,7 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.dval_alt = ar.take<int32_t>(cap);
     r.sorted_f = ar.take<int32_t>(cap);
     r.cs = ar.take<int32_t>(cap);
-    r.sbytes = scan_temp_bytes_for(cap);
+    r.sbytes = scan_temp_bytes_for(scan_items(cap, tiling));
     r.stemp = ar.take<char>((int64_t)r.sbytes);
     r.block_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub) * kKeepSub);
     r.group_counts = ar.take<int32_t>(ceil_div(cap, kProjThreads * kKeepSub));
@@ -1339,6 +1613,10 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.rect_diff = ar.take<int32_t>(kRectCopies * r.ndiff);
     r.nblk = ceil_div(buf->key_capacity, kEmitTile) + 2;
     r.blk_first = ar.take<int32_t>(r.nblk);
+    r.tile_counts = ar.take<int32_t>(tiling ? (int64_t)kBinMaxSegs * tiling->nb_tiles_x * tiling->nb_tiles_y : 0);
+    r.block_end = ar.take<int32_t>(tiling ? bin_geom(tiling).nblocks() : 0);
+    r.ntt = tiling ? ((int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y + 3) / 4 * 4 : 0;
+    r.tile_totals = ar.take<int32_t>(r.ntt);
     return r;
 }
 
@@ -1398,66 +1676,79 @@ static int launch_keep_and_project(hipStream_t s, const tdgs_gaussians* g, const
 
 using namespace tdgs;
 
-// Steps 6-9 of tdgs_render with TDGS_FLAG_DEVICE_COUNTS: no host synchronisation. The launches
-// are sized by the key capacity and every kernel reads N_f, the non-empty count and M from the
-// context's counters; k_emit_count records the key count the passes use (0 when M does not
-// fit the key arrays, with the frame status saying so), and the blend copies the counts to the
-// frame counts of the buffers. At most 65535 tiles (16-bit tile ids); the tile ranges come
-// from the sorted ids.
-static int render_keys_device_counts(tdgs_ctx* ctx, hipStream_t s, const tdgs_camera* cam,
-                                     const tdgs_tiling* tiling, const tdgs_render_options* opt,
-                                     tdgs_render_buffers* buf, const tdgs_render_outputs* out,
-                                     const RenderScratch& r, int64_t n) {
-    int64_t* dc = ctx->d_counters;
-    uint32_t* d_err = ctx_error_word(ctx);
-    const int64_t kc = buf->key_capacity;
-    const int eb = end_bit_of(tiling);
-    const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
-    const int te_bit = eb - 32;
-    const int passes = radix_passes(0, te_bit);
-    const int nbits0 = radix_digit_bits(0, te_bit);
-    uint16_t* t16_out = reinterpret_cast<uint16_t*>(buf->keys);
-    uint16_t* t16_alt = t16_out + kc;
-    const unsigned egrid = (unsigned)ceil_div(kc, kEmitTile);
-    const int64_t count_tiles = radix_tiles<uint16_t>(kc);
-    uint32_t* table = radix_count_table(r.rtemp);
-    uint32_t* totals = radix_totals(r.rtemp, kc);
+// Steps 6-8 for at most 65535 tiles: the coarse blocks' lists (emission of one block id per
+// (Gaussian, block touched) in depth order, fused with the first stable radix pass on the
+// ids; usually the only pass), their ends, then the tile lists (count, scan, write).
+// Synchronous: nb, mc (entries) and m (keys) are the host's counts. With device counts
+// (dc not null) the launches are sized by the key capacity, k_emit_count decides on the device
+// whether the keys fit, and every kernel reads the entry count it uses from dc.
+static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_buffers* buf,
+                          const RenderScratch& r, int64_t nb, int64_t mc, int64_t m, int64_t* dc,
+                          uint32_t* d_err) {
+    const BinGeom bg = bin_geom(tiling);
+    const int32_t nblocks = bg.nblocks();
+    int cbits = 0;   // bits of the 1-based block ids
+    while ((1ll << cbits) <= nblocks) ++cbits;
+    const int passes = radix_passes(0, cbits);
+    const int nbits0 = radix_digit_bits(0, cbits);
     const bool one_pass = passes == 1;
-    (void)n;
+    const int64_t kc = buf->key_capacity;
+    const int64_t mb = dc ? kc : mc;   // launch bound of the entries
+    uint16_t* c16 = reinterpret_cast<uint16_t*>(buf->keys);
+    uint16_t* c16_alt = c16 + kc;
+    const EmitGrid cg{bg.nbx, bg.sx, bg.sy};
+    const unsigned egrid = (unsigned)ceil_div(mb, kEmitTile);
+    const int64_t count_tiles = radix_tiles<uint16_t>(mb);
+    uint32_t* table = radix_count_table(r.rtemp);
+    uint32_t* totals = radix_totals(r.rtemp, mb);
+    const int64_t* d_used = dc ? dc + kCntCoarseUsed : nullptr;
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
-        k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(0, 0, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges,
-                                                        tiling->nb_tiles_x, nbits0, table, count_tiles, dc, kc);
+        k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges, cg,
+                                                        nbits0, table, count_tiles, dc, kc);
         TDGS_LAUNCHED();
     }
     {
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
         k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals);
         TDGS_LAUNCHED();
-        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(0, 0, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges,
-                                                          tiling->nb_tiles_x, nbits0, table, totals, count_tiles,
-                                                          one_pass ? t16_out : t16_alt,
-                                                          one_pass ? buf->sorted_values : buf->values, d_err, dc);
+        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges,
+                                                          cg, nbits0, table, totals, count_tiles,
+                                                          one_pass ? c16 : c16_alt,
+                                                          one_pass ? buf->values : buf->sorted_values, d_err, dc);
         TDGS_LAUNCHED();
         if (!one_pass)
-            TDGS_TRY(radix_sort_pairs<uint16_t>(t16_alt, t16_out, buf->values, buf->sorted_values, t16_alt,
-                                                buf->values, kc, nbits0, te_bit, r.rtemp, r.rbytes, s, nullptr, d_err,
-                                                nullptr, dc + kCntKeysUsed));
+            TDGS_TRY(radix_sort_pairs<uint16_t>(c16_alt, c16, buf->sorted_values, buf->values, c16_alt,
+                                                buf->sorted_values, mb, nbits0, cbits, r.rtemp, r.rbytes, s, nullptr,
+                                                d_err, nullptr, d_used));
     }
-    {
-        StageScope sc(TDGS_STAGE_TILE_RANGES, s);
-        const int64_t threads = ceil_div(kc, 8) > nb_tiles ? ceil_div(kc, 8) : nb_tiles;
-        if (((uintptr_t)t16_out & 15) == 0)
-            k_tile_ranges16<<<(unsigned)ceil_div(threads, 256), 256, 0, s>>>(kc, t16_out, nb_tiles, buf->tiles_end,
-                                                                              dc + kCntKeysUsed);
-        else
-            k_tile_ranges<uint16_t><<<(unsigned)ceil_div(kc > nb_tiles ? kc : nb_tiles, 256), 256, 0, s>>>(
-                kc, t16_out, nb_tiles, buf->tiles_end, dc + kCntKeysUsed);
-        TDGS_LAUNCHED();
-    }
-    StageScope sc(TDGS_STAGE_BLEND, s);
-    return launch_render_tiles(s, cam, tiling, opt, kc, buf->tiles_end, buf->sorted_values, buf->f2d, buf->depths,
-                               out, nullptr, dc, frame_counts(buf), ctx->d_counters + kCounters, ctx->h_monitor_dev);
+    StageScope sc(TDGS_STAGE_TILE_RANGES, s);
+    // ends of the blocks' runs
+    const int64_t rthreads = ceil_div(mb, 8) > nblocks ? ceil_div(mb, 8) : nblocks;
+    k_tile_ranges16<<<(unsigned)ceil_div(rthreads, 256), 256, 0, s>>>(mb, c16, nblocks, r.block_end, d_used,
+                                                                      r.tile_totals, r.ntt);
+    TDGS_LAUNCHED();
+    // the tile lists
+    BinArgs ba;
+    const int segs = bin_segments(nblocks);
+    ba.ntx = tiling->nb_tiles_x; ba.nty = tiling->nb_tiles_y; ba.nbx = bg.nbx; ba.sy = bg.sy;
+    ba.nblocks = nblocks; ba.segs = segs;
+    ba.cvals = buf->values; ba.cend = r.block_end; ba.mc = mb; ba.dmc = d_used;
+    ba.ranges = buf->tile_ranges; ba.tile_counts = r.tile_counts; ba.tile_totals = r.tile_totals;
+    ba.tiles_end = buf->tiles_end;
+    ba.out = buf->sorted_values; ba.cap = (int32_t)(kc < INT32_MAX ? kc : INT32_MAX); ba.err = d_err;
+    const unsigned bthreads = 4u << (bg.sx + bg.sy);
+    const unsigned bgrid = (unsigned)(nblocks * segs);
+    if (bg.sx == 3) k_bin_tiles<3, false><<<bgrid, bthreads, 0, s>>>(ba);
+    else k_bin_tiles<4, false><<<bgrid, bthreads, 0, s>>>(ba);
+    TDGS_LAUNCHED();
+    k_bin_scan<<<1, 1024, 0, s>>>(r.tile_totals, tiling->nb_tiles_x * tiling->nb_tiles_y, buf->tiles_end,
+                                  dc ? dc + kCntKeysUsed : nullptr, m, d_err);
+    TDGS_LAUNCHED();
+    if (bg.sx == 3) k_bin_tiles<3, true><<<bgrid, bthreads, 0, s>>>(ba);
+    else k_bin_tiles<4, true><<<bgrid, bthreads, 0, s>>>(ba);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
 }
 
 extern "C" {
@@ -1598,9 +1889,10 @@ int tdgs_render_sorted_keys(void* stream, const tdgs_tiling* tiling, const tdgs_
     TDGS_REQUIRE(tiling && tiling->nb_tiles_x > 0 && tiling->nb_tiles_y > 0, "bad tiling");
     TDGS_REQUIRE(buf && nb_keys >= 0 && nb_keys <= buf->key_capacity, "bad buffers or key count");
     if (nb_keys == 0 || (int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y > 65535) return TDGS_OK;
-    TDGS_REQUIRE(buf->keys && buf->sorted_values && buf->sorted_keys && buf->depths, "null buffers");
-    k_assemble_keys<<<(unsigned)ceil_div(nb_keys, 256), 256, 0, (hipStream_t)stream>>>(
-        nb_keys, reinterpret_cast<const uint16_t*>(buf->keys), buf->sorted_values, buf->depths, buf->sorted_keys);
+    TDGS_REQUIRE(buf->tiles_end && buf->sorted_values && buf->sorted_keys && buf->depths, "null buffers");
+    k_assemble_keys_te<<<(unsigned)ceil_div(nb_keys, 256), 256, 0, (hipStream_t)stream>>>(
+        nb_keys, buf->tiles_end, tiling->nb_tiles_x * tiling->nb_tiles_y, buf->sorted_values, buf->depths,
+        buf->sorted_keys);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
@@ -1680,6 +1972,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     int64_t* d_m = ctx->d_counters + 1;
     uint32_t* d_err = ctx_error_word(ctx);
 
+    const bool tile16 = (int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y <= 65535;
+
     // 1-3: keep counts, compaction + projection
     TDGS_TRY(launch_keep_and_project(s, g, cam, tiling, opt, buf, r, d_nbf, dkey, dval));
     // 4: the N_b non-empty Gaussians by (depth bits, fgidx); empty and culled ones (all-ones
@@ -1690,6 +1984,48 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
                                             rtemp, rbytes, s, nullptr, d_err, d_nb));
     }
+    if (tile16) {
+        // 5: tiles and blocks touched, in depth order -> the blocks' entries (emission offsets)
+        // and M
+        const BinGeom bg = bin_geom(tiling);
+        {
+            StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
+            const SortedTileBlockCounts stb{sorted_f, buf->counts, buf->tile_ranges, bg.sx, bg.sy, d_nb};
+            TDGS_TRY(device_scan(stb, stb, WriteBlockScan{WriteScanAndBlocks{cs, blk_first, nblk}}, n, stemp, sbytes,
+                                 ctx->d_counters + kCntCoarse, s, d_nb));
+        }
+        if (device_counts) {
+            // 6-8 sized by the key capacity; the blend copies the counts to the frame counts
+            TDGS_TRY(bin_tile_lists(s, tiling, buf, r, n, buf->key_capacity, 0, ctx->d_counters, d_err));
+            StageScope sc(TDGS_STAGE_BLEND, s);
+            return launch_render_tiles(s, cam, tiling, opt, buf->key_capacity, buf->tiles_end, buf->sorted_values,
+                                       buf->f2d, buf->depths, out, nullptr, ctx->d_counters, frame_counts(buf),
+                                       ctx->d_counters + kCounters, ctx->h_monitor_dev);
+        }
+        TDGS_TRY(read_counters(ctx, s));
+        const int64_t nbf = ctx->h_counters[0];
+        const int64_t m = ctx->h_counters[kCntCoarse] >> 32;
+        const int64_t nb = ctx->h_counters[4];
+        const int64_t mc = ctx->h_counters[kCntCoarse] & kLow32;
+        *nb_fgaussians_out = (int32_t)nbf;
+        *nb_keys_out = m;
+        if (nbf == 0 || m == 0) return launch_render_void(s, cam, opt, out);
+        if (m >= (int64_t)INT32_MAX) {
+            set_error("%lld duplicated keys exceed the int32 index range", (long long)m);
+            return TDGS_ERR_CAPACITY;
+        }
+        if (m > buf->key_capacity || !buf->keys || !buf->values || !buf->sorted_keys || !buf->sorted_values) {
+            set_error("key buffers hold %lld keys, %lld needed", (long long)buf->key_capacity, (long long)m);
+            return TDGS_ERR_CAPACITY;
+        }
+        // 6-8: the tile lists by coarse binning
+        TDGS_TRY(bin_tile_lists(s, tiling, buf, r, nb, mc, m, nullptr, d_err));
+        // 9: blending
+        StageScope sc(TDGS_STAGE_BLEND, s);
+        return launch_render_tiles(s, cam, tiling, opt, m, buf->tiles_end, buf->sorted_values, buf->f2d,
+                                   buf->depths, out);
+    }
+    // more than 65535 tiles: the reference's 64-bit keys, sorted
     // 5: tile counts in depth order -> M
     {
         StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
@@ -1697,8 +2033,6 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
                              SortedCounts{sorted_f, buf->counts, d_nb}, WriteScanAndBlocks{cs, blk_first, nblk}, n, stemp,
                              sbytes, d_m, s, d_nb));
     }
-    if (opt->flags & TDGS_FLAG_DEVICE_COUNTS)
-        return render_keys_device_counts(ctx, s, cam, tiling, opt, buf, out, r, n);
     TDGS_TRY(read_counters(ctx, s));
     const int64_t nbf = ctx->h_counters[0];
     const int64_t m = ctx->h_counters[1];
@@ -1714,47 +2048,14 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         set_error("key buffers hold %lld keys, %lld needed", (long long)buf->key_capacity, (long long)m);
         return TDGS_ERR_CAPACITY;
     }
-    // 6-7: emit in depth order, then stable sort on the tile bits. With at most 65535 tiles the
-    // sort moves 16-bit tile ids (two arrays carved from buf->keys) and the values, and its
-    // first pass is fused with emission (k_emit_count, k_rs_scan_rows, k_emit_scatter: the keys
-    // are generated twice instead of written and read back); the remaining bits take at most
-    // one more pass. Beyond 65535 tiles emission writes 64-bit keys (with the first pass's
-    // counts) and radix_sort_pairs sorts their tile bits.
+    // 6-7: emit the 64-bit keys in depth order (with the first pass's counts), then the stable
+    // sort of their tile bits
     const int eb = end_bit_of(tiling);
     const int32_t nb_tiles = tiling->nb_tiles_x * tiling->nb_tiles_y;
-    const bool tile16 = nb_tiles <= 65535;
-    const int tb = tile16 ? 0 : 32;   // first tile bit of the sorted key
-    const int te_bit = tile16 ? eb - 32 : eb;
-    const int passes = radix_passes(tb, te_bit);
-    const int nbits0 = radix_digit_bits(tb, te_bit);   // digit of the first tile-sort pass
-    uint16_t* t16_out = reinterpret_cast<uint16_t*>(buf->keys);
-    uint16_t* t16_alt = t16_out + buf->key_capacity;
+    const int passes = radix_passes(32, eb);
+    const int nbits0 = radix_digit_bits(32, eb);   // digit of the first tile-sort pass
     const unsigned egrid = (unsigned)ceil_div(m, kEmitTile);
-    if (tile16) {
-        const int64_t count_tiles = radix_tiles<uint16_t>(m);
-        uint32_t* table = radix_count_table(rtemp);
-        uint32_t* totals = radix_totals(rtemp, m);
-        const bool one_pass = passes == 1;
-        {
-            StageScope sc(TDGS_STAGE_EMIT, s);
-            k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->tile_ranges,
-                                                            tiling->nb_tiles_x, nbits0, table, count_tiles, nullptr, 0);
-            TDGS_LAUNCHED();
-        }
-        StageScope sc(TDGS_STAGE_TILE_SORT, s);
-        k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals);
-        TDGS_LAUNCHED();
-        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->tile_ranges,
-                                                          tiling->nb_tiles_x, nbits0, table, totals, count_tiles,
-                                                          one_pass ? t16_out : t16_alt,
-                                                          one_pass ? buf->sorted_values : buf->values, d_err,
-                                                          nullptr);
-        TDGS_LAUNCHED();
-        if (!one_pass)
-            TDGS_TRY(radix_sort_pairs<uint16_t>(t16_alt, t16_out, buf->values, buf->sorted_values, t16_alt,
-                                                buf->values, m, tb + nbits0, te_bit, rtemp, rbytes, s, nullptr,
-                                                d_err));
-    } else {
+    {
         // the first radix pass writes the output arrays when the pass count is odd and the
         // alternate ones when even; emit into the other
         const bool emit_into_out = (passes % 2) == 0;
@@ -1764,13 +2065,14 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         {
             StageScope sc(TDGS_STAGE_EMIT, s);
             k_emit_depth_order<false><<<egrid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->depths,
-                                                                    buf->tile_ranges, tiling->nb_tiles_x, ek, ev2,
-                                                                    nbits0, radix_count_table(rtemp), count_tiles);
+                                                                    buf->tile_ranges, EmitGrid{tiling->nb_tiles_x, 0, 0},
+                                                                    ek, ev2, nbits0, radix_count_table(rtemp),
+                                                                    count_tiles);
             TDGS_LAUNCHED();
         }
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
         TDGS_TRY(radix_sort_pairs<uint64_t>((const uint64_t*)ek, (uint64_t*)buf->sorted_keys, ev2,
-                                            buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, tb, te_bit,
+                                            buf->sorted_values, (uint64_t*)buf->keys, buf->values, m, 32, eb,
                                             rtemp, rbytes, s, radix_count_table(rtemp), d_err));
     }
     // 8: tile ranges
@@ -1787,16 +2089,10 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
             TDGS_LAUNCHED();
             k_tiles_end_from_rects<<<(unsigned)tiling->nb_tiles_y, kTeThreads, 0, s>>>(
                 rect_diff, tiling->nb_tiles_x, buf->tiles_end);
-        } else if (tile16)
-            if (((uintptr_t)t16_out & 15) == 0)   // 16-byte loads of eight ids
-                k_tile_ranges16<<<(unsigned)ceil_div(ceil_div(m, 8), 256), 256, 0, s>>>(m, t16_out, nb_tiles,
-                                                                                       buf->tiles_end);
-            else
-                k_tile_ranges<uint16_t><<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, t16_out, nb_tiles,
-                                                                                  buf->tiles_end);
-        else
+        } else {
             k_tile_ranges<int64_t><<<(unsigned)ceil_div(m, 256), 256, 0, s>>>(m, buf->sorted_keys, nb_tiles,
                                                                              buf->tiles_end);
+        }
         TDGS_LAUNCHED();
     }
     // 9: blending

@@ -15,7 +15,7 @@ struct tdgs_ctx {
 
 namespace tdgs {
 
-constexpr int kCounters = 8;
+constexpr int kCounters = 12;
 // Frame monitor of device-count renders: [frames, largest M, frames whose keys did not fit,
 // last M], kept on the device after the counters (d_counters + kCounters) and copied to the
 // host (h_monitor) by every such frame.
@@ -28,9 +28,12 @@ constexpr uint32_t kErrSortCounts = 1u;   // radix-sort counts disagreed with th
 inline uint32_t* ctx_error_word(tdgs_ctx* ctx) { return reinterpret_cast<uint32_t*>(ctx->d_counters + kErrSlot); }
 
 // Other slots of ctx->d_counters: 0 filtered count N_f, 1 key count M, 2 ADC count, 4 count of
-// non-empty Gaussians; in a render with TDGS_FLAG_DEVICE_COUNTS, 5 the key count the key
-// passes use (M, or 0 when M does not fit the key arrays) and 6 the frame status.
-constexpr int kCntKeysUsed = 5, kCntStatus = 6;
+// non-empty Gaussians, 8 entries of the coarse blocks' lists (with M: see kLow32); in a render with
+// TDGS_FLAG_DEVICE_COUNTS, 5 the key count the frame uses (M, or 0 when M does not fit the key
+// arrays), 6 the frame status and 9 the coarse entries used (0 with 5).
+constexpr int kCntKeysUsed = 5, kCntStatus = 6, kCntCoarse = 8, kCntCoarseUsed = 9;
+// Slot kCntCoarse holds (M << 32) | coarse entries (one scan of packed counts).
+constexpr int64_t kLow32 = 0xffffffffll;
 // Frame status: the keys fit, M > key_capacity, M >= 2^31.
 constexpr int64_t kFrameOk = 0, kFrameKeyCapacity = 1, kFrameKeyRange = 2;
 // A device-count render leaves [N_f, M, non-empty count, status] in the first four int64 of

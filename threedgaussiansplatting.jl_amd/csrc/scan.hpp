@@ -1,4 +1,4 @@
-// scan.hpp — device-wide inclusive scan of int32 items with int64 running sums
+// scan.hpp — device-wide inclusive scan of int32 (or int64) items with int64 running sums
 // (replaces CUDA.jl's accumulate!(+) at src/forward_core.jl:231, 259 and
 // src/training.jl:384). Reduce-then-scan in three launches:
 //   1. each 2048-item tile reduces its items            (k_scan_reduce)
@@ -91,7 +91,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_apply(In in, Out out, int
                                                              const int64_t* tile_offsets, const int64_t* d_limit) {
     if (d_limit && (int64_t)blockIdx.x * kScanTile >= *d_limit) return;
     const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
-    int32_t v[kScanItems];
+    using Item = decltype(in(int64_t(0)));   // int32_t, or int64_t for two packed counts
+    Item v[kScanItems];
     int64_t acc = 0;
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
