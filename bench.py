@@ -105,9 +105,32 @@ def backward_evaluations(last, tiles_end, tiling):
     return int(torch.where(lst > 0, lst - beg, torch.zeros_like(lst)).sum().item())
 
 
+def bin_geometry(tiling):
+    """The coarse blocks of the tile lists (forward.hip bin_geom): log2 of the block size in tiles
+    (x, y), the smallest of 8x8, 16x8, 16x16 tiles that leaves at most 255 blocks."""
+    for sx, sy in ((3, 3), (4, 3), (4, 4)):
+        nbx, nby = -(-tiling.nb_tiles_x // (1 << sx)), -(-tiling.nb_tiles_y // (1 << sy))
+        if nbx * nby <= 255:
+            break
+    return sx, sy
+
+
+def coarse_entries(ranges, counts, tiling):
+    """M_c: (Gaussian, coarse block) pairs of the non-empty Gaussians (the binning's entries);
+    ranges holds each Gaussian's 1-based inclusive tile rectangle (x0, y0, x1, y1)."""
+    if tiling.nb_tiles > 65535:
+        return 0
+    sx, sy = bin_geometry(tiling)
+    r = ranges[counts > 0].astype(np.int64)
+    bx = ((r[:, 2] - 1) >> sx) - ((r[:, 0] - 1) >> sx) + 1
+    by = ((r[:, 3] - 1) >> sy) - ((r[:, 1] - 1) >> sy) + 1
+    return int(bx.dot(by))
+
+
 def frame_stats(core, g, cams, tiling, opts, buffers, idx):
-    """N_f, N_b, M, blending evaluations E_f (all, past the exponent cut, contributing) and the
-    backward walk's evaluations E_b, for the given cameras (untimed pass)."""
+    """N_f, N_b, M, blending evaluations E_f (all, past the exponent cut, contributing), the
+    backward walk's evaluations E_b and the binning's coarse entries M_c, for the given cameras
+    (untimed pass)."""
     import torch
     L = core.lib()
     outputs = core.RenderOutputs.for_camera(cams[0], 0, include_rgb=True, include_transmittance=True,
@@ -117,14 +140,16 @@ def frame_stats(core, g, cams, tiling, opts, buffers, idx):
     for k in idx:
         core.render_(outputs, g, cams[k], tiling, opts, buffers)
         nf = buffers.nb_fgaussians
-        nb = int((buffers.counts[:nf] > 0).sum().item())
+        counts = buffers.counts[:nf].cpu().numpy()
+        nb = int((counts > 0).sum())
+        mc = coarse_entries(buffers.tile_ranges[:nf].cpu().numpy(), counts, tiling)
         ev.zero_()
         core.check(L.tdgs_blend_evaluations(core.stream_ptr(0), C.byref(cams[k].to_c()), C.byref(tiling.to_c()),
                                             C.byref(opts.to_c()), C.byref(buffers.struct()),
                                             C.c_int64(buffers.nb_keys), C.c_void_p(ev.data_ptr())))
         e = ev.cpu().tolist()
         eb = backward_evaluations(outputs.last, buffers.tiles_end, tiling)
-        st.append((nf, nb, buffers.nb_keys, e[0], e[1], e[2], eb))
+        st.append((nf, nb, buffers.nb_keys, e[0], e[1], e[2], eb, mc))
     torch.cuda.synchronize()
     return np.array(st, dtype=np.float64)
 
@@ -346,23 +371,35 @@ def stress_cfg4(core, repeats=5):
     cnt = (C.c_int64 * 13)()
     core.check(L.tdgs_profile_end(ms, cnt))
     stage = {STAGES[i]: round(ms[i] / cnt[i], 4) for i in range(13) if cnt[i] > 0}
-    m = buf.nb_keys
-    # the tile sort's bytes as the metric prices them (two 8-bit passes of CUB over 24 bytes per
-    # key for the tile bits) and as this build moves them (two passes over 16-bit tile ids and
-    # 32-bit values, or 64-bit keys past 65535 tiles)
-    conv_gbs = 2 * 24 * m / (stage["tile_sort"] * 1e-3) / 1e9
-    impl_b = algorithmic_bytes("tile_sort", 0, 0, 0, m, 0, 0, 0) if tiling.nb_tiles <= 65535 else 2 * 24 * m + 8 * m
-    impl_gbs = impl_b / (stage["tile_sort"] * 1e-3) / 1e9
-    return {"workload": w.name, "keys": m, "filtered": buf.nb_fgaussians, "forward_ms": round(float(np.median(fw)), 3),
+    m, nf = buf.nb_keys, buf.nb_fgaussians
+    counts = buf.counts[:nf].cpu().numpy()
+    nb = int((counts > 0).sum())
+    mc = coarse_entries(buf.tile_ranges[:nf].cpu().numpy(), counts, tiling)
+    # the sort and ranges (the depth presort, the coarse sort and the binning) priced as the
+    # metric does (CUB's 8-bit LSD passes over the 64-bit keys, then the ranges) and as this
+    # build's kernels move them
+    t_sort = sum(stage.get(s_, 0.0) for s_ in ("depth_sort", "tile_sort", "tile_ranges"))
+    conv_b = 8 * m + 24 * m * math.ceil(tiling.end_bit() / 8) + 8 * m + 4 * tiling.nb_tiles
+    impl_b = sum(algorithmic_bytes(s_, len(g), nf, nb, m, 0, 16, tiling.nb_tiles, mc)
+                 for s_ in ("depth_sort", "tile_sort", "tile_ranges"))
+    gbs = lambda b: b / (t_sort * 1e-3) / 1e9
+    return {"workload": w.name, "keys": m, "filtered": nf, "nonempty": nb, "coarse_entries": mc,
+            "forward_ms": round(float(np.median(fw)), 3),
             "backward_ms": round(float(np.median(bw)), 3), "stage_ms": stage,
-            "tile_sort_convention_GBs": round(conv_gbs, 1), "tile_sort_convention_hbm_frac": round(conv_gbs / HBM_PEAK_GBS, 4),
-            "tile_sort_impl_bytes": int(impl_b), "tile_sort_impl_GBs": round(impl_gbs, 1),
-            "tile_sort_impl_hbm_frac": round(impl_gbs / HBM_PEAK_GBS, 4)}
+            "sort_ranges_ms": round(t_sort, 4),
+            "sort_ranges_convention_bytes": int(conv_b),
+            # the rate a 64-bit key sort would need to finish in the same time (above the HBM
+            # peak here: the binning moves far fewer bytes than a sort of the M keys)
+            "sort_ranges_convention_equivalent_GBs": round(gbs(conv_b), 1),
+            "sort_ranges_impl_bytes": int(impl_b), "sort_ranges_impl_GBs": round(gbs(impl_b), 1),
+            "sort_ranges_impl_hbm_frac": round(gbs(impl_b) / HBM_PEAK_GBS, 4)}
 
 
-def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles):
+def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles, mc=0):
     """Bytes one launch of a stage moves as this build's kernels do it (per frame averages),
-    each input read once and each output written once."""
+    each input read once and each output written once. With at most 65535 tiles the tile lists
+    come from coarse binning over mc (Gaussian, block) entries: emit counts the block ids,
+    tile_sort is their one radix pass, tile_ranges the lists themselves (count, scan, write)."""
     if stage == "cull_compact":          # keep test: means + opacity in; per-block counts out
         return 16 * n
     if stage == "project":               # parameters of every Gaussian, SH of the non-empty ones;
@@ -372,16 +409,16 @@ def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles):
     if stage == "depth_sort":            # first pass over all N depth keys (count + scatter of the
         # kept), three more over the N_b non-empty ones: count 4, scatter 8 in + 8 out
         return 4 * n + 8 * n + 8 * nb + 3 * (4 + 16) * nb
-    if stage == "count_scan":            # sorted fgidx + their counts in, scan out (reduce + apply)
-        return 2 * (4 + 4) * nb + 4 * nb
-    if stage == "emit":                  # scan, fgidx, rectangle of the non-empty in; 16-bit tile id
-        # and value per key out
-        return 24 * nb + 6 * m
-    if stage == "tile_sort":             # two passes over (16-bit tile id, value): scatter 6 in + 6 out
-        # each, the second pass's count 2 in (the first pass's counts come from emission)
-        return 12 * m + 2 * m + 12 * m
-    if stage == "tile_ranges":
-        return 2 * m + 4 * ntiles
+    if stage == "count_scan":            # sorted fgidx, their counts and rectangles in (reduce +
+        # apply: tiles and blocks per Gaussian), packed scan out
+        return 2 * (4 + 4 + 16) * nb + 8 * nb
+    if stage == "emit":                  # scan, fgidx, rectangle of the non-empty in (block ids counted)
+        return (8 + 4 + 16) * nb
+    if stage == "tile_sort":             # the same in again; (16-bit block id, 32-bit value) per entry out
+        return (8 + 4 + 16) * nb + 6 * mc
+    if stage == "tile_ranges":           # block ends (ids in); count and write passes read value +
+        # rectangle per entry; per-(segment, tile) counts scanned; the M list entries out
+        return 2 * mc + 2 * (4 + 16) * mc + 8 * ntiles + 4 * m
     if stage == "blend":                 # metric's K5: 40 per key, 20 per pixel
         return 40 * m + 20 * npx
     return None
@@ -401,8 +438,9 @@ def measured_traffic():
 # the counter-summary kernels of each survey row (sums of their per-launch bytes)
 MEASURED_KERNELS = {
     "K1_project": ["keep_counts", "project"],
-    "K3_sort": ["depth_sort_count", "depth_sort_scatter", "tile_sort_count", "tile_sort_scatter"],
-    "K4_ranges": ["tile_ranges"],
+    "K2_scan_keys": ["count_scan_reduce", "count_scan_apply", "emit_count"],
+    "K3_K4_sort_ranges": ["depth_sort_count", "depth_sort_scatter", "coarse_sort_scatter", "block_ends",
+                          "bin_count", "bin_scan", "bin_write"],
     "K5_blend": ["blend"],
     "K6_backward_blend": ["backward_blend"],
     "K7_backward_project": ["backward_project"],
@@ -411,11 +449,13 @@ MEASURED_KERNELS = {
 }
 
 
-def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit, e_f, e_b):
+def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit, e_f, e_b, mc=0):
     """Per-kernel roofline fractions. `bytes` follow the metric's accounting (K1 = cull,
     compaction and projection: 16 N + (28 + 12h) N_f read, 8 N_f + 56 N_b written; K2 = count
-    scan and key emission: 8 N_f + 24 N_b + 12 M; K3 = the sort, priced as CUB's 8-bit-digit LSD
-    sort of the 64-bit keys: 8 M + 24 M ceil(end_bit / 8); K4 = ranges: 8 M + 4 T; K5 = blend:
+    scan and key emission: 8 N_f + 24 N_b + 12 M; K3 + K4 = the sort, priced as CUB's 8-bit-digit
+    LSD sort of the 64-bit keys: 8 M + 24 M ceil(end_bit / 8), and the ranges: 8 M + 4 T, whose
+    results this build obtains together from the depth presort and the coarse binning (stages
+    depth_sort, tile_sort, tile_ranges; reported as one row, K3_K4); K5 = blend:
     40 M + 20 P, FLOP 20 E_f + E_f exponentials; K6 = backward blend: 40 M + 20 P + 36 A with A the
     per-(tile, Gaussian) atomic flushes (<= M), FLOP 60 E_b; K7 = backward projection
     (160 + 24h) N_f; K8 = Adam 28 (11 + 3h) N_f + 4 N_f; K7_K8_fused = the trainer's fused launch,
@@ -428,8 +468,8 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit,
     rows = {
         "K1_project": (16 * n + (28 + 12 * h) * nf + 8 * nf + 56 * nb, ["cull_compact", "project"], stage_ms, None),
         "K2_scan_keys": (8 * nf + 24 * nb + 12 * m, ["count_scan", "emit"], stage_ms, None),
-        "K3_sort": (8 * m + 24 * m * math.ceil(end_bit / 8), ["depth_sort", "tile_sort"], stage_ms, None),
-        "K4_ranges": (8 * m + 4 * ntiles, ["tile_ranges"], stage_ms, None),
+        "K3_K4_sort_ranges": (8 * m + 24 * m * math.ceil(end_bit / 8) + 8 * m + 4 * ntiles,
+                              ["depth_sort", "tile_sort", "tile_ranges"], stage_ms, None),
         "K5_blend": (40 * m + 20 * npx, ["blend"], stage_ms, (BLEND_FLOP_PER_EVAL + BLEND_EXP_PER_EVAL) * e_f),
     }
     if train_stage:
@@ -440,7 +480,7 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit,
         rows["K8_adam"] = (k8, ["adam"], sep, None)
         if "adam" not in train_stage:   # the trainer's fused launch
             rows["K7_K8_fused"] = (k7 + k8 - 2 * 4 * g3 * nf, ["backward_project"], train_stage, None)
-    impl = {s_: algorithmic_bytes(s_, n, nf, nb, m, npx, h, ntiles) for s_ in stage_ms}
+    impl = {s_: algorithmic_bytes(s_, n, nf, nb, m, npx, h, ntiles, mc) for s_ in stage_ms}
     measured = measured_traffic()
     out = {}
     for k, (b, stages, src, flop) in rows.items():
@@ -574,17 +614,17 @@ def main():
 
     st = frame_stats(core, g, cams, tiling, opts, buf, used)
     n = len(g)
-    nf, nb, m, evals, evals_live, evals_contrib, evals_back = st.mean(axis=0)
+    nf, nb, m, evals, evals_live, evals_contrib, evals_back, mc = st.mean(axis=0)
     npx = cam0.width * cam0.height
     h = (deg + 1) ** 2
     stage_ms = {STAGES[i]: ms[i] / cnt[i] for i in range(13) if cnt[i] > 0}
     dom = max(stage_ms, key=stage_ms.get)
     stage_gbs = {}
     for s_, t_ in stage_ms.items():
-        b = algorithmic_bytes(s_, n, nf, nb, m, npx, h, tiling.nb_tiles)
+        b = algorithmic_bytes(s_, n, nf, nb, m, npx, h, tiling.nb_tiles, mc)
         if b is not None:
             stage_gbs[s_] = b / (t_ * 1e-3) / 1e9
-    b_dom = algorithmic_bytes(dom, n, nf, nb, m, npx, h, tiling.nb_tiles)
+    b_dom = algorithmic_bytes(dom, n, nf, nb, m, npx, h, tiling.nb_tiles, mc)
     achieved = b_dom / (stage_ms[dom] * 1e-3) / 1e9
     roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
@@ -646,13 +686,13 @@ def main():
         "mean_counts": {"filtered": round(nf), "nonempty": round(nb), "keys": round(m),
                         "blend_evaluations": round(evals), "blend_evaluations_live": round(evals_live),
                         "blend_evaluations_contributing": round(evals_contrib),
-                        "backward_blend_evaluations": round(evals_back)},
+                        "backward_blend_evaluations": round(evals_back), "coarse_entries": round(mc)},
         "train": train,
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
         "stage_algorithmic_GBs": {k: round(v, 1) for k, v in stage_gbs.items()},
         "roofline": roofline,
         "survey_kernels": survey_kernels(stage_ms, train["stage_ms"] if train else None, n, nf, nb, m, npx, h,
-                                         tiling.nb_tiles, tiling.end_bit(), evals, evals_back),
+                                         tiling.nb_tiles, tiling.end_bit(), evals, evals_back, mc),
         "cpu_baseline": cpu,
         "extra_configs": extra,
     }

@@ -863,10 +863,14 @@ struct BinArgs {
 // its tiles with one ballot.
 constexpr int kBinPer = 4;   // candidates each thread stages per chunk (their loads in flight together)
 
+// (Staging the writes in LDS rings and storing 64 entries at a time measured no faster: the
+// kernel is bound by its per-(tile, batch) instruction stream, not by the partial stores.)
+// LDS (dynamic): the chunk's candidates, 2 kBinPer words per thread.
 template <int SX, bool WRITE>
 __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
-    __shared__ int32_t s_f[1024 * kBinPer];
-    __shared__ uint32_t s_m[1024 * kBinPer];
+    extern __shared__ uint32_t s_dyn[];
+    int32_t* const s_f = reinterpret_cast<int32_t*>(s_dyn);
+    uint32_t* const s_m = s_dyn + blockDim.x * kBinPer;
     constexpr int BW = 1 << SX;
     const int BH = 1 << a.sy;
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
@@ -1739,14 +1743,15 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     ba.out = buf->sorted_values; ba.cap = (int32_t)(kc < INT32_MAX ? kc : INT32_MAX); ba.err = d_err;
     const unsigned bthreads = 4u << (bg.sx + bg.sy);
     const unsigned bgrid = (unsigned)(nblocks * segs);
-    if (bg.sx == 3) k_bin_tiles<3, false><<<bgrid, bthreads, 0, s>>>(ba);
-    else k_bin_tiles<4, false><<<bgrid, bthreads, 0, s>>>(ba);
+    const size_t lds = (size_t)bthreads * kBinPer * 2 * sizeof(uint32_t);
+    if (bg.sx == 3) k_bin_tiles<3, false><<<bgrid, bthreads, lds, s>>>(ba);
+    else k_bin_tiles<4, false><<<bgrid, bthreads, lds, s>>>(ba);
     TDGS_LAUNCHED();
     k_bin_scan<<<1, 1024, 0, s>>>(r.tile_totals, tiling->nb_tiles_x * tiling->nb_tiles_y, buf->tiles_end,
                                   dc ? dc + kCntKeysUsed : nullptr, m, d_err);
     TDGS_LAUNCHED();
-    if (bg.sx == 3) k_bin_tiles<3, true><<<bgrid, bthreads, 0, s>>>(ba);
-    else k_bin_tiles<4, true><<<bgrid, bthreads, 0, s>>>(ba);
+    if (bg.sx == 3) k_bin_tiles<3, true><<<bgrid, bthreads, lds, s>>>(ba);
+    else k_bin_tiles<4, true><<<bgrid, bthreads, lds, s>>>(ba);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
