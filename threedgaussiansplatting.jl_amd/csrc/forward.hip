@@ -342,14 +342,14 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
 // Key duplication
 // ------------------------------------------------------------------------------------
 
-// Overlap counts of the non-empty Gaussians in depth order (entries past N_b count 0).
+// Overlap counts of the non-empty Gaussians in depth order (entries past N_b count 0): the
+// areas of their tile rectangles, which the depth sort's last pass gathered into depth order
+// (srect: contiguous reads here instead of a gather per reader).
+__device__ __forceinline__ int32_t rect_area(const int4 r) { return (r.z - r.x + 1) * (r.w - r.y + 1); }
 struct SortedCounts {
-    const int32_t* sorted_f;
-    const int32_t* counts;
+    const int4* srect;
     const int64_t* d_nb;
-    __device__ int32_t operator()(int64_t j) const {
-        return j < *d_nb ? counts[sorted_f[j] - 1] : 0;
-    }
+    __device__ int32_t operator()(int64_t j) const { return j < *d_nb ? rect_area(srect[j]) : 0; }
 };
 
 // The inclusive scan of the tile counts in depth order, and for every emission block (keys
@@ -424,7 +424,7 @@ __device__ __forceinline__ int emit_slot(int k) {
 template <int THREADS, int ITEMS>
 __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t block, const int32_t* __restrict__ sorted_f,
                                               const int32_t* __restrict__ cs, const int32_t* __restrict__ blk_first,
-                                              const int32_t* __restrict__ ranges, EmitGrid grid, int32_t* s_buf,
+                                              const int4* __restrict__ srect, EmitGrid grid, int32_t* s_buf,
                                               int64_t* s_range, int32_t (&tile)[ITEMS], int32_t (&val)[ITEMS]) {
     constexpr int kBlock = THREADS * ITEMS;
     static_assert(kBlock == kEmitTile, "emission blocks of kEmitTile keys");
@@ -462,10 +462,8 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
             const int64_t j = j_lo + k - 1;
             s_cs[k] = j < 0 ? 0 : cs[j];
             if (full && k < cnt) {
-                const int32_t f = sorted_f[j + 1];
-                const int4 r = reinterpret_cast<const int4*>(ranges)[f - 1];
-                s_f[k] = f;
-                grid.rect(r, &s_t0[k], &s_wx[k]);
+                s_f[k] = sorted_f[j + 1];
+                grid.rect(srect[j + 1], &s_t0[k], &s_wx[k]);
             }
         }
     }
@@ -490,7 +488,7 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
                 f = s_f[k]; t0 = s_t0[k]; wx = s_wx[k];
             } else {
                 f = sorted_f[j_lo + k];
-                grid.rect(reinterpret_cast<const int4*>(ranges)[f - 1], &t0, &wx);
+                grid.rect(srect[j_lo + k], &t0, &wx);
             }
         };
         load(lo);
@@ -523,7 +521,7 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
 template <bool TILE16>
 __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
-    const int32_t* __restrict__ blk_first, const float* __restrict__ depths, const int32_t* __restrict__ ranges,
+    const int32_t* __restrict__ blk_first, const float* __restrict__ depths, const int4* __restrict__ srect,
     EmitGrid grid, void* __restrict__ keys_out, int32_t* __restrict__ vals, int nbits0,
     uint32_t* __restrict__ counts0, int64_t count_tiles) {
     __shared__ int32_t s_buf[kEmitTile + 1];
@@ -533,7 +531,7 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
     s_h[t] = 0;
     const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
     int32_t tile[kEmitItems], val[kEmitItems];
-    emit_generate<kEmitThreads, kEmitItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, grid, s_buf, s_range,
+    emit_generate<kEmitThreads, kEmitItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, srect, grid, s_buf, s_range,
                                             tile, val);
     // values, then tile ids (or keys), through LDS to coalesced stores
     const int64_t nk = m - d0 < kEmitTile ? m - d0 : kEmitTile;
@@ -584,7 +582,7 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
                                                                  const int32_t* __restrict__ sorted_f,
                                                                  const int32_t* __restrict__ cs,
                                                                  const int32_t* __restrict__ blk_first,
-                                                                 const int32_t* __restrict__ ranges, EmitGrid grid,
+                                                                 const int4* __restrict__ srect, EmitGrid grid,
                                                                  int nbits0, uint32_t* __restrict__ counts0,
                                                                  int64_t count_tiles, int64_t* dc, int64_t key_cap) {
     __shared__ int32_t s_buf[kEmitTile + 1];
@@ -612,7 +610,7 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
     }
     if (t < kRsBins) s_h[t] = 0;
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
-    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, grid, s_buf,
+    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, srect, grid, s_buf,
                                                     s_range, tile, val);
     const int64_t first = (int64_t)blockIdx.x * kEmitTile + (int64_t)t * kEmitSortItems;
     const uint32_t mask0 = (1u << nbits0) - 1u;
@@ -633,7 +631,7 @@ __device__ __forceinline__ int emit_sort_slot(int k) {
 
 __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
-    const int32_t* __restrict__ blk_first, const int32_t* __restrict__ ranges, EmitGrid grid, int nbits0,
+    const int32_t* __restrict__ blk_first, const int4* __restrict__ srect, EmitGrid grid, int nbits0,
     const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, int64_t count_tiles,
     uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err, const int64_t* dc) {
     __shared__ int32_t s_buf[kEmitTile + 1];
@@ -646,7 +644,7 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
         if (d0 >= m) return;
     }
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
-    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, ranges, grid, s_buf,
+    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, srect, grid, s_buf,
                                                     s_range, tile, val);
     uint16_t key[kEmitSortItems];
     int32_t v[kEmitSortItems];
@@ -811,18 +809,15 @@ static BinGeom bin_geom(const tdgs_tiling* t) {
 // offsets in the low half and, in its total, the key count M in the high half (both below
 // 2^31, so the halves never carry into each other).
 struct SortedTileBlockCounts {
-    const int32_t* sorted_f;
-    const int32_t* counts;
-    const int32_t* ranges;
+    const int4* srect;   // rectangles in depth order
     int sx, sy;
     const int64_t* d_nb;
     __device__ int64_t operator()(int64_t j) const {
         if (j >= *d_nb) return 0;
-        const int32_t f = sorted_f[j] - 1;
-        const int4 r = reinterpret_cast<const int4*>(ranges)[f];
+        const int4 r = srect[j];
         const int32_t blocks =
             (((r.z - 1) >> sx) - ((r.x - 1) >> sx) + 1) * (((r.w - 1) >> sy) - ((r.y - 1) >> sy) + 1);
-        return ((int64_t)counts[f] << 32) | (int64_t)blocks;
+        return ((int64_t)rect_area(r) << 32) | (int64_t)blocks;
     }
 };
 // WriteScanAndBlocks on the blocks' half of the packed scan.
@@ -1573,6 +1568,7 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(t ? (int64_t)kBinMaxSegs * t->nb_tiles_x * t->nb_tiles_y : 0);   // per (segment, tile)
     ar.template take<int32_t>(t ? bin_geom(t).nblocks() : 0);                    // ends of the blocks' lists
     ar.template take<int32_t>(t ? ((int64_t)t->nb_tiles_x * t->nb_tiles_y + 3) / 4 * 4 : 0);   // tiles' totals
+    ar.template take<int4>(cap);                                                  // rectangles in depth order
 }
 
 // The scratch arrays of tdgs_render / tdgs_project inside buf->temp (render_layout's order).
@@ -1592,6 +1588,7 @@ struct RenderScratch {
     int32_t* block_end;
     int32_t* tile_totals;
     int64_t ntt;   // entries of tile_totals (tiles, padded to 4)
+    int4* srect;   // tile rectangles of the non-empty Gaussians in depth order
 };
 
 static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const tdgs_tiling* tiling) {
@@ -1621,6 +1618,7 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.block_end = ar.take<int32_t>(tiling ? bin_geom(tiling).nblocks() : 0);
     r.ntt = tiling ? ((int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y + 3) / 4 * 4 : 0;
     r.tile_totals = ar.take<int32_t>(r.ntt);
+    r.srect = ar.take<int4>(cap);
     return r;
 }
 
@@ -1708,7 +1706,7 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     const int64_t* d_used = dc ? dc + kCntCoarseUsed : nullptr;
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
-        k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges, cg,
+        k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg,
                                                         nbits0, table, count_tiles, dc, kc);
         TDGS_LAUNCHED();
     }
@@ -1716,7 +1714,7 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
         k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals);
         TDGS_LAUNCHED();
-        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, buf->tile_ranges,
+        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
                                                           cg, nbits0, table, totals, count_tiles,
                                                           one_pass ? c16 : c16_alt,
                                                           one_pass ? buf->values : buf->sorted_values, d_err, dc);
@@ -1987,7 +1985,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     {
         StageScope sc(TDGS_STAGE_DEPTH_SORT, s);
         TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
-                                            rtemp, rbytes, s, nullptr, d_err, d_nb));
+                                            rtemp, rbytes, s, nullptr, d_err, d_nb, nullptr,
+                                            RsGather{reinterpret_cast<const int4*>(buf->tile_ranges), r.srect}));
     }
     if (tile16) {
         // 5: tiles and blocks touched, in depth order -> the blocks' entries (emission offsets)
@@ -1995,7 +1994,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         const BinGeom bg = bin_geom(tiling);
         {
             StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
-            const SortedTileBlockCounts stb{sorted_f, buf->counts, buf->tile_ranges, bg.sx, bg.sy, d_nb};
+            const SortedTileBlockCounts stb{r.srect, bg.sx, bg.sy, d_nb};
             TDGS_TRY(device_scan(stb, stb, WriteBlockScan{WriteScanAndBlocks{cs, blk_first, nblk}}, n, stemp, sbytes,
                                  ctx->d_counters + kCntCoarse, s, d_nb));
         }
@@ -2034,8 +2033,8 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     // 5: tile counts in depth order -> M
     {
         StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
-        TDGS_TRY(device_scan(SortedCounts{sorted_f, buf->counts, d_nb},
-                             SortedCounts{sorted_f, buf->counts, d_nb}, WriteScanAndBlocks{cs, blk_first, nblk}, n, stemp,
+        TDGS_TRY(device_scan(SortedCounts{r.srect, d_nb}, SortedCounts{r.srect, d_nb},
+                             WriteScanAndBlocks{cs, blk_first, nblk}, n, stemp,
                              sbytes, d_m, s, d_nb));
     }
     TDGS_TRY(read_counters(ctx, s));
@@ -2070,7 +2069,7 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
         {
             StageScope sc(TDGS_STAGE_EMIT, s);
             k_emit_depth_order<false><<<egrid, kEmitThreads, 0, s>>>(nb, m, sorted_f, cs, blk_first, buf->depths,
-                                                                    buf->tile_ranges, EmitGrid{tiling->nb_tiles_x, 0, 0},
+                                                                    r.srect, EmitGrid{tiling->nb_tiles_x, 0, 0},
                                                                     ek, ev2, nbits0, radix_count_table(rtemp),
                                                                     count_tiles);
             TDGS_LAUNCHED();

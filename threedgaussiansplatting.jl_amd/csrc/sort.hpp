@@ -186,14 +186,20 @@ static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restric
 // 64-bit for 64-bit keys), and writes keys and values out as contiguous per-digit runs at
 // totals-prefix[d] + offsets[d][tile] + rank. `n` bounds the output index (an inconsistent
 // count sets *err instead of writing out of bounds). When d_kept is not null, tile 0 writes
-// the number of keys sorted in all.
+// the number of keys sorted in all. When gather.src is not null, each written value v (a
+// 1-based index) also moves gather.src[v - 1] to gather.dst at the value's output index.
+struct RsGather {
+    const int4* src;
+    int4* dst;
+};
+
 template <class K>
 __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems], const int32_t (&val)[RsTile<K>::kItems],
                                                 const bool (&valid)[RsTile<K>::kItems], int64_t tile, int64_t n,
                                                 int shift, int nbits, const uint32_t* __restrict__ offsets,
                                                 const uint32_t* __restrict__ totals, int64_t tiles,
                                                 K* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err,
-                                                int64_t* d_kept, uint32_t* s_raw) {
+                                                int64_t* d_kept, uint32_t* s_raw, RsGather gather = {nullptr, nullptr}) {
     constexpr int kRsItems = RsTile<K>::kItems;
     constexpr int kRsTile = RsTile<K>::kTile;
     // Keys narrower than 32 bits are staged as 32-bit words: lanes storing 16-bit keys to
@@ -288,7 +294,11 @@ __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
         const int i = k * kRsThreads + t;
-        if (opos[k] >= 0) vout[opos[k]] = s_val[i];
+        if (opos[k] >= 0) {
+            const int32_t v = s_val[i];
+            vout[opos[k]] = v;
+            if (gather.src) gather.dst[opos[k]] = gather.src[v - 1];
+        }
     }
 }
 
@@ -303,7 +313,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     const K* __restrict__ kin, const int32_t* __restrict__ vin, K* __restrict__ kout,
     int32_t* __restrict__ vout, int64_t n, int shift, int nbits, const uint32_t* __restrict__ offsets,
     const uint32_t* __restrict__ totals, int64_t tiles, uint32_t* err, const int64_t* d_n, int drop_max,
-    int64_t* d_kept) {
+    int64_t* d_kept, RsGather gather) {
     constexpr int kRsItems = RsTile<K>::kItems;
     constexpr int kRsTile = RsTile<K>::kTile;
     __shared__ uint32_t s_raw[rs_stage_words<K>()];
@@ -325,7 +335,7 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) valid[k] = wbase + k * kWave < nn && !(drop_max && key[k] == (K)~(K)0);
     rs_scatter_tile<K>(key, val, valid, tile, n, shift, nbits, offsets, totals, tiles, kout, vout, err,
-                       drop_max ? d_kept : nullptr, s_raw);
+                       drop_max ? d_kept : nullptr, s_raw, gather);
 }
 
 inline int radix_passes(int begin_bit, int end_bit) {
@@ -377,11 +387,16 @@ inline size_t radix_temp_bytes(int64_t n) {
 //
 // d_count (device word, may be null; not with kept_out) holds the number of pairs to sort,
 // min(*d_count, n): n only sizes the launches, so the host needs no synchronisation.
+//
+// gather (src may be null): the last pass also writes gather.dst[i] = gather.src[vout[i] - 1]
+// for every output i (the values are 1-based indices into src), so per-value data comes out
+// in sorted order from one gather instead of one per later reader.
 template <class K>
 int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K* alt_k,
                      int32_t* alt_v, int64_t n, int begin_bit, int end_bit, void* temp,
                      size_t temp_bytes, hipStream_t stream, uint32_t* first_counts = nullptr,
-                     uint32_t* err = nullptr, int64_t* kept_out = nullptr, const int64_t* d_count = nullptr) {
+                     uint32_t* err = nullptr, int64_t* kept_out = nullptr, const int64_t* d_count = nullptr,
+                     RsGather gather = {nullptr, nullptr}) {
     const int passes = radix_passes(begin_bit, end_bit);
     const int width = radix_digit_bits(begin_bit, end_bit);
     if (n <= 0) return TDGS_OK;
@@ -390,8 +405,8 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
         return TDGS_ERR_INVALID;
     }
     if (passes == 0) {
-        if (kept_out || d_count) {
-            set_error("radix sort: dropping keys or a device count needs at least one pass");
+        if (kept_out || d_count || gather.src) {
+            set_error("radix sort: dropping keys, a device count or a gather needs at least one pass");
             return TDGS_ERR_INVALID;
         }
         if (kout != kin) TDGS_HIP(hipMemcpyAsync(kout, kin, n * sizeof(K), hipMemcpyDeviceToDevice, stream));
@@ -431,7 +446,8 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
         TDGS_LAUNCHED();
         k_rs_scatter<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, src_v, dk, dv, n, shift, nbits, table,
                                                                      totals, tiles, err, d_n, drop,
-                                                                     drop ? kept_out : nullptr);
+                                                                     drop ? kept_out : nullptr,
+                                                                     p == passes - 1 ? gather : RsGather{nullptr, nullptr});
         TDGS_LAUNCHED();
         src_k = dk;
         src_v = dv;
