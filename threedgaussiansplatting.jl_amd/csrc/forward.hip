@@ -790,6 +790,7 @@ struct BinGeom {
     int sx, sy;
     int32_t nbx, nby;
     int32_t nblocks() const { return nbx * nby; }
+    int tpb() const { return 1 << (sx + sy); }   // tiles per block
 };
 static BinGeom bin_geom(const tdgs_tiling* t) {
     const int shapes[3][2] = {{3, 3}, {4, 3}, {4, 4}};
@@ -828,22 +829,31 @@ struct WriteBlockScan {
     }
 };
 
-// Each block's list is cut into `segs` consecutive segments, one workgroup each (more
-// workgroups in flight; the counts and offsets are per (segment, tile)).
-constexpr int kBinMaxSegs = 16;
-inline int bin_segments(int32_t nblocks) {
-    const int s = 1024 / (nblocks > 0 ? nblocks : 1);
-    return s < 1 ? 1 : s > kBinMaxSegs ? kBinMaxSegs : s;
+// Work is dealt in chunks of the coarse list, not per block, so that every workgroup gets the
+// same number of entries however unevenly the Gaussians spread over the blocks: chunk k is
+// entries [k E, (k + 1) E) of the lists of all blocks one after the other (E = the
+// workgroup's threads x kBinPer). A chunk that straddles block boundaries is processed as one
+// segment per block; segment (k, b) has the unique index k + b (both grow along the list), and
+// its per-tile counts are table[(k + b) tpb + local tile] (tpb = tiles per block).
+constexpr int kBinPer = 2;   // candidates each thread stages per chunk (their loads in flight together)
+constexpr int kBinMaxGrid = 2048;   // workgroups of a launch (a grid-stride loop covers the rest)
+
+// Entries of the segment count table for key capacity kc (the coarse entries never exceed
+// the keys: each Gaussian touches at least one tile of every block it is listed in): at most
+// 4 / (4 kBinPer) bytes per key. (Chunks of 2 entries per thread measured 70 -> 66 us for the
+// tile lists at 1M Gaussians, 1080p; 1 per thread 63 us, but twice the table.)
+inline int64_t bin_table_entries(int64_t kc, int32_t nblocks, int tpb) {
+    return (ceil_div(kc > 0 ? kc : 1, (int64_t)tpb * 4 * kBinPer) + nblocks + 1) * tpb;
 }
 
 struct BinArgs {
-    int32_t ntx, nty, nbx, sy, nblocks, segs;
+    int32_t ntx, nty, nbx, sy, nblocks;
     const int32_t* cvals;      // the blocks' lists: fgidx (1-based), block by block, depth order within
-    const int32_t* cend;       // inclusive end of each block's run in cvals
+    const int32_t* cend;       // end (exclusive) of each block's run in cvals
     int64_t mc;                // entries of cvals (launch bound)
     const int64_t* dmc;        // entries used (device counts), or null
     const int32_t* ranges;     // tile rectangles [x0, y0, x1, y1] (1-based, inclusive) by fgidx
-    int32_t* tile_counts;      // [tiles][segs]: COUNT writes the Gaussians of the segment covering each tile
+    int32_t* table;            // COUNT writes the Gaussians of each segment covering each tile
     int32_t* tile_totals;      // COUNT adds them up per tile (zeroed beforehand)
     const int32_t* tiles_end;  // WRITE: inclusive ends of the tiles' lists
     int32_t* out;              // WRITE: sdfgidx_to_fgidx
@@ -851,114 +861,144 @@ struct BinArgs {
     uint32_t* err;
 };
 
-// Workgroup: one segment of one block of 2^SX x 2^sy tiles, 4 threads per tile; wavefront w
-// takes the block's tiles 16 w .. 16 w + 15 (row-major, 2^SX per row). The segment's Gaussians
-// go through LDS in chunks of kBinPer per thread, as the tile rectangle clipped to the block in
-// two bit masks (columns, rows); a wavefront then tests 64 of them at a time against each of
-// its tiles with one ballot.
-constexpr int kBinPer = 4;   // candidates each thread stages per chunk (their loads in flight together)
-
-// (Staging the writes in LDS rings and storing 64 entries at a time measured no faster: the
-// kernel is bound by its per-(tile, batch) instruction stream, not by the partial stores.)
+// Workgroup: 4 threads per tile of a block of 2^SX x 2^sy tiles; wavefront w takes the
+// block's tiles 16 w .. 16 w + 15 (row-major, 2^SX per row). A segment's Gaussians go
+// through LDS, kBinPer per thread, as the tile rectangle clipped to the block in two bit
+// masks (columns, rows); a wavefront then tests 64 of them at a time against each of its
+// tiles with one ballot. COUNT counts the hits of each (segment, tile); WRITE writes each
+// hit at the tile's list start + the earlier segments' hits + the hits before it.
+// (Staging the writes in LDS rings and storing 64 entries at a time measured no faster.)
 // LDS (dynamic): the chunk's candidates, 2 kBinPer words per thread.
 template <int SX, bool WRITE>
 __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
     extern __shared__ uint32_t s_dyn[];
+    __shared__ int32_t s_cend[1024];   // the blocks' ends, when there are at most 1024 blocks
+    __shared__ int32_t s_b[2];
     int32_t* const s_f = reinterpret_cast<int32_t*>(s_dyn);
     uint32_t* const s_m = s_dyn + blockDim.x * kBinPer;
     constexpr int BW = 1 << SX;
     const int BH = 1 << a.sy;
+    const int tpb = BW * BH;
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
-    const int nt = (int)blockDim.x * kBinPer;   // candidates per chunk
-    const int b = blockIdx.x % a.nblocks, seg = blockIdx.x / a.nblocks;
-    const int bx = b % a.nbx, by = b / a.nbx;
-    const int x0b = bx * BW, y0b = by * BH;   // 0-based first tile of the block
+    const int nt = (int)blockDim.x * kBinPer;   // entries per chunk
     int64_t mc = a.mc;
     if (a.dmc && *a.dmc < mc) mc = *a.dmc;
-    int64_t ce = a.cend[b], cb = b == 0 ? 0 : a.cend[b - 1];
-    if (ce > mc) ce = mc;
-    if (cb > ce) cb = ce;
-    {   // the segment
-        const int64_t len = ce - cb;
-        ce = cb + len * (seg + 1) / a.segs;
-        cb = cb + len * seg / a.segs;
-    }
-    int32_t* const seg_counts = a.tile_counts + seg;   // entry of tile t: seg_counts[t segs]
+    const int64_t nchunks = (mc + nt - 1) / nt;
+    if ((int64_t)blockIdx.x >= nchunks) return;
+    const bool lds_ends = a.nblocks <= 1024;
+    if (lds_ends)
+        for (int i = t; i < a.nblocks; i += blockDim.x) s_cend[i] = a.cend[i];
+    auto end_of = [&](int i) -> int64_t {
+        const int64_t e = lds_ends ? s_cend[i] : a.cend[i];
+        return e < mc ? e : mc;
+    };
+    const int li = 16 * w + lane;     // lanes < 16: the tile this lane reports (local index)
     const int ly0 = (16 * w) >> SX;   // the wavefront's first local row
-    int32_t cnt[16];                  // COUNT: hits so far; WRITE: the next output index
-    int32_t start = 0;
-    if (WRITE) {
-        // lane i < 16: tile i's list start plus the earlier segments' Gaussians in it (all the
-        // loads in flight at once)
-        const int x = x0b + ((16 * w + lane) & (BW - 1)), y = y0b + ((16 * w + lane) >> SX);
-        if (lane < 16 && x < a.ntx && y < a.nty) {
-            const int tile = x + y * a.ntx;
-            int32_t c[kBinMaxSegs];
-#pragma unroll
-            for (int q = 0; q < kBinMaxSegs; ++q) c[q] = q < seg ? a.tile_counts[(int64_t)tile * a.segs + q] : 0;
-            start = tile > 0 ? a.tiles_end[tile - 1] : 0;
-#pragma unroll
-            for (int q = 0; q < kBinMaxSegs; ++q) start += c[q];
+    for (int64_t k = blockIdx.x; k < nchunks; k += gridDim.x) {
+        const int64_t lo = k * nt, hi = lo + nt < mc ? lo + nt : mc;
+        // the blocks holding entries lo and hi - 1 (the ends never decrease): counts of the
+        // blocks ending at or before lo, and before hi
+        if (t == 0) s_b[0] = s_b[1] = 0;
+        __syncthreads();
+        int c0 = 0, c1 = 0;
+        for (int i = t; i < a.nblocks; i += blockDim.x) {
+            const int64_t e = end_of(i);
+            c0 += e <= lo;
+            c1 += e < hi;
         }
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) cnt[i] = WRITE ? __builtin_amdgcn_readlane(start, i) : 0;
-    for (int64_t base = cb; base < ce; base += nt) {
-        // candidates base + t + blockDim q (q < kBinPer): the loads of each stage issue together
-        int32_t f[kBinPer];
-#pragma unroll
-        for (int q = 0; q < kBinPer; ++q) {
-            const int64_t k = base + t + (int64_t)blockDim.x * q;
-            f[q] = k < ce ? a.cvals[k] : 0;
+        for (int d = kWave / 2; d >= 1; d >>= 1) {
+            c0 += __shfl_xor(c0, d);
+            c1 += __shfl_xor(c1, d);
         }
-        int4 r[kBinPer];
-#pragma unroll
-        for (int q = 0; q < kBinPer; ++q)
-            r[q] = f[q] > 0 ? reinterpret_cast<const int4*>(a.ranges)[f[q] - 1] : make_int4(1, 1, 0, 0);
-#pragma unroll
-        for (int q = 0; q < kBinPer; ++q) {
-            // columns in bits 0-15, rows in bits 16-31 (of the block); none for an empty slot
-            const int cx0 = max(r[q].x - 1 - x0b, 0), cx1 = min(r[q].z - 1 - x0b, BW - 1);
-            const int cy0 = max(r[q].y - 1 - y0b, 0), cy1 = min(r[q].w - 1 - y0b, BH - 1);
-            const uint32_t cm = cx1 >= cx0 ? (2u << cx1) - (1u << cx0) : 0u;
-            const uint32_t rm = cy1 >= cy0 ? (2u << cy1) - (1u << cy0) : 0u;
-            s_f[t + blockDim.x * q] = f[q];
-            s_m[t + blockDim.x * q] = cm | (rm << 16);
+        if (lane == 0 && (c0 | c1) != 0) {
+            atomicAdd(&s_b[0], c0);
+            atomicAdd(&s_b[1], c1);
         }
         __syncthreads();
-        const int nk = (int)(ce - base < nt ? ce - base : nt);
-        for (int j0 = 0; j0 < nk; j0 += kWave) {
-            const uint32_t p = s_m[j0 + lane];   // (entries past nk are zero: no hits)
-            // the wavefront's 16 tiles as bits: 8 x 2 (SX = 3) or 16 x 1 (SX = 4)
-            uint32_t h;
-            if (SX == 3)
-                h = (((p >> (16 + ly0)) & 1u) ? (p & 0xffu) : 0u) | (((p >> (17 + ly0)) & 1u) ? (p & 0xffu) << 8 : 0u);
-            else
-                h = ((p >> (16 + ly0)) & 1u) ? (p & 0xffffu) : 0u;
-            int32_t fv = 0;
-            if (WRITE) fv = s_f[j0 + lane];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const bool hit = (h >> i) & 1u;
-                const uint64_t bal = __ballot(hit);
-                if (WRITE && hit) {
-                    // (the counts come from the same walk; the index is clamped all the same)
-                    const int32_t o = cnt[i] + (int32_t)__popcll(bal & lanemask_lt());
-                    a.out[o < a.cap ? o : a.cap - 1] = fv;
+        const int b0 = s_b[0], b1 = s_b[1];
+        __syncthreads();   // (s_b is reset by the next chunk)
+        for (int b = b0; b <= b1 && b < a.nblocks; ++b) {
+            const int64_t bb = b == 0 ? 0 : end_of(b - 1), be = end_of(b);
+            const int64_t cb = lo > bb ? lo : bb, ce = hi < be ? hi : be;
+            if (cb >= ce) continue;
+            const int bx = b % a.nbx, by = b / a.nbx;
+            const int x0b = bx * BW, y0b = by * BH;   // 0-based first tile of the block
+            const int x = x0b + (li & (BW - 1)), y = y0b + (li >> SX);
+            const bool in_image = lane < 16 && x < a.ntx && y < a.nty;
+            int32_t* const row = a.table + (k + b) * (int64_t)tpb;
+            int32_t cnt[16];   // COUNT: hits so far; WRITE: the next output index
+            int32_t start = 0;
+            if (WRITE) {
+                // tile i (i < 16) of the wavefront: its list start plus the block's earlier
+                // segments' hits, summed by lanes i, i + 16, i + 32, i + 48 over every fourth
+                // segment (independent loads), then across the four
+                const int tl = 16 * w + (lane & 15), part = lane >> 4;
+                const int xs = x0b + (tl & (BW - 1)), ys = y0b + (tl >> SX);
+                if (xs < a.ntx && ys < a.nty) {
+                    const int tile = xs + ys * a.ntx;
+                    if (part == 0 && tile > 0) start = a.tiles_end[tile - 1];
+#pragma unroll 4
+                    for (int64_t k2 = bb / nt + part; k2 < k; k2 += 4) start += a.table[(k2 + b) * (int64_t)tpb + tl];
                 }
-                cnt[i] += __popcll(bal);
+                start += __shfl_xor(start, 16);
+                start += __shfl_xor(start, 32);
             }
-        }
-        __syncthreads();
-    }
-    if (!WRITE) {
-        int32_t mine = 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mine = lane == i ? cnt[i] : mine;
-        const int x = x0b + ((16 * w + lane) & (BW - 1)), y = y0b + ((16 * w + lane) >> SX);
-        if (lane < 16 && x < a.ntx && y < a.nty) {
-            seg_counts[(int64_t)(x + y * a.ntx) * a.segs] = mine;
-            if (mine != 0) atomicAdd(&a.tile_totals[x + y * a.ntx], mine);
+            for (int i = 0; i < 16; ++i) cnt[i] = WRITE ? __builtin_amdgcn_readlane(start, i) : 0;
+            // candidates cb + t + blockDim q (q < kBinPer): the loads issue together
+            int32_t f[kBinPer];
+#pragma unroll
+            for (int q = 0; q < kBinPer; ++q) {
+                const int64_t e = cb + t + (int64_t)blockDim.x * q;
+                f[q] = e < ce ? a.cvals[e] : 0;
+            }
+            int4 r[kBinPer];
+#pragma unroll
+            for (int q = 0; q < kBinPer; ++q)
+                r[q] = f[q] > 0 ? reinterpret_cast<const int4*>(a.ranges)[f[q] - 1] : make_int4(1, 1, 0, 0);
+#pragma unroll
+            for (int q = 0; q < kBinPer; ++q) {
+                // columns in bits 0-15, rows in bits 16-31 (of the block); none for an empty slot
+                const int cx0 = max(r[q].x - 1 - x0b, 0), cx1 = min(r[q].z - 1 - x0b, BW - 1);
+                const int cy0 = max(r[q].y - 1 - y0b, 0), cy1 = min(r[q].w - 1 - y0b, BH - 1);
+                const uint32_t cm = cx1 >= cx0 ? (2u << cx1) - (1u << cx0) : 0u;
+                const uint32_t rm = cy1 >= cy0 ? (2u << cy1) - (1u << cy0) : 0u;
+                s_f[t + blockDim.x * q] = f[q];
+                s_m[t + blockDim.x * q] = cm | (rm << 16);
+            }
+            __syncthreads();
+            const int nk = (int)(ce - cb);
+            for (int j0 = 0; j0 < nk; j0 += kWave) {
+                const uint32_t p = s_m[j0 + lane];   // (entries past nk are zero: no hits)
+                // the wavefront's 16 tiles as bits: 8 x 2 (SX = 3) or 16 x 1 (SX = 4)
+                uint32_t h;
+                if (SX == 3)
+                    h = (((p >> (16 + ly0)) & 1u) ? (p & 0xffu) : 0u) |
+                        (((p >> (17 + ly0)) & 1u) ? (p & 0xffu) << 8 : 0u);
+                else
+                    h = ((p >> (16 + ly0)) & 1u) ? (p & 0xffffu) : 0u;
+                int32_t fv = 0;
+                if (WRITE) fv = s_f[j0 + lane];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const bool hit = (h >> i) & 1u;
+                    const uint64_t bal = __ballot(hit);
+                    if (WRITE && hit) {
+                        // (the counts come from the same walk; the index is clamped all the same)
+                        const int32_t o = cnt[i] + (int32_t)__popcll(bal & lanemask_lt());
+                        a.out[o < a.cap ? o : a.cap - 1] = fv;
+                    }
+                    cnt[i] += __popcll(bal);
+                }
+            }
+            if (!WRITE) {
+                int32_t mine = 0;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mine = lane == i ? cnt[i] : mine;
+                if (lane < 16) row[li] = mine;
+                if (in_image && mine != 0) atomicAdd(&a.tile_totals[x + y * a.ntx], mine);
+            }
+            __syncthreads();   // s_f, s_m are free again
         }
     }
 }
@@ -1565,7 +1605,7 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<char>((int64_t)radix_temp_bytes(big));
     ar.template take<int32_t>(kRectCopies * rect_diff_size(t));   // tile-coverage difference arrays
     ar.template take<int32_t>(ceil_div(key_cap, kEmitTile) + 2);  // first Gaussian of each emission block
-    ar.template take<int32_t>(t ? (int64_t)kBinMaxSegs * t->nb_tiles_x * t->nb_tiles_y : 0);   // per (segment, tile)
+    ar.template take<int32_t>(t ? bin_table_entries(key_cap, bin_geom(t).nblocks(), bin_geom(t).tpb()) : 0);   // per (segment, tile)
     ar.template take<int32_t>(t ? bin_geom(t).nblocks() : 0);                    // ends of the blocks' lists
     ar.template take<int32_t>(t ? ((int64_t)t->nb_tiles_x * t->nb_tiles_y + 3) / 4 * 4 : 0);   // tiles' totals
     ar.template take<int4>(cap);                                                  // rectangles in depth order
@@ -1614,7 +1654,8 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.rect_diff = ar.take<int32_t>(kRectCopies * r.ndiff);
     r.nblk = ceil_div(buf->key_capacity, kEmitTile) + 2;
     r.blk_first = ar.take<int32_t>(r.nblk);
-    r.tile_counts = ar.take<int32_t>(tiling ? (int64_t)kBinMaxSegs * tiling->nb_tiles_x * tiling->nb_tiles_y : 0);
+    r.tile_counts = ar.take<int32_t>(
+        tiling ? bin_table_entries(buf->key_capacity, bin_geom(tiling).nblocks(), bin_geom(tiling).tpb()) : 0);
     r.block_end = ar.take<int32_t>(tiling ? bin_geom(tiling).nblocks() : 0);
     r.ntt = tiling ? ((int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y + 3) / 4 * 4 : 0;
     r.tile_totals = ar.take<int32_t>(r.ntt);
@@ -1732,15 +1773,15 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     TDGS_LAUNCHED();
     // the tile lists
     BinArgs ba;
-    const int segs = bin_segments(nblocks);
     ba.ntx = tiling->nb_tiles_x; ba.nty = tiling->nb_tiles_y; ba.nbx = bg.nbx; ba.sy = bg.sy;
-    ba.nblocks = nblocks; ba.segs = segs;
+    ba.nblocks = nblocks;
     ba.cvals = buf->values; ba.cend = r.block_end; ba.mc = mb; ba.dmc = d_used;
-    ba.ranges = buf->tile_ranges; ba.tile_counts = r.tile_counts; ba.tile_totals = r.tile_totals;
+    ba.ranges = buf->tile_ranges; ba.table = r.tile_counts; ba.tile_totals = r.tile_totals;
     ba.tiles_end = buf->tiles_end;
     ba.out = buf->sorted_values; ba.cap = (int32_t)(kc < INT32_MAX ? kc : INT32_MAX); ba.err = d_err;
     const unsigned bthreads = 4u << (bg.sx + bg.sy);
-    const unsigned bgrid = (unsigned)(nblocks * segs);
+    const int64_t nchunks = ceil_div(mb > 0 ? mb : 1, (int64_t)bthreads * kBinPer);
+    const unsigned bgrid = (unsigned)(nchunks < kBinMaxGrid ? nchunks : kBinMaxGrid);
     const size_t lds = (size_t)bthreads * kBinPer * 2 * sizeof(uint32_t);
     if (bg.sx == 3) k_bin_tiles<3, false><<<bgrid, bthreads, lds, s>>>(ba);
     else k_bin_tiles<4, false><<<bgrid, bthreads, lds, s>>>(ba);
