@@ -584,11 +584,14 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
                                                                  const int32_t* __restrict__ blk_first,
                                                                  const int4* __restrict__ srect, EmitGrid grid,
                                                                  int nbits0, uint32_t* __restrict__ counts0,
-                                                                 int64_t count_tiles, int64_t* dc, int64_t key_cap) {
+                                                                 int64_t count_tiles, int64_t* dc, int64_t key_cap,
+                                                                 int32_t* zero, int64_t nzero) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
     __shared__ uint32_t s_h[kRsBins];
     const int t = threadIdx.x;
+    // (also clears zero[0, nzero) for the binning that follows)
+    for (int64_t k = (int64_t)blockIdx.x * blockDim.x + t; k < nzero; k += (int64_t)gridDim.x * blockDim.x) zero[k] = 0;
     if (dc) {
         // device counts: the grid covers key_cap entries; when the M keys fit the key arrays the
         // passes emit the blocks' entries (at most M), else none (the status says why)
@@ -849,7 +852,8 @@ inline int64_t bin_table_entries(int64_t kc, int32_t nblocks, int tpb) {
 struct BinArgs {
     int32_t ntx, nty, nbx, sy, nblocks;
     const int32_t* cvals;      // the blocks' lists: fgidx (1-based), block by block, depth order within
-    const int32_t* cend;       // end (exclusive) of each block's run in cvals
+    const int32_t* cend;       // end (exclusive) of each block's run in cvals, or null:
+    const uint32_t* totals;    // the coarse radix pass's digit totals (block b has id b + 1)
     int64_t mc;                // entries of cvals (launch bound)
     const int64_t* dmc;        // entries used (device counts), or null
     const int32_t* ranges;     // tile rectangles [x0, y0, x1, y1] (1-based, inclusive) by fgidx
@@ -886,8 +890,25 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
     const int64_t nchunks = (mc + nt - 1) / nt;
     if ((int64_t)blockIdx.x >= nchunks) return;
     const bool lds_ends = a.nblocks <= 1024;
-    if (lds_ends)
+    if (a.totals) {
+        // one radix pass sorted the 8-bit block ids (at most 255 blocks, at least 256
+        // threads): the ends are the inclusive prefix sums of the digit totals 1..255
+        const int lane = __lane_id();
+        int32_t c = t < kRsBins && t > 0 ? (int32_t)a.totals[t] : 0;
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int32_t o = __shfl_up(c, d, kWave);
+            if (lane >= d) c += o;
+        }
+        if (t < kRsBins && lane == kWave - 1) s_cend[1020 + t / kWave] = c;   // wave totals (t < 256)
+        __syncthreads();
+        if (t < kRsBins) {
+            for (int q = 0; q < t / kWave; ++q) c += s_cend[1020 + q];
+        }
+        __syncthreads();
+        if (t > 0 && t <= a.nblocks) s_cend[t - 1] = c;
+    } else if (lds_ends) {
         for (int i = t; i < a.nblocks; i += blockDim.x) s_cend[i] = a.cend[i];
+    }
     auto end_of = [&](int i) -> int64_t {
         const int64_t e = lds_ends ? s_cend[i] : a.cend[i];
         return e < mc ? e : mc;
@@ -1748,7 +1769,8 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
         k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg,
-                                                        nbits0, table, count_tiles, dc, kc);
+                                                        nbits0, table, count_tiles, dc, kc,
+                                                        one_pass ? r.tile_totals : nullptr, one_pass ? r.ntt : 0);
         TDGS_LAUNCHED();
     }
     {
@@ -1766,16 +1788,19 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
                                                 d_err, nullptr, d_used));
     }
     StageScope sc(TDGS_STAGE_TILE_RANGES, s);
-    // ends of the blocks' runs
-    const int64_t rthreads = ceil_div(mb, 8) > nblocks ? ceil_div(mb, 8) : nblocks;
-    k_tile_ranges16<<<(unsigned)ceil_div(rthreads, 256), 256, 0, s>>>(mb, c16, nblocks, r.block_end, d_used,
-                                                                      r.tile_totals, r.ntt);
-    TDGS_LAUNCHED();
+    if (!one_pass) {
+        // ends of the blocks' runs (with one pass they are the prefix sums of its digit totals)
+        const int64_t rthreads = ceil_div(mb, 8) > nblocks ? ceil_div(mb, 8) : nblocks;
+        k_tile_ranges16<<<(unsigned)ceil_div(rthreads, 256), 256, 0, s>>>(mb, c16, nblocks, r.block_end, d_used,
+                                                                          r.tile_totals, r.ntt);
+        TDGS_LAUNCHED();
+    }
     // the tile lists
     BinArgs ba;
     ba.ntx = tiling->nb_tiles_x; ba.nty = tiling->nb_tiles_y; ba.nbx = bg.nbx; ba.sy = bg.sy;
     ba.nblocks = nblocks;
     ba.cvals = buf->values; ba.cend = r.block_end; ba.mc = mb; ba.dmc = d_used;
+    ba.totals = one_pass ? totals : nullptr;
     ba.ranges = buf->tile_ranges; ba.table = r.tile_counts; ba.tile_totals = r.tile_totals;
     ba.tiles_end = buf->tiles_end;
     ba.out = buf->sorted_values; ba.cap = (int32_t)(kc < INT32_MAX ? kc : INT32_MAX); ba.err = d_err;

@@ -1,9 +1,11 @@
 // scan.hpp — device-wide inclusive scan of int32 (or int64) items with int64 running sums
 // (replaces CUDA.jl's accumulate!(+) at src/forward_core.jl:231, 259 and
-// src/training.jl:384). Reduce-then-scan in three launches:
-//   1. each 2048-item tile reduces its items            (k_scan_reduce)
-//   2. one block scans the tile sums, writes the total   (k_scan_tiles)
-//   3. each tile rescans its items with its offset        (k_scan_apply)
+// src/training.jl:384). Reduce-then-scan in two launches:
+//   1. each 2048-item tile reduces its items                      (k_scan_reduce)
+//   2. each tile sums the earlier tiles' sums into its offset and
+//      rescans its items; tile 0 also writes the total              (k_scan_apply)
+// (A third launch that scanned the tile sums once cost more than every tile summing its
+// predecessors: a kernel boundary is ~4 us, the extra loads of a few hundred sums ~1 us.)
 // Items come from a functor In(i) and results go to a functor Out(i, inclusive, item), so
 // compaction, gathers and scatters fuse into the scan passes instead of separate kernels.
 #pragma once
@@ -61,35 +63,25 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_reduce(In in, int64_t n, 
     if (threadIdx.x == 0) tile_sums[blockIdx.x] = total;
 }
 
-// Single block: exclusive scan of the tile sums in place; grand total to *total_out.
-static __global__ __launch_bounds__(kScanThreads) void k_scan_tiles(int64_t* tile_sums, int64_t ntiles,
-                                                             int64_t* total_out) {
-    int64_t carry = 0;
-    for (int64_t start = 0; start < ntiles; start += (int64_t)kScanThreads * kScanItems) {
-        const int64_t base = start + (int64_t)threadIdx.x * kScanItems;
-        int64_t v[kScanItems];
-        int64_t acc = 0;
-#pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            v[k] = base + k < ntiles ? tile_sums[base + k] : 0;
-            acc += v[k];
-        }
-        int64_t total;
-        int64_t off = block_exclusive_scan(acc, &total) + carry;
-#pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            if (base + k < ntiles) tile_sums[base + k] = off;
-            off += v[k];
-        }
-        carry += total;
-    }
-    if (threadIdx.x == 0 && total_out) *total_out = carry;
-}
-
+// Tile b's offset is the sum of tile_sums[0, b); tile 0 sums all ntiles and writes the
+// total to *total_out (when not null).
 template <class In, class Out>
-__global__ __launch_bounds__(kScanThreads) void k_scan_apply(In in, Out out, int64_t n,
-                                                             const int64_t* tile_offsets, const int64_t* d_limit) {
-    if (d_limit && (int64_t)blockIdx.x * kScanTile >= *d_limit) return;
+__global__ __launch_bounds__(kScanThreads) void k_scan_apply(In in, Out out, int64_t n, const int64_t* tile_sums,
+                                                             int64_t ntiles, int64_t* total_out,
+                                                             const int64_t* d_limit) {
+    const int64_t b = blockIdx.x;
+    const bool past = d_limit && b * kScanTile >= *d_limit;
+    if (past && b != 0) return;
+    const int64_t upto = b == 0 ? ntiles : b;
+    int64_t part = 0;
+    for (int64_t k = threadIdx.x; k < upto; k += kScanThreads) part += tile_sums[k];
+    int64_t before;
+    block_exclusive_scan(part, &before);   // (only the block total is used)
+    if (b == 0) {
+        if (threadIdx.x == 0 && total_out) *total_out = before;
+        before = 0;
+    }
+    if (past) return;
     const int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
     using Item = decltype(in(int64_t(0)));   // int32_t, or int64_t for two packed counts
     Item v[kScanItems];
@@ -101,7 +93,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan_apply(In in, Out out, int
         acc += v[k];
     }
     int64_t total;
-    int64_t run = block_exclusive_scan(acc, &total) + tile_offsets[blockIdx.x];
+    int64_t run = block_exclusive_scan(acc, &total) + before;
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
         const int64_t i = base + k;
@@ -129,9 +121,8 @@ int device_scan(In1 in_reduce, In2 in_apply, Out out, int64_t n, void* temp, siz
     int64_t* tile_sums = (int64_t*)temp;
     k_scan_reduce<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_reduce, n, tile_sums, d_limit);
     TDGS_LAUNCHED();
-    k_scan_tiles<<<1, kScanThreads, 0, stream>>>(tile_sums, ntiles, d_total);
-    TDGS_LAUNCHED();
-    k_scan_apply<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_apply, out, n, tile_sums, d_limit);
+    k_scan_apply<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_apply, out, n, tile_sums, ntiles, d_total,
+                                                                 d_limit);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
