@@ -8,9 +8,9 @@
 //   k_ssim_forward   filters x, y, x^2, y^2, xy with the separable window (LDS tile with a
 //                    5-pixel halo), evaluates the SSIM map S and its partial derivatives
 //                    D1 = dS/dmu_x, D2 = dS/dE[x^2], D3 = dS/dE[xy] per pixel, and sums S
-//                    and |x - y| per workgroup (one partial pair per workgroup; a one-block
-//                    launch adds the partials to the caller's sums, so no workgroup waits on
-//                    an atomic to a shared address)
+//                    and |x - y| per workgroup (one partial pair per workgroup; workgroup 0
+//                    of the backward launch adds them to the caller's sums, so no workgroup
+//                    waits on an atomic to a shared address)
 //   k_ssim_backward  filters D1, D2, D3 with the same window and forms
 //                    dL/dx = (1-lambda) sign(x - y)/N - lambda/N (G*D1 + 2 x G*D2 + y G*D3)
 // Images use the reference layout 3 x h x w (pixel (v, u) channel c at 3 (v + h u) + c).
@@ -55,44 +55,75 @@ struct SsimWindow {
     float w[2 * kSsimR + 1];
 };
 
-// k_ssim_forward LDS: the input (x, y) pairs of the 26 x 26 tile per (column, channel), then
-// the pass-1 values of the 15 quantities per (quantity, output row), columns contiguous; the
-// pass-2 output (15 values per pixel) reuses the latter's space.
+// k_ssim_forward LDS: one buffer, in turn the input (x, y) pairs of the 26 x 26 tile per
+// (column, channel), the pass-1 values of the 15 quantities per (quantity, output row), columns
+// contiguous, and the pass-2 output (15 values per pixel). Each pass reads its inputs into
+// registers and passes a barrier before it overwrites them, so the tile needs 26 KB of LDS
+// (6 workgroups per CU) instead of 43 KB for separate buffers (3 per CU); |x - y| of the
+// tile's own pixels is summed while the inputs are loaded.
+constexpr int kSsimFwdLds = (kSsimIn * 3 * kRow * 2 > kQF * kSsimT * kRow) ? kSsimIn * 3 * kRow * 2 : kQF * kSsimT * kRow;
 __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ x, const float* __restrict__ y,
                                                       int W, int H, SsimWindow win, float* __restrict__ dmap,
                                                       double* __restrict__ partials) {
-    __shared__ float2 s_in[kSsimIn * 3 * kRow];        // (iu, c, iv) at (iu*3 + c)*kRow + iv
-    __shared__ float s_v[kQF * kSsimT * kRow];         // (q, ov, iu) at (q*16 + ov)*kRow + iu
+    __shared__ float4 s_buf4[kSsimFwdLds / 4 + 1];
     __shared__ double s_red[2][256 / kWave];
+    float2* const s_in = reinterpret_cast<float2*>(s_buf4);   // (iu, c, iv) at (iu*3 + c)*kRow + iv
+    float* const s_v = reinterpret_cast<float*>(s_buf4);      // (q, ov, iu) at (q*16 + ov)*kRow + iu
     float* const s_out = s_v;                          // (ou, ov, q) at (ou*16 + ov)*kOutPitch + q
-    static_assert(kSsimT * kSsimT * kOutPitch <= kQF * kSsimT * kRow, "pass-2 output fits");
+    static_assert(kSsimT * kSsimT * kOutPitch <= kSsimFwdLds, "pass-2 output fits");
     const int t = threadIdx.x;
     int tv, tu;
     ssim_tile((H + kSsimT - 1) / kSsimT, gridDim.x, &tv, &tu);
     const int v0 = tv * kSsimT - kSsimR, u0 = tu * kSsimT - kSsimR;
-    for (int k = t; k < kSsimIn * kSsimIn; k += 256) {
+    // the tile's inputs: pixel k = t + 256 i (i < 3) of the 26 x 26 tile, all loads issued
+    // before the first LDS store
+    double l1 = 0.0;
+    constexpr int kLoads = (kSsimIn * kSsimIn + 255) / 256;
+    float2 xy[kLoads][3];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int k = t + 256 * i;
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
-        const bool in = v >= 0 && v < H && u >= 0 && u < W;
+        const bool in = k < kSsimIn * kSsimIn && v >= 0 && v < H && u >= 0 && u < W;
         const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
 #pragma unroll
-        for (int c = 0; c < 3; ++c)
-            s_in[(iu * 3 + c) * kRow + iv] = in ? make_float2(x[p + c], y[p + c]) : make_float2(0.0f, 0.0f);
+        for (int c = 0; c < 3; ++c) xy[i][c] = in ? make_float2(x[p + c], y[p + c]) : make_float2(0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int k = t + 256 * i;
+        if (k >= kSsimIn * kSsimIn) break;
+        const int iv = k % kSsimIn, iu = k / kSsimIn;
+        const bool own = iv >= kSsimR && iv < kSsimR + kSsimT && iu >= kSsimR && iu < kSsimR + kSsimT;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            s_in[(iu * 3 + c) * kRow + iv] = xy[i][c];
+            if (own) l1 += fabs((double)xy[i][c].x - (double)xy[i][c].y);   // (zero outside the image)
+        }
     }
     __syncthreads();
-    // pass 1: thread (iu, c, half) filters rows ov = 8 half .. 8 half + 7 of column iu, channel c
-    if (t < kSsimIn * 3 * 2) {
-        const int iu = t % kSsimIn, c = (t / kSsimIn) % 3, half = t / (3 * kSsimIn);
-        const float2* src = s_in + (iu * 3 + c) * kRow + 8 * half;
-        float a[18], b[18];
+    // pass 1: thread (iu, c, part) filters output rows ov = o0 .. o0 + no - 1 of column iu,
+    // channel c, the 16 rows split 6 + 5 + 5 over three parts (234 of the 256 threads)
+    const bool p1 = t < kSsimIn * 3 * 3;
+    const int p1_iu = t % kSsimIn, p1_c = (t / kSsimIn) % 3, p1_part = t / (3 * kSsimIn);
+    const int o0 = p1_part == 0 ? 0 : 1 + 5 * p1_part, no = p1_part == 0 ? 6 : 5;
+    float a[16], b[16];
+    if (p1) {
+        const float2* src = s_in + (p1_iu * 3 + p1_c) * kRow + o0;
 #pragma unroll
-        for (int k = 0; k < 18; ++k) {
-            const float2 ab = src[k];
+        for (int k = 0; k < 16; ++k) {
+            const float2 ab = k < no + 2 * kSsimR ? src[k] : make_float2(0.0f, 0.0f);
             a[k] = ab.x;
             b[k] = ab.y;
         }
+    }
+    __syncthreads();   // s_v overwrites s_in
+    if (p1) {
+        const int iu = p1_iu, c = p1_c;
 #pragma unroll
-        for (int o = 0; o < 8; ++o) {
+        for (int o = 0; o < 6; ++o) {
+            if (o >= no) break;
             float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f, m4 = 0.0f;
 #pragma unroll
             for (int d = 0; d < 2 * kSsimR + 1; ++d) {
@@ -103,7 +134,7 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
                 m3 = fmaf(wd, bv * bv, m3);
                 m4 = fmaf(wd, av * bv, m4);
             }
-            const int ov = 8 * half + o;
+            const int ov = o0 + o;
             float* dst = s_v + ((5 * c) * kSsimT + ov) * kRow + iu;
             dst[0] = m0;
             dst[kSsimT * kRow] = m1;
@@ -139,7 +170,7 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     float m[kQF];
 #pragma unroll
     for (int q = 0; q < kQF; ++q) m[q] = s_out[(ou * kSsimT + ov) * kOutPitch + q];
-    double ssum = 0.0, l1 = 0.0;
+    double ssum = 0.0;
     if (on) {
         const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
 #pragma unroll
@@ -157,8 +188,6 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
             dmap[3 * p + 3 + c] = -S / b2;            // dS/dE[x^2]
             dmap[3 * p + 6 + c] = 2.0f * a1 / B;      // dS/dE[xy]
             ssum += (double)S;
-            const float2 px = s_in[((ou + kSsimR) * 3 + c) * kRow + ov + kSsimR];
-            l1 += fabs((double)px.x - (double)px.y);
         }
     }
     for (int d = 32; d >= 1; d >>= 1) {
@@ -179,12 +208,12 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     }
 }
 
-// One workgroup: sums[k] += sum over the nblk partial pairs.
-__global__ __launch_bounds__(1024) void k_ssim_sums(const double* __restrict__ partials, int64_t nblk,
-                                                    double* __restrict__ sums) {
-    __shared__ double s_red[2][1024 / kWave];
+// Workgroup of 256 threads: sums[k] += sum over the nblk partial pairs (run by workgroup 0 of
+// k_ssim_backward, after k_ssim_forward wrote the partials: no launch of its own).
+__device__ void ssim_add_partials(const double* __restrict__ partials, int64_t nblk, double* __restrict__ sums) {
+    __shared__ double s_red[2][256 / kWave];
     double a = 0.0, b = 0.0;
-    for (int64_t i = threadIdx.x; i < nblk; i += 1024) {
+    for (int64_t i = threadIdx.x; i < nblk; i += 256) {
         a += partials[2 * i];
         b += partials[2 * i + 1];
     }
@@ -199,7 +228,7 @@ __global__ __launch_bounds__(1024) void k_ssim_sums(const double* __restrict__ p
     __syncthreads();
     if (threadIdx.x == 0) {
         double ta = 0.0, tb = 0.0;
-        for (int k = 0; k < 1024 / kWave; ++k) { ta += s_red[0][k]; tb += s_red[1][k]; }
+        for (int k = 0; k < 256 / kWave; ++k) { ta += s_red[0][k]; tb += s_red[1][k]; }
         sums[0] += ta;
         sums[1] += tb;
     }
@@ -208,31 +237,65 @@ __global__ __launch_bounds__(1024) void k_ssim_sums(const double* __restrict__ p
 __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__ x, const float* __restrict__ y,
                                                        int W, int H, SsimWindow win,
                                                        const float* __restrict__ dmap, float w_l1, float w_ssim,
-                                                       float* __restrict__ grad) {
+                                                       float* __restrict__ grad, const double* __restrict__ partials,
+                                                       int64_t nblk, double* __restrict__ sums) {
+    // one buffer, in turn the input columns, the pass-1 values and the pass-2 output (as in
+    // k_ssim_forward: every pass reads its inputs into registers before a barrier)
     __shared__ float s_in[kSsimIn * kQB * kRow];       // (iu, q, iv) at (iu*9 + q)*kRow + iv
-    __shared__ float s_v[kQB * kSsimT * kRow];         // (q, ov, iu) at (q*16 + ov)*kRow + iu
+    float* const s_v = s_in;                           // (q, ov, iu) at (q*16 + ov)*kRow + iu
     float* const s_out = s_in;                         // (ou, ov, q) at (ou*16 + ov)*kOutPitch + q
     static_assert(kSsimT * kSsimT * kOutPitch <= kSsimIn * kQB * kRow, "pass-2 output fits");
+    static_assert(kQB * kSsimT * kRow <= kSsimIn * kQB * kRow, "pass-1 output fits");
     const int t = threadIdx.x;
     int tv, tu;
     ssim_tile((H + kSsimT - 1) / kSsimT, gridDim.x, &tv, &tu);
     const int v0 = tv * kSsimT - kSsimR, u0 = tu * kSsimT - kSsimR;
-    for (int k = t; k < kSsimIn * kSsimIn; k += 256) {
+    if (blockIdx.x == 0) ssim_add_partials(partials, nblk, sums);
+    // this thread's output pixel and its inputs (read now, used at the end)
+    const int ov = t % kSsimT, ou = t / kSsimT;
+    const int v = v0 + kSsimR + ov, u = u0 + kSsimR + ou;
+    const bool on = v < H && u < W;
+    const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
+    float xv[3], yv[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        xv[c] = on ? x[p + c] : 0.0f;
+        yv[c] = on ? y[p + c] : 0.0f;
+    }
+    // the tile's nine maps: pixel k = t + 256 i (i < 3) of the 26 x 26 tile, all loads issued
+    // before the first LDS store
+    constexpr int kLoads = (kSsimIn * kSsimIn + 255) / 256;
+    float dv[kLoads][kQB];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int k = t + 256 * i;
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
-        const bool in = v >= 0 && v < H && u >= 0 && u < W;
+        const bool in = k < kSsimIn * kSsimIn && v >= 0 && v < H && u >= 0 && u < W;
         const int64_t p = 9 * ((int64_t)v + (int64_t)H * u);
 #pragma unroll
-        for (int q = 0; q < kQB; ++q) s_in[(iu * kQB + q) * kRow + iv] = in ? dmap[p + q] : 0.0f;
+        for (int q = 0; q < kQB; ++q) dv[i][q] = in ? dmap[p + q] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int k = t + 256 * i;
+        if (k >= kSsimIn * kSsimIn) break;
+        const int iv = k % kSsimIn, iu = k / kSsimIn;
+#pragma unroll
+        for (int q = 0; q < kQB; ++q) s_in[(iu * kQB + q) * kRow + iv] = dv[i][q];
     }
     __syncthreads();
     // pass 1: thread (iu, q) filters the whole column iu of quantity q along v
-    if (t < kSsimIn * kQB) {
+    const bool p1 = t < kSsimIn * kQB;
+    float a[kSsimIn];
+    if (p1) {
         const float* src = s_in + t * kRow;   // t = iu * 9 + q
-        const int iu = t / kQB, q = t % kQB;
-        float a[kSsimIn];
 #pragma unroll
         for (int k = 0; k < kSsimIn; ++k) a[k] = src[k];
+    }
+    __syncthreads();   // s_v overwrites s_in
+    if (p1) {
+        const int iu = t / kQB, q = t % kQB;
 #pragma unroll
         for (int ov = 0; ov < kSsimT; ++ov) {
             float m = 0.0f;
@@ -243,33 +306,34 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
     }
     __syncthreads();
     // pass 2: thread (ov, q) filters row ov of quantity q along u
-    if (t < kSsimT * kQB) {
+    const bool p2 = t < kSsimT * kQB;
+    float b[kSsimIn];
+    if (p2) {
         const int ov = t % kSsimT, q = t / kSsimT;
         const float* src = s_v + (q * kSsimT + ov) * kRow;
-        float b[kSsimIn];
 #pragma unroll
         for (int k = 0; k < kSsimIn; ++k) b[k] = src[k];
+    }
+    __syncthreads();   // s_out overwrites s_v
+    if (p2) {
+        const int ov = t % kSsimT, q = t / kSsimT;
 #pragma unroll
         for (int ou = 0; ou < kSsimT; ++ou) {
             float m = 0.0f;
 #pragma unroll
             for (int d = 0; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], b[ou + d], m);
-            s_out[(ou * kSsimT + ov) * kOutPitch + q] = m;   // s_in is no longer read
+            s_out[(ou * kSsimT + ov) * kOutPitch + q] = m;
         }
     }
     __syncthreads();
-    const int ov = t % kSsimT, ou = t / kSsimT;
-    const int v = v0 + kSsimR + ov, u = u0 + kSsimR + ou;
-    if (v >= H || u >= W) return;
+    if (!on) return;
     float f[kQB];
 #pragma unroll
     for (int q = 0; q < kQB; ++q) f[q] = s_out[(ou * kSsimT + ov) * kOutPitch + q];
-    const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        const float xv = x[p + c], yv = y[p + c];
-        const float dssim = -(f[c] + 2.0f * xv * f[3 + c] + yv * f[6 + c]);
-        const float s = xv > yv ? w_l1 : -w_l1;
+        const float dssim = -(f[c] + 2.0f * xv[c] * f[3 + c] + yv[c] * f[6 + c]);
+        const float s = xv[c] > yv[c] ? w_l1 : -w_l1;
         grad[p + c] = fmaf(w_ssim, dssim, s);
     }
 }
@@ -317,12 +381,10 @@ int tdgs_loss_grad(void* stream, const float* rendered, const float* gt, int32_t
     double* partials = (double*)((char*)temp + loss_dmap_bytes(width, height));
     k_ssim_forward<<<grid, 256, 0, s>>>(rendered, gt, width, height, win, (float*)temp, partials);
     TDGS_LAUNCHED();
-    k_ssim_sums<<<1, 1024, 0, s>>>(partials, loss_blocks(width, height), sums_dev);
-    TDGS_LAUNCHED();
     const float w_l1 = (1.0f - dssim_weight) / (float)count;
     const float w_ssim = dssim_weight / (float)count;
     k_ssim_backward<<<grid, 256, 0, s>>>(rendered, gt, width, height, win, (const float*)temp, w_l1, w_ssim,
-                                         grad_out);
+                                         grad_out, partials, loss_blocks(width, height), sums_dev);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
