@@ -385,34 +385,42 @@ __device__ __forceinline__ void adam_in_place(const AdamInPlace& d, float& p, fl
 // the operation order of k_adam's geometry items.
 __device__ __forceinline__ void adam_geometry(const BackProjectArgs& a, int64_t gi, const float dm[3], float dlogit,
                                               const float dlogs[3], const float dq[4]) {
+    // every load before the first store (a store could alias a later load, which would
+    // otherwise make each load wait for the stores before it)
     const AdamInPlace& d = a.adam;
-    float4 mo = reinterpret_cast<float4*>(a.g.means_opacity)[gi];
+    float4 mo = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
     float2* mm = reinterpret_cast<float2*>(d.m_means) + 3 * gi;
     float2 m0 = mm[0], m1 = mm[1], m2 = mm[2];
-    adam_in_place(d, mo.x, dm[0], m0.x, m0.y, d.lr[0]);
-    adam_in_place(d, mo.y, dm[1], m1.x, m1.y, d.lr[0]);
-    adam_in_place(d, mo.z, dm[2], m2.x, m2.y, d.lr[0]);
-    float2 mop = reinterpret_cast<float2*>(d.m_op)[gi];
-    adam_in_place(d, mo.w, dlogit, mop.x, mop.y, d.lr[1]);
-    reinterpret_cast<float4*>(a.g.means_opacity)[gi] = mo;
-    mm[0] = m0; mm[1] = m1; mm[2] = m2;
-    reinterpret_cast<float2*>(d.m_op)[gi] = mop;
+    float2 mop = reinterpret_cast<const float2*>(d.m_op)[gi];
+    float sc[3];
+    float2 msc[3];
     float2* ms = reinterpret_cast<float2*>(d.m_sc) + 3 * gi;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
-        float p = a.g.scaling[3 * gi + k];
-        float2 m = ms[k];
-        adam_in_place(d, p, dlogs[k], m.x, m.y, d.lr[2]);
-        a.g.scaling[3 * gi + k] = p;
-        ms[k] = m;
+        sc[k] = a.g.scaling[3 * gi + k];
+        msc[k] = ms[k];
     }
-    float4 r = reinterpret_cast<float4*>(a.g.rotation)[gi];
+    float4 r = reinterpret_cast<const float4*>(a.g.rotation)[gi];
     float4* mr = reinterpret_cast<float4*>(d.m_rot) + 2 * gi;
     float4 ma = mr[0], mb = mr[1];
+    adam_in_place(d, mo.x, dm[0], m0.x, m0.y, d.lr[0]);
+    adam_in_place(d, mo.y, dm[1], m1.x, m1.y, d.lr[0]);
+    adam_in_place(d, mo.z, dm[2], m2.x, m2.y, d.lr[0]);
+    adam_in_place(d, mo.w, dlogit, mop.x, mop.y, d.lr[1]);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) adam_in_place(d, sc[k], dlogs[k], msc[k].x, msc[k].y, d.lr[2]);
     adam_in_place(d, r.x, dq[0], ma.x, ma.y, d.lr[3]);
     adam_in_place(d, r.y, dq[1], ma.z, ma.w, d.lr[3]);
     adam_in_place(d, r.z, dq[2], mb.x, mb.y, d.lr[3]);
     adam_in_place(d, r.w, dq[3], mb.z, mb.w, d.lr[3]);
+    reinterpret_cast<float4*>(a.g.means_opacity)[gi] = mo;
+    mm[0] = m0; mm[1] = m1; mm[2] = m2;
+    reinterpret_cast<float2*>(d.m_op)[gi] = mop;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        a.g.scaling[3 * gi + k] = sc[k];
+        ms[k] = msc[k];
+    }
     reinterpret_cast<float4*>(a.g.rotation)[gi] = r;
     mr[0] = ma;
     mr[1] = mb;
@@ -574,23 +582,45 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
         // update! on the SH coefficients k < hr of every row (k_adam's SH items)
         const AdamInPlace& d = a.adam;
         if (hs == hg && hg == hr && (3 * hr) % 4 == 0) {
+            // kBpGroup items per thread at a time, all their loads issued before any store
+            // (the parameter and moment stores could alias the next items' loads, so a plain
+            // loop would wait on every load in turn)
+            constexpr int kBpGroup = 4;
             const int q4 = 3 * hr / 4;
-            for (int i = t; i < nrows * q4; i += kBpThreads) {
-                const int j = i / q4, q = i - j * q4;
-                const int64_t gi = s_gall[j];
-                if (gi < 0) continue;
-                const int k0 = (4 * q) % hr;
-                const float* sv = s_sh + j * kShRow + 4 * q;
-                float4* pp = reinterpret_cast<float4*>(a.g.sh + (int64_t)3 * hs * gi) + q;
-                float4* mp = reinterpret_cast<float4*>(d.m_sh + (int64_t)6 * hs * gi) + 2 * q;
-                float4 p = *pp, m0 = mp[0], m1 = mp[1];
-                adam_in_place(d, p.x, sv[0], m0.x, m0.y, k0 == 0 ? d.lr[4] : d.lr[5]);
-                adam_in_place(d, p.y, sv[1], m0.z, m0.w, d.lr[5]);
-                adam_in_place(d, p.z, sv[2], m1.x, m1.y, d.lr[5]);
-                adam_in_place(d, p.w, sv[3], m1.z, m1.w, d.lr[5]);
-                *pp = p;
-                mp[0] = m0;
-                mp[1] = m1;
+            const int items = nrows * q4;
+            for (int base = 0; base < items; base += kBpGroup * kBpThreads) {
+                float4 p[kBpGroup], m0[kBpGroup], m1[kBpGroup];
+                int64_t gi[kBpGroup];
+                int jq[kBpGroup][2];
+#pragma unroll
+                for (int u = 0; u < kBpGroup; ++u) {
+                    const int i = base + t + kBpThreads * u;
+                    const int j = i / q4, q = i - j * q4;
+                    jq[u][0] = j;
+                    jq[u][1] = q;
+                    gi[u] = i < items ? s_gall[j] : -1;
+                    if (gi[u] >= 0) {
+                        p[u] = reinterpret_cast<const float4*>(a.g.sh + (int64_t)3 * hs * gi[u])[q];
+                        const float4* mp = reinterpret_cast<const float4*>(d.m_sh + (int64_t)6 * hs * gi[u]) + 2 * q;
+                        m0[u] = mp[0];
+                        m1[u] = mp[1];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < kBpGroup; ++u) {
+                    if (gi[u] < 0) continue;
+                    const int j = jq[u][0], q = jq[u][1];
+                    const int k0 = (4 * q) % hr;
+                    const float* sv = s_sh + j * kShRow + 4 * q;
+                    adam_in_place(d, p[u].x, sv[0], m0[u].x, m0[u].y, k0 == 0 ? d.lr[4] : d.lr[5]);
+                    adam_in_place(d, p[u].y, sv[1], m0[u].z, m0[u].w, d.lr[5]);
+                    adam_in_place(d, p[u].z, sv[2], m1[u].x, m1[u].y, d.lr[5]);
+                    adam_in_place(d, p[u].w, sv[3], m1[u].z, m1[u].w, d.lr[5]);
+                    reinterpret_cast<float4*>(a.g.sh + (int64_t)3 * hs * gi[u])[q] = p[u];
+                    float4* mp = reinterpret_cast<float4*>(d.m_sh + (int64_t)6 * hs * gi[u]) + 2 * q;
+                    mp[0] = m0[u];
+                    mp[1] = m1[u];
+                }
             }
         } else {
             const int per = 3 * hr;
