@@ -1005,8 +1005,10 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
                     const bool hit = (h >> i) & 1u;
                     const uint64_t bal = __ballot(hit);
                     if (WRITE && hit) {
-                        // (the counts come from the same walk; the index is clamped all the same)
-                        const int32_t o = cnt[i] + (int32_t)__popcll(bal & lanemask_lt());
+                        // the tile's next index plus the hits in lower lanes (v_mbcnt); the
+                        // counts come from the same walk, the index is clamped all the same
+                        const int32_t o = (int32_t)__builtin_amdgcn_mbcnt_hi(
+                            (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, (uint32_t)cnt[i]));
                         a.out[o < a.cap ? o : a.cap - 1] = fv;
                     }
                     cnt[i] += __popcll(bal);
