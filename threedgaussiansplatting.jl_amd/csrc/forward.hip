@@ -578,6 +578,7 @@ constexpr int kEmitSortThreads = kRsThreads;
 constexpr int kEmitSortItems = kEmitTile / kEmitSortThreads;
 static_assert(kEmitSortItems == RsTile<uint16_t>::kItems, "radix tile layout");
 
+template <bool LOOP>
 __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int64_t m,
                                                                  const int32_t* __restrict__ sorted_f,
                                                                  const int32_t* __restrict__ cs,
@@ -606,22 +607,25 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
             dc[kCntCoarseUsed] = m;
             dc[kCntStatus] = st;
         }
-        if ((int64_t)blockIdx.x * kEmitTile >= m) {   // past the entries: an empty column of counts
-            if (t < kRsBins) counts0[rs_entry(t, blockIdx.x, count_tiles)] = 0;
-            return;
-        }
     }
-    if (t < kRsBins) s_h[t] = 0;
-    int32_t tile[kEmitSortItems], val[kEmitSortItems];
-    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, srect, grid, s_buf,
-                                                    s_range, tile, val);
-    const int64_t first = (int64_t)blockIdx.x * kEmitTile + (int64_t)t * kEmitSortItems;
+    // emission blocks blockIdx.x, + gridDim.x, ... (LOOP: a grid capped below the
+    // capacity-sized block count of a device-count render; else one block per workgroup); the
+    // count columns of the blocks past the entries are left alone (the row scan reads the used
+    // ones only)
     const uint32_t mask0 = (1u << nbits0) - 1u;
+    for (int64_t blk = blockIdx.x; blk * kEmitTile < m; blk += LOOP ? gridDim.x : m) {
+        if (t < kRsBins) s_h[t] = 0;
+        int32_t tile[kEmitSortItems], val[kEmitSortItems];
+        emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blk, sorted_f, cs, blk_first, srect, grid, s_buf,
+                                                        s_range, tile, val);
+        const int64_t first = blk * kEmitTile + (int64_t)t * kEmitSortItems;
 #pragma unroll
-    for (int i = 0; i < kEmitSortItems; ++i)
-        if (first + i < m) atomicAdd(&s_h[(uint32_t)tile[i] & mask0], 1u);
-    __syncthreads();
-    if (t < kRsBins) counts0[rs_entry(t, blockIdx.x, count_tiles)] = s_h[t];
+        for (int i = 0; i < kEmitSortItems; ++i)
+            if (first + i < m) atomicAdd(&s_h[(uint32_t)tile[i] & mask0], 1u);
+        __syncthreads();
+        if (t < kRsBins) counts0[rs_entry(t, blk, count_tiles)] = s_h[t];
+        __syncthreads();   // s_h and s_buf are reused by the next block
+    }
 }
 
 // Slot of key k of the block in k_emit_scatter's transpose (thread k / 8 writes item k % 8,
@@ -632,23 +636,19 @@ __device__ __forceinline__ int emit_sort_slot(int k) {
     return t * kEmitSortItems + ((i + t) & (kEmitSortItems - 1));
 }
 
-__global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
-    int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
-    const int32_t* __restrict__ blk_first, const int4* __restrict__ srect, EmitGrid grid, int nbits0,
-    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, int64_t count_tiles,
-    uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err, const int64_t* dc) {
-    __shared__ int32_t s_buf[kEmitTile + 1];
-    __shared__ int64_t s_range[2];
+// One emission block of k_emit_scatter.
+__device__ __forceinline__ void emit_scatter_block(int64_t blk, int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f,
+                                                   const int32_t* __restrict__ cs, const int32_t* __restrict__ blk_first,
+                                                   const int4* __restrict__ srect, EmitGrid grid, int nbits0,
+                                                   const uint32_t* __restrict__ offsets,
+                                                   const uint32_t* __restrict__ totals, int64_t count_tiles,
+                                                   uint16_t* __restrict__ kout, int32_t* __restrict__ vout,
+                                                   uint32_t* err, int32_t* s_buf, int64_t* s_range) {
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
-    const int64_t d0 = (int64_t)blockIdx.x * kEmitTile;
-    if (dc) {   // device counts (k_emit_count set the entry count used)
-        nb = dc[4];
-        m = dc[kCntCoarseUsed];
-        if (d0 >= m) return;
-    }
+    const int64_t d0 = blk * kEmitTile;
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
-    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blockIdx.x, sorted_f, cs, blk_first, srect, grid, s_buf,
-                                                    s_range, tile, val);
+    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blk, sorted_f, cs, blk_first, srect, grid, s_buf, s_range,
+                                                    tile, val);
     uint16_t key[kEmitSortItems];
     int32_t v[kEmitSortItems];
     bool valid[kEmitSortItems];
@@ -668,8 +668,36 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
 #pragma unroll
     for (int k = 0; k < kEmitSortItems; ++k) v[k] = s_buf[emit_sort_slot(w * (kEmitSortItems * kWave) + k * kWave + lane)];
     // (rs_scatter_tile reuses s_buf for its staging after its first barrier)
-    rs_scatter_tile<uint16_t>(key, v, valid, blockIdx.x, m, 0, nbits0, offsets, totals, count_tiles, kout, vout, err,
-                              nullptr, reinterpret_cast<uint32_t*>(s_buf));
+    rs_scatter_tile<uint16_t>(key, v, valid, blk, m, 0, nbits0, offsets, totals, count_tiles, kout, vout, err, nullptr,
+                              reinterpret_cast<uint32_t*>(s_buf));
+}
+
+// LOOP: a capped grid walks the emission blocks blockIdx.x, + gridDim.x, ... (a device-count
+// render whose capacity-sized block count exceeds the cap; the loop costs registers: 134
+// VGPRs against 73, so the grid is one block per workgroup otherwise).
+template <bool LOOP>
+__global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
+    int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
+    const int32_t* __restrict__ blk_first, const int4* __restrict__ srect, EmitGrid grid, int nbits0,
+    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, int64_t count_tiles,
+    uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err, const int64_t* dc) {
+    __shared__ int32_t s_buf[kEmitTile + 1];
+    __shared__ int64_t s_range[2];
+    if (dc) {   // device counts (k_emit_count set the entry count used)
+        nb = dc[4];
+        m = dc[kCntCoarseUsed];
+    }
+    if (!LOOP) {
+        if ((int64_t)blockIdx.x * kEmitTile < m)
+            emit_scatter_block(blockIdx.x, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals,
+                               count_tiles, kout, vout, err, s_buf, s_range);
+        return;
+    }
+    for (int64_t blk = blockIdx.x; blk * kEmitTile < m; blk += gridDim.x) {
+        emit_scatter_block(blk, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals, count_tiles, kout,
+                           vout, err, s_buf, s_range);
+        __syncthreads();   // s_buf is reused by the next block
+    }
 }
 
 // fill_df2dgs_codes_and_dfgidx_to_fgidx_kernel! (forward_core.jl:531-603): reference
@@ -1763,26 +1791,42 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     uint16_t* c16 = reinterpret_cast<uint16_t*>(buf->keys);
     uint16_t* c16_alt = c16 + kc;
     const EmitGrid cg{bg.nbx, bg.sx, bg.sy};
-    const unsigned egrid = (unsigned)ceil_div(mb, kEmitTile);
+    // (with device counts the blocks are bounded by the key capacity; a capped grid walks them)
+    constexpr int64_t kEmitMaxGrid = 4096;
+    const int64_t eblocks = ceil_div(mb, kEmitTile);
+    const unsigned egrid = (unsigned)(dc && eblocks > kEmitMaxGrid ? kEmitMaxGrid : eblocks);
     const int64_t count_tiles = radix_tiles<uint16_t>(mb);
     uint32_t* table = radix_count_table(r.rtemp);
     uint32_t* totals = radix_totals(r.rtemp, mb);
     const int64_t* d_used = dc ? dc + kCntCoarseUsed : nullptr;
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
-        k_emit_count<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg,
-                                                        nbits0, table, count_tiles, dc, kc,
-                                                        one_pass ? r.tile_totals : nullptr, one_pass ? r.ntt : 0);
+        if ((int64_t)egrid < eblocks)
+            k_emit_count<true><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg,
+                                                                  nbits0, table, count_tiles, dc, kc,
+                                                                  one_pass ? r.tile_totals : nullptr, one_pass ? r.ntt : 0);
+        else
+            k_emit_count<false><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg,
+                                                                   nbits0, table, count_tiles, dc, kc,
+                                                                   one_pass ? r.tile_totals : nullptr,
+                                                                   one_pass ? r.ntt : 0);
         TDGS_LAUNCHED();
     }
     {
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
-        k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals);
+        k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals, d_used, kEmitTile);
         TDGS_LAUNCHED();
-        k_emit_scatter<<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
-                                                          cg, nbits0, table, totals, count_tiles,
-                                                          one_pass ? c16 : c16_alt,
-                                                          one_pass ? buf->values : buf->sorted_values, d_err, dc);
+        if ((int64_t)egrid < eblocks)
+            k_emit_scatter<true><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
+                                                                    cg, nbits0, table, totals, count_tiles,
+                                                                    one_pass ? c16 : c16_alt,
+                                                                    one_pass ? buf->values : buf->sorted_values, d_err, dc);
+        else
+            k_emit_scatter<false><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
+                                                                     cg, nbits0, table, totals, count_tiles,
+                                                                     one_pass ? c16 : c16_alt,
+                                                                     one_pass ? buf->values : buf->sorted_values, d_err,
+                                                                     dc);
         TDGS_LAUNCHED();
         if (!one_pass)
             TDGS_TRY(radix_sort_pairs<uint16_t>(c16_alt, c16, buf->sorted_values, buf->values, c16_alt,

@@ -129,17 +129,27 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_count(const K* __restrict__ k
                                                          int nbits, uint32_t* __restrict__ counts, int64_t tiles,
                                                          const int64_t* d_n, int drop_max) {
     __shared__ uint32_t s_h[kRsBins];
+    // (tiles past a device count hold no keys; the row scan skips their columns)
+    if (d_n && (int64_t)blockIdx.x * RsTile<K>::kTile >= *d_n) return;
     tile_digit_histogram(keys, d_n ? (*d_n < n ? *d_n : n) : n, blockIdx.x, shift, nbits, s_h, drop_max != 0);
     if (threadIdx.x < kRsBins) counts[rs_entry(threadIdx.x, blockIdx.x, tiles)] = s_h[threadIdx.x];
 }
 
 // Workgroup d: exclusive prefix of digit d's counts over the tiles (in tile order), in place,
-// total to totals[d].
-static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restrict__ counts, int64_t tiles,
-                                                             uint32_t* __restrict__ totals) {
+// total to totals[d]. With d_n (device count, may be null), only the tiles holding the first
+// *d_n keys (tile_keys per tile) are scanned: the table's other columns are neither written
+// by the counts nor read by the scatter.
+static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restrict__ counts, int64_t tiles_all,
+                                                             uint32_t* __restrict__ totals,
+                                                             const int64_t* d_n = nullptr, int tile_keys = 1) {
     __shared__ uint32_t s_tmp[4];
-    uint32_t* const row0 = counts + (int64_t)blockIdx.x * rs_pitch(tiles);
-    const int64_t per = rs_pitch(tiles) / kXcds;
+    uint32_t* const row0 = counts + (int64_t)blockIdx.x * rs_pitch(tiles_all);
+    const int64_t per = rs_pitch(tiles_all) / kXcds;
+    int64_t tiles = tiles_all;
+    if (d_n) {
+        const int64_t used = (*d_n + tile_keys - 1) / tile_keys;
+        if (used < tiles) tiles = used > 0 ? used : 0;
+    }
     // entry of tile i in the row
     auto at = [&](int64_t i) -> uint32_t& { return row0[(i % kXcds) * per + i / kXcds]; };
     const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
@@ -442,7 +452,7 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
             k_rs_count<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, n, shift, nbits, table, tiles, d_n, drop);
             TDGS_LAUNCHED();
         }
-        k_rs_scan_rows<<<kRsBins, 256, 0, stream>>>(table, tiles, totals);
+        k_rs_scan_rows<<<kRsBins, 256, 0, stream>>>(table, tiles, totals, d_n, RsTile<K>::kTile);
         TDGS_LAUNCHED();
         k_rs_scatter<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, src_v, dk, dv, n, shift, nbits, table,
                                                                      totals, tiles, err, d_n, drop,
