@@ -331,6 +331,47 @@ def render_other_tiling(core, w, g, tile, frames=240, warmup=10):
             "stage_ms": {STAGES[i]: round(ms[i] / cnt[i], 4) for i in range(13) if cnt[i] > 0}}
 
 
+def render_in_flight(core, g, cams, tiling, opts, key_capacity, frames, streams):
+    """The headline frames with `streams` frames in flight: frame k is rendered on stream
+    k % streams with that stream's own library context, render buffers and outputs (a
+    context holds the device counters of one frame at a time), without host synchronisation.
+    While one frame's sort chain (short, latency-bound launches) runs, another frame's
+    blending fills the rest of the GPU. Wall-clock frames/s over all streams."""
+    import torch
+    ncam = len(cams)
+    ctxs = [core.Context(0) for _ in range(streams)]
+    strs = [torch.cuda.Stream() for _ in range(streams)]
+    outs = [core.RenderOutputs.for_camera(cams[0], 0, include_rgb=True, include_transmittance=True,
+                                          include_depth=False, include_last_contributing_indices=False)
+            for _ in range(streams)]
+    bufs = [core.RenderBuffers(len(g), tiling, 0, key_capacity) for _ in range(streams)]
+    mons = []
+    for c in ctxs:
+        p = C.POINTER(C.c_int64)()
+        core.check(core.lib().tdgs_ctx_frame_monitor(c.handle, C.byref(p)))
+        mons.append(p)
+    torch.cuda.synchronize()
+
+    def run(k0, k1):
+        for k in range(k0, k1):
+            s = k % streams
+            with torch.cuda.stream(strs[s]):
+                core.render_(outs[s], g, cams[k % ncam], tiling, opts, bufs[s], device_counts=True, ctx=ctxs[s])
+
+    run(0, 4 * streams)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(0, frames)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    assert all(int(p[2]) == 0 for p in mons), "a frame's keys did not fit the key arrays"
+    assert sum(int(p[0]) for p in mons) == frames + 4 * streams
+    for c in ctxs:
+        c.close()
+    return {"streams": streams, "frames": frames, "frames_per_s": round(frames / dt, 2),
+            "ms_per_frame": round(dt * 1000.0 / frames, 4)}
+
+
 def stress_cfg4(core, repeats=5):
     """Config 4: 3M Gaussians at 3840x2160 (SH3, 16x32 tiles), forward and backward of one
     camera against a seeded uniform target; more than 100M duplicated keys."""
@@ -612,6 +653,8 @@ def main():
     core.check(L.tdgs_profile_end(ms, cnt))
     assert int(mon[2]) == overflows0, "a frame's keys did not fit the key arrays"
 
+    in_flight = [render_in_flight(core, g, cams, tiling, opts, buf.key_capacity, args.steps, s) for s in (2, 3)]
+
     st = frame_stats(core, g, cams, tiling, opts, buf, used)
     n = len(g)
     nf, nb, m, evals, evals_live, evals_contrib, evals_back, mc = st.mean(axis=0)
@@ -683,6 +726,7 @@ def main():
         "frames_per_s_host_counts": round(fps_sync, 2),
         "frame_ms_p50": round(float(np.percentile(frame_ms, 50)), 4),
         "frame_ms_p99": round(float(np.percentile(frame_ms, 99)), 4),
+        "frames_in_flight": in_flight,
         "mean_counts": {"filtered": round(nf), "nonempty": round(nb), "keys": round(m),
                         "blend_evaluations": round(evals), "blend_evaluations_live": round(evals_live),
                         "blend_evaluations_contributing": round(evals_contrib),

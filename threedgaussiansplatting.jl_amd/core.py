@@ -95,6 +95,33 @@ def context(device=0):
     return _CTX[device]
 
 
+class Context:
+    """A library context of its own (tdgs_ctx_create / tdgs_ctx_destroy). The context holds
+    the device counters of the frame in progress, so frames rendered concurrently on several
+    streams each need their own context (and their own RenderBuffers and RenderOutputs);
+    the Gaussians may be shared. context(device) is the default one per device."""
+
+    def __init__(self, device=0):
+        self.device = int(device)
+        self.handle = C.c_void_p()
+        check(lib().tdgs_ctx_create(self.device, C.byref(self.handle)))
+
+    def close(self):
+        if self.handle:
+            check(lib().tdgs_ctx_destroy(self.handle))
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _handle(ctx, device):
+    return context(device) if ctx is None else ctx.handle
+
+
 def _dev(device):
     return torch.device("cuda", int(device))
 
@@ -303,14 +330,18 @@ class RenderBuffers:
 # ------------------------------------------------------------------------------------
 
 def render_(outputs: RenderOutputs, gaussians, camera: PinholeCamera, tiling: Tiling,
-            options: RenderOptions, buffers: RenderBuffers, device_counts: bool = False):
+            options: RenderOptions, buffers: RenderBuffers, device_counts: bool = False, ctx: Context = None):
     """render! (src/forward_core.jl:196-314). Grows the key buffers when needed.
 
     device_counts=True renders without synchronising with the host (TDGS_FLAG_DEVICE_COUNTS):
     buffers.nb_fgaussians and nb_keys become -1 and the counts stay on the device
     (buffers.frame_counts() reads them); the key arrays are not grown, and a frame whose keys
-    do not fit renders as render_void! with the status TDGS_FRAME_KEY_CAPACITY."""
+    do not fit renders as render_void! with the status TDGS_FRAME_KEY_CAPACITY.
+
+    ctx (a Context, default: the device's) and torch's current stream order the call: frames
+    in flight on several streams each use a Context of their own."""
     dev = gaussians.device.index
+    h = _handle(ctx, dev)
     buffers.ensure_capacity(len(gaussians))
     g = gaussians.struct()
     cam, t, o = camera.to_c(), tiling.to_c(), options.to_c()
@@ -318,7 +349,7 @@ def render_(outputs: RenderOutputs, gaussians, camera: PinholeCamera, tiling: Ti
     if device_counts:
         o.flags |= abi.TDGS_FLAG_DEVICE_COUNTS
         nbf, m = C.c_int32(0), C.c_int64(0)
-        check(lib().tdgs_render(context(dev), stream_ptr(dev), C.byref(g), C.byref(cam), C.byref(t), C.byref(o),
+        check(lib().tdgs_render(h, stream_ptr(dev), C.byref(g), C.byref(cam), C.byref(t), C.byref(o),
                                 C.byref(buffers.struct()), C.byref(out), C.byref(nbf), C.byref(m)))
         buffers.nb_fgaussians = -1
         buffers.nb_keys = -1
@@ -328,7 +359,7 @@ def render_(outputs: RenderOutputs, gaussians, camera: PinholeCamera, tiling: Ti
     m = C.c_int64(0)
     for _ in range(2):
         b = buffers.struct()
-        rc = lib().tdgs_render(context(dev), stream_ptr(dev), C.byref(g), C.byref(cam), C.byref(t),
+        rc = lib().tdgs_render(h, stream_ptr(dev), C.byref(g), C.byref(cam), C.byref(t),
                                C.byref(o), C.byref(b), C.byref(out), C.byref(nbf), C.byref(m))
         if rc == abi.TDGS_ERR_CAPACITY and m.value > buffers.key_capacity and m.value < 2**31 - 1:
             buffers._alloc_keys(int(m.value * 1.25) + 1024)
@@ -355,9 +386,9 @@ def project_(gaussians, camera: PinholeCamera, tiling: Tiling, options: RenderOp
     return buffers.nb_fgaussians
 
 
-def ctx_check(device=0):
+def ctx_check(device=0, ctx: Context = None):
     """tdgs_ctx_check: synchronise and raise on a device-side error flag of the context."""
-    check(lib().tdgs_ctx_check(context(device), stream_ptr(device)))
+    check(lib().tdgs_ctx_check(_handle(ctx, device), stream_ptr(device)))
 
 
 # ------------------------------------------------------------------------------------
