@@ -153,10 +153,15 @@ __global__ __launch_bounds__(256) void k_rect_diff(int64_t nbf, const int32_t* _
 // look-back over per-workgroup counts measured slower: the cross-workgroup status round
 // trips cost more than this pass.)
 constexpr int kKeepSub = 4;
+// It also clears zero[0, nzero) (16-byte aligned, nzero a multiple of 4: the frame's zeroed
+// scratch) for the sorts and scans that accumulate into it.
 __global__ __launch_bounds__(256) void k_keep_counts(KeepEval ev, int64_t n, int32_t* __restrict__ block_counts,
-                                                     int32_t* __restrict__ group_counts, int64_t nblocks) {
+                                                     int32_t* __restrict__ group_counts, int64_t nblocks,
+                                                     uint32_t* __restrict__ zero, int64_t nzero) {
     __shared__ int32_t s_cnt[kKeepSub][256 / kWave];
     const int t = threadIdx.x, lane = __lane_id(), wave = t / kWave;
+    for (int64_t k = (int64_t)blockIdx.x * 256 + t; k < nzero / 4; k += (int64_t)gridDim.x * 256)
+        reinterpret_cast<uint4*>(zero)[k] = make_uint4(0u, 0u, 0u, 0u);
     float4 mv[kKeepSub];   // all loads in flight before any test
 #pragma unroll
     for (int k = 0; k < kKeepSub; ++k) {
@@ -569,8 +574,10 @@ __global__ __launch_bounds__(kEmitThreads) void k_emit_depth_order(
 
 // The 16-bit tile sort's first pass fused with key emission: emission blocks are radix tiles
 // (kEmitTile keys), generated twice instead of written and read back.
-//   k_emit_count:   the first-pass digit (low nbits0 bits of the tile id) histogram of each
-//                   block's keys, counts0[d][block], for k_rs_scan_rows;
+//   k_emit_count:   the first-pass digit (low nbits0 bits of the block id) histogram of each
+//                   block's keys: with group sums (grp), one row counts0[block][d] added into
+//                   its group's sums, from which every scatter workgroup takes its offsets;
+//                   else counts0[d][block] for k_rs_scan_rows;
 //   k_emit_scatter: the keys again, moved through LDS into the radix tile layout (wavefront
 //                   w, item k, lane l <-> key w 512 + k 64 + l), then rs_scatter_tile writes
 //                   tile ids and values straight to their first-pass sorted positions.
@@ -585,8 +592,9 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
                                                                  const int32_t* __restrict__ blk_first,
                                                                  const int4* __restrict__ srect, EmitGrid grid,
                                                                  int nbits0, uint32_t* __restrict__ counts0,
-                                                                 int64_t count_tiles, int64_t* dc, int64_t key_cap,
-                                                                 int32_t* zero, int64_t nzero) {
+                                                                 int64_t count_tiles, uint32_t* __restrict__ grp,
+                                                                 int64_t* dc, int64_t key_cap, int32_t* zero,
+                                                                 int64_t nzero) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
     __shared__ uint32_t s_h[kRsBins];
@@ -623,7 +631,15 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_count(int64_t nb, int
         for (int i = 0; i < kEmitSortItems; ++i)
             if (first + i < m) atomicAdd(&s_h[(uint32_t)tile[i] & mask0], 1u);
         __syncthreads();
-        if (t < kRsBins) counts0[rs_entry(t, blk, count_tiles)] = s_h[t];
+        if (t < kRsBins) {
+            const uint32_t c = s_h[t];
+            if (grp) {   // grouped tables: the block's row, added into its group's sums
+                counts0[blk * kRsBins + t] = c;
+                if (c) atomicAdd(&grp[(blk / kRsGroup) * kRsBins + t], c);
+            } else {
+                counts0[rs_entry(t, blk, count_tiles)] = c;
+            }
+        }
         __syncthreads();   // s_h and s_buf are reused by the next block
     }
 }
@@ -641,9 +657,10 @@ __device__ __forceinline__ void emit_scatter_block(int64_t blk, int64_t nb, int6
                                                    const int32_t* __restrict__ cs, const int32_t* __restrict__ blk_first,
                                                    const int4* __restrict__ srect, EmitGrid grid, int nbits0,
                                                    const uint32_t* __restrict__ offsets,
-                                                   const uint32_t* __restrict__ totals, int64_t count_tiles,
-                                                   uint16_t* __restrict__ kout, int32_t* __restrict__ vout,
-                                                   uint32_t* err, int32_t* s_buf, int64_t* s_range) {
+                                                   uint32_t* __restrict__ totals, int64_t count_tiles,
+                                                   const uint32_t* __restrict__ grp, uint16_t* __restrict__ kout,
+                                                   int32_t* __restrict__ vout, uint32_t* err, int32_t* s_buf,
+                                                   int64_t* s_range, uint32_t* s_part) {
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const int64_t d0 = blk * kEmitTile;
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
@@ -667,8 +684,16 @@ __device__ __forceinline__ void emit_scatter_block(int64_t blk, int64_t nb, int6
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kEmitSortItems; ++k) v[k] = s_buf[emit_sort_slot(w * (kEmitSortItems * kWave) + k * kWave + lane)];
+    uint32_t off_t = 0, total_t = 0;
+    if (grp) {
+        rs_group_offsets(offsets, grp, blk, (m + kEmitTile - 1) / kEmitTile, off_t, total_t, s_part);
+        if (blk == 0 && t < kRsBins) totals[t] = total_t;   // (the binning's block ends)
+    } else if (t < kRsBins) {
+        off_t = offsets[rs_entry(t, blk, count_tiles)];
+        total_t = totals[t];
+    }
     // (rs_scatter_tile reuses s_buf for its staging after its first barrier)
-    rs_scatter_tile<uint16_t>(key, v, valid, blk, m, 0, nbits0, offsets, totals, count_tiles, kout, vout, err, nullptr,
+    rs_scatter_tile<uint16_t>(key, v, valid, blk, m, 0, nbits0, off_t, total_t, kout, vout, err, nullptr,
                               reinterpret_cast<uint32_t*>(s_buf));
 }
 
@@ -679,23 +704,27 @@ template <bool LOOP>
 __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
     const int32_t* __restrict__ blk_first, const int4* __restrict__ srect, EmitGrid grid, int nbits0,
-    const uint32_t* __restrict__ offsets, const uint32_t* __restrict__ totals, int64_t count_tiles,
-    uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err, const int64_t* dc) {
+    const uint32_t* __restrict__ offsets, uint32_t* __restrict__ totals, int64_t count_tiles,
+    const uint32_t* __restrict__ grp, uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err,
+    const int64_t* dc) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
+    __shared__ uint32_t s_part[kRsBins];
     if (dc) {   // device counts (k_emit_count set the entry count used)
         nb = dc[4];
         m = dc[kCntCoarseUsed];
     }
+    // no entries: the digit totals are zero (with group sums nothing else writes them)
+    if (grp && m == 0 && blockIdx.x == 0 && threadIdx.x < kRsBins) totals[threadIdx.x] = 0;
     if (!LOOP) {
         if ((int64_t)blockIdx.x * kEmitTile < m)
             emit_scatter_block(blockIdx.x, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals,
-                               count_tiles, kout, vout, err, s_buf, s_range);
+                               count_tiles, grp, kout, vout, err, s_buf, s_range, s_part);
         return;
     }
     for (int64_t blk = blockIdx.x; blk * kEmitTile < m; blk += gridDim.x) {
-        emit_scatter_block(blk, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals, count_tiles, kout,
-                           vout, err, s_buf, s_range);
+        emit_scatter_block(blk, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals, count_tiles, grp,
+                           kout, vout, err, s_buf, s_range, s_part);
         __syncthreads();   // s_buf is reused by the next block
     }
 }
@@ -1635,6 +1664,21 @@ static int64_t scan_items(int64_t cap, const tdgs_tiling* t) {
     const int64_t nt = t ? (int64_t)t->nb_tiles_x * t->nb_tiles_y : 0;
     return cap > nt ? cap : nt;
 }
+// The frame's zeroed scratch (cleared by k_keep_counts): the depth sort's group sums (when
+// grouped), the emission pass's group sums (when grouped: decided by the key capacity) and
+// the count scan's tile sums (int64, accumulated by the depth sort's last pass).
+static int64_t depth_group_words(int64_t cap) {
+    return radix_tiles<uint32_t>(cap) <= kRsMaxGroupedTiles ? radix_group_words<uint32_t>(cap, 0, 32) : 0;
+}
+static int64_t emit_group_words(int64_t key_cap) {
+    const int64_t tiles = radix_tiles<uint16_t>(key_cap);
+    return tiles <= kRsMaxGroupedTiles ? rs_groups(tiles) * kRsBins : 0;
+}
+static_assert(kScanTile == (1 << kRsSumShift), "the depth sort sums the count scan's tiles");
+static int64_t zero_words(int64_t cap, int64_t key_cap) {
+    return (depth_group_words(cap) + emit_group_words(key_cap) + 2 * ceil_div(cap > 0 ? cap : 1, kScanTile) + 3) /
+           4 * 4;
+}
 static int64_t rect_diff_size(const tdgs_tiling* t) {
     return t ? (int64_t)(t->nb_tiles_x + 1) * (t->nb_tiles_y + 1) : 0;
 }
@@ -1660,6 +1704,7 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(t ? bin_geom(t).nblocks() : 0);                    // ends of the blocks' lists
     ar.template take<int32_t>(t ? ((int64_t)t->nb_tiles_x * t->nb_tiles_y + 3) / 4 * 4 : 0);   // tiles' totals
     ar.template take<int4>(cap);                                                  // rectangles in depth order
+    ar.template take<uint32_t>(zero_words(cap, key_cap));                         // zeroed each frame
 }
 
 // The scratch arrays of tdgs_render / tdgs_project inside buf->temp (render_layout's order).
@@ -1680,6 +1725,13 @@ struct RenderScratch {
     int32_t* tile_totals;
     int64_t ntt;   // entries of tile_totals (tiles, padded to 4)
     int4* srect;   // tile rectangles of the non-empty Gaussians in depth order
+    uint32_t* zero;   // the frame's zeroed scratch: dgrp, egrp, scan_sums
+    int64_t nzero;
+    uint32_t* dgrp;   // depth sort group sums (ndgrp words; 0: the sort is not grouped)
+    int64_t ndgrp;
+    uint32_t* egrp;   // emission pass group sums (negrp words; 0: not grouped)
+    int64_t negrp;
+    int64_t* scan_sums;   // count scan tile sums (kScanTile items each)
 };
 
 static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const tdgs_tiling* tiling) {
@@ -1711,6 +1763,13 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.ntt = tiling ? ((int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y + 3) / 4 * 4 : 0;
     r.tile_totals = ar.take<int32_t>(r.ntt);
     r.srect = ar.take<int4>(cap);
+    r.nzero = zero_words(cap, buf->key_capacity);
+    r.zero = ar.take<uint32_t>(r.nzero);
+    r.dgrp = r.zero;
+    r.ndgrp = depth_group_words(cap);
+    r.egrp = r.dgrp + r.ndgrp;
+    r.negrp = emit_group_words(buf->key_capacity);
+    r.scan_sums = reinterpret_cast<int64_t*>(r.egrp + r.negrp);
     return r;
 }
 
@@ -1748,7 +1807,8 @@ static int launch_keep_and_project(hipStream_t s, const tdgs_gaussians* g, const
     {
         StageScope sc(TDGS_STAGE_CULL_COMPACT, s);
         KeepEval ev{g->means_opacity, g->kind, *cam, *opt, buf->keep};
-        k_keep_counts<<<(unsigned)ngroups, 256, 0, s>>>(ev, n, r.block_counts, r.group_counts, nblocks);
+        k_keep_counts<<<(unsigned)ngroups, 256, 0, s>>>(ev, n, r.block_counts, r.group_counts, nblocks, r.zero,
+                                                         r.nzero);
         TDGS_LAUNCHED();
     }
     ProjectArgs pa;
@@ -1799,31 +1859,35 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     uint32_t* table = radix_count_table(r.rtemp);
     uint32_t* totals = radix_totals(r.rtemp, mb);
     const int64_t* d_used = dc ? dc + kCntCoarseUsed : nullptr;
+    // group sums (cleared at frame start) replace the row scan when the capacity allows
+    uint32_t* grp = r.negrp > 0 && count_tiles <= kRsMaxGroupedTiles ? r.egrp : nullptr;
     {
         StageScope sc(TDGS_STAGE_EMIT, s);
         if ((int64_t)egrid < eblocks)
             k_emit_count<true><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg,
-                                                                  nbits0, table, count_tiles, dc, kc,
+                                                                  nbits0, table, count_tiles, grp, dc, kc,
                                                                   one_pass ? r.tile_totals : nullptr, one_pass ? r.ntt : 0);
         else
             k_emit_count<false><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg,
-                                                                   nbits0, table, count_tiles, dc, kc,
+                                                                   nbits0, table, count_tiles, grp, dc, kc,
                                                                    one_pass ? r.tile_totals : nullptr,
                                                                    one_pass ? r.ntt : 0);
         TDGS_LAUNCHED();
     }
     {
         StageScope sc(TDGS_STAGE_TILE_SORT, s);
-        k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals, d_used, kEmitTile);
-        TDGS_LAUNCHED();
+        if (!grp) {
+            k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals, d_used, kEmitTile);
+            TDGS_LAUNCHED();
+        }
         if ((int64_t)egrid < eblocks)
             k_emit_scatter<true><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
-                                                                    cg, nbits0, table, totals, count_tiles,
+                                                                    cg, nbits0, table, totals, count_tiles, grp,
                                                                     one_pass ? c16 : c16_alt,
                                                                     one_pass ? buf->values : buf->sorted_values, d_err, dc);
         else
             k_emit_scatter<false><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
-                                                                     cg, nbits0, table, totals, count_tiles,
+                                                                     cg, nbits0, table, totals, count_tiles, grp,
                                                                      one_pass ? c16 : c16_alt,
                                                                      one_pass ? buf->values : buf->sorted_values, d_err,
                                                                      dc);
@@ -2096,19 +2160,24 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     int64_t* d_nb = ctx->d_counters + 4;
     {
         StageScope sc(TDGS_STAGE_DEPTH_SORT, s);
-        TDGS_TRY(radix_sort_pairs<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
-                                            rtemp, rbytes, s, nullptr, d_err, d_nb, nullptr,
-                                            RsGather{reinterpret_cast<const int4*>(buf->tile_ranges), r.srect}));
+        // (the last pass gathers the rectangles into depth order and, for the tile lists, sums
+        // their packed tile and block counts per scan tile)
+        const BinGeom bg = tile16 ? bin_geom(tiling) : BinGeom{};
+        TDGS_TRY(radix_sort_pairs_grouped<uint32_t>(
+            dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32, rtemp, rbytes, r.dgrp, r.ndgrp, s, d_err,
+            d_nb, nullptr,
+            RsGather{reinterpret_cast<const int4*>(buf->tile_ranges), r.srect, tile16 ? r.scan_sums : nullptr,
+                     bg.sx, bg.sy}));
     }
     if (tile16) {
         // 5: tiles and blocks touched, in depth order -> the blocks' entries (emission offsets)
-        // and M
+        // and M (the scan's tile sums come from the depth sort)
         const BinGeom bg = bin_geom(tiling);
         {
             StageScope sc(TDGS_STAGE_COUNT_SCAN, s);
             const SortedTileBlockCounts stb{r.srect, bg.sx, bg.sy, d_nb};
-            TDGS_TRY(device_scan(stb, stb, WriteBlockScan{WriteScanAndBlocks{cs, blk_first, nblk}}, n, stemp, sbytes,
-                                 ctx->d_counters + kCntCoarse, s, d_nb));
+            TDGS_TRY(device_scan_apply(stb, WriteBlockScan{WriteScanAndBlocks{cs, blk_first, nblk}}, n, r.scan_sums,
+                                       ctx->d_counters + kCntCoarse, s, d_nb));
         }
         if (device_counts) {
             // 6-8 sized by the key capacity; the blend copies the counts to the frame counts

@@ -1,6 +1,7 @@
 // scan.hpp — device-wide inclusive scan of int32 (or int64) items with int64 running sums
 // (replaces CUDA.jl's accumulate!(+) at src/forward_core.jl:231, 259 and
-// src/training.jl:384). Reduce-then-scan in two launches:
+// src/training.jl:384). Reduce-then-scan in two launches (or the second alone when the
+// producer of the items sums the tiles, device_scan_apply):
 //   1. each 2048-item tile reduces its items                      (k_scan_reduce)
 //   2. each tile sums the earlier tiles' sums into its offset and
 //      rescans its items; tile 0 also writes the total              (k_scan_apply)
@@ -123,6 +124,17 @@ int device_scan(In1 in_reduce, In2 in_apply, Out out, int64_t n, void* temp, siz
     TDGS_LAUNCHED();
     k_scan_apply<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in_apply, out, n, tile_sums, ntiles, d_total,
                                                                  d_limit);
+    TDGS_LAUNCHED();
+    return TDGS_OK;
+}
+
+// The apply pass alone, for a producer that has already summed the items of every kScanTile
+// tile into tile_sums (ceil(n / kScanTile) entries).
+template <class In, class Out>
+int device_scan_apply(In in, Out out, int64_t n, const int64_t* tile_sums, int64_t* d_total, hipStream_t stream,
+                      const int64_t* d_limit = nullptr) {
+    const int64_t ntiles = ceil_div(n > 0 ? n : 1, kScanTile);
+    k_scan_apply<<<(unsigned)ntiles, kScanThreads, 0, stream>>>(in, out, n, tile_sums, ntiles, d_total, d_limit);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }

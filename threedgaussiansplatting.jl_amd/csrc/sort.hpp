@@ -13,7 +13,14 @@
 // the row scan orders tiles by index, so equal digits keep their input order.
 //
 // The count of a pass can come from the kernel that produced the keys (the render pipeline
-// fuses it into key emission and projection), so a pass reads its keys once.
+// fuses it into key emission), so a pass reads its keys once.
+//
+// Grouped variant (radix_sort_pairs_grouped, up to kRsMaxGroupedTiles tiles): two launches a
+// pass. The count writes each tile's histogram as one contiguous row (cnt[tile][digit]) and
+// adds it into the sums of its group of kRsGroup tiles (grp[group][digit], 16 atomics per
+// word); each scatter workgroup then finds its own offsets by summing the earlier groups'
+// sums and the earlier tiles of its group (at most G + 15 loads per digit, all in flight at
+// once) instead of waiting for a scan launch. The group sums must be zero on entry.
 // Decoupled look-back (Onesweep, Adinets & Merrill 2022) replaces the count and scan
 // launches by a chained prefix over tiles; on this part it was measured slower: with
 // ~800 tiles in flight the walk back to a published prefix takes several dependent
@@ -198,18 +205,48 @@ static __global__ __launch_bounds__(256) void k_rs_scan_rows(uint32_t* __restric
 // count sets *err instead of writing out of bounds). When d_kept is not null, tile 0 writes
 // the number of keys sorted in all. When gather.src is not null, each written value v (a
 // 1-based index) also moves gather.src[v - 1] to gather.dst at the value's output index.
+// With sums not null, every gathered rectangle r = (x0, y0, x1, y1) (1-based, inclusive) also
+// adds (its tile count << 32) | (the count of 2^sx x 2^sy tile blocks it touches) to
+// sums[i >> kRsSumShift] for its output index i (the tile sums of a scan of these packed counts
+// in output order, which then needs no reduce launch; sums zero on entry).
 struct RsGather {
     const int4* src;
     int4* dst;
+    int64_t* sums;
+    int sx, sy;
 };
+constexpr int kRsSumShift = 11;   // 2048 outputs per tile sum
 
+// Adds v of every lane whose key is >= 0 to dst[key]: one atomic per run of equal keys in
+// consecutive lanes (the run's sum from an inclusive scan over the wavefront).
+__device__ __forceinline__ void wave_run_add(int64_t key, int64_t v, int64_t* dst) {
+    const int lane = __lane_id();
+    const int64_t prev = __shfl_up(key, 1, kWave);
+    const bool head = lane == 0 || prev != key;
+    const uint64_t heads = __ballot(head);
+    int64_t incl = v;
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int64_t o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    const uint64_t upto = heads & ((2ull << lane) - 1ull);   // heads at or below this lane (lane 0 is one)
+    const int start = 63 - __clzll((long long)upto);
+    const int64_t before = __shfl(incl, start > 0 ? start - 1 : 0, kWave);
+    const bool tail = lane == kWave - 1 || ((heads >> (lane + 1)) & 1ull);
+    if (tail && key >= 0) {
+        const int64_t sum = incl - (start > 0 ? before : 0);
+        if (sum != 0) atomicAdd(reinterpret_cast<unsigned long long*>(dst + key), (unsigned long long)sum);
+    }
+}
+
+// off_t and total_t (read by the digit owners, threads t < kRsBins): the tile's offset inside
+// digit t's output (digit t's keys in earlier tiles) and digit t's total.
 template <class K>
 __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems], const int32_t (&val)[RsTile<K>::kItems],
                                                 const bool (&valid)[RsTile<K>::kItems], int64_t tile, int64_t n,
-                                                int shift, int nbits, const uint32_t* __restrict__ offsets,
-                                                const uint32_t* __restrict__ totals, int64_t tiles,
+                                                int shift, int nbits, uint32_t off_t, uint32_t total_t,
                                                 K* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err,
-                                                int64_t* d_kept, uint32_t* s_raw, RsGather gather = {nullptr, nullptr}) {
+                                                int64_t* d_kept, uint32_t* s_raw, RsGather gather = {}) {
     constexpr int kRsItems = RsTile<K>::kItems;
     constexpr int kRsTile = RsTile<K>::kTile;
     // Keys narrower than 32 bits are staged as 32-bit words: lanes storing 16-bit keys to
@@ -223,8 +260,6 @@ __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems
     __shared__ uint32_t s_tile_n;                 // keys of the tile that are sorted
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const bool owner = t < kRsBins;
-    const uint32_t total_t = owner ? totals[t] : 0u;
-    const uint32_t off_t = owner ? offsets[rs_entry(t, tile, tiles)] : 0u;
     for (int i = t; i < kRsWaves * kRsBins; i += kRsThreads) (&s_wh[0][0])[i] = 0;
     __syncthreads();
     const uint32_t mask = (1u << nbits) - 1u;
@@ -304,11 +339,20 @@ __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) {
         const int i = k * kRsThreads + t;
+        int64_t item = 0;
         if (opos[k] >= 0) {
             const int32_t v = s_val[i];
             vout[opos[k]] = v;
-            if (gather.src) gather.dst[opos[k]] = gather.src[v - 1];
+            if (gather.src) {
+                const int4 r = gather.src[v - 1];
+                gather.dst[opos[k]] = r;
+                const int32_t blocks = (((r.z - 1) >> gather.sx) - ((r.x - 1) >> gather.sx) + 1) *
+                                       (((r.w - 1) >> gather.sy) - ((r.y - 1) >> gather.sy) + 1);
+                item = ((int64_t)((r.z - r.x + 1) * (r.w - r.y + 1)) << 32) | (int64_t)blocks;
+            }
         }
+        // (consecutive lanes hold consecutive outputs of a digit's run: few runs per wavefront)
+        if (gather.sums) wave_run_add(opos[k] >= 0 ? (int64_t)(opos[k] >> kRsSumShift) : -1, item, gather.sums);
     }
 }
 
@@ -344,7 +388,106 @@ __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6)))
     }
 #pragma unroll
     for (int k = 0; k < kRsItems; ++k) valid[k] = wbase + k * kWave < nn && !(drop_max && key[k] == (K)~(K)0);
-    rs_scatter_tile<K>(key, val, valid, tile, n, shift, nbits, offsets, totals, tiles, kout, vout, err,
+    const bool owner = t < kRsBins;
+    rs_scatter_tile<K>(key, val, valid, tile, n, shift, nbits, owner ? offsets[rs_entry(t, tile, tiles)] : 0u,
+                       owner ? totals[t] : 0u, kout, vout, err, drop_max ? d_kept : nullptr, s_raw, gather);
+}
+
+// ---- grouped count tables ----------------------------------------------------------------
+constexpr int kRsGroup = 16;                    // radix tiles per group
+constexpr int64_t kRsMaxGroupedTiles = 4096;    // at most 256 groups: 256 + 15 loads per digit
+__host__ __device__ inline int64_t rs_groups(int64_t tiles) { return (tiles + kRsGroup - 1) / kRsGroup; }
+
+// Digit owners (t < kRsBins) get the offset of radix tile `tile` inside digit t's output (the
+// digit's keys in earlier tiles) and digit t's total over the first tiles_used tiles, from the
+// per-tile rows cnt[tile][digit] and the group sums grp[group][digit]; threads kRsBins..2
+// kRsBins-1 load the earlier tiles of the tile's own group. Ends with a block barrier.
+__device__ __forceinline__ void rs_group_offsets(const uint32_t* __restrict__ cnt, const uint32_t* __restrict__ grp,
+                                                 int64_t tile, int64_t tiles_used, uint32_t& off, uint32_t& tot,
+                                                 uint32_t* s_part) {
+    static_assert(kRsThreads == 2 * kRsBins, "one owner and one helper thread per digit");
+    const int t = threadIdx.x;
+    const int64_t g = tile / kRsGroup;
+    const int64_t groups = rs_groups(tiles_used);
+    constexpr int U = 8;
+    off = 0;
+    tot = 0;
+    if (t < kRsBins) {
+        for (int64_t q0 = 0; q0 < groups; q0 += U) {
+            uint32_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = q0 + u < groups ? grp[(q0 + u) * kRsBins + t] : 0u;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                tot += v[u];
+                if (q0 + u < g) off += v[u];
+            }
+        }
+    } else {
+        const int d = t - kRsBins;
+        uint32_t v[kRsGroup - 1];
+#pragma unroll
+        for (int u = 0; u < kRsGroup - 1; ++u) {
+            const int64_t q = g * kRsGroup + u;
+            v[u] = q < tile ? cnt[q * kRsBins + d] : 0u;
+        }
+        uint32_t in = 0;
+#pragma unroll
+        for (int u = 0; u < kRsGroup - 1; ++u) in += v[u];
+        s_part[d] = in;
+    }
+    __syncthreads();
+    if (t < kRsBins) off += s_part[t];
+}
+
+// Per-tile histogram as a row of cnt, added into its group's sums (d_n, drop_max: as k_rs_count).
+template <class K>
+__global__ __launch_bounds__(kRsThreads) void k_rs_count_grouped(const K* __restrict__ keys, int64_t n, int shift,
+                                                                 int nbits, uint32_t* __restrict__ cnt,
+                                                                 uint32_t* __restrict__ grp, const int64_t* d_n,
+                                                                 int drop_max) {
+    __shared__ uint32_t s_h[kRsBins];
+    if (d_n && (int64_t)blockIdx.x * RsTile<K>::kTile >= *d_n) return;
+    tile_digit_histogram(keys, d_n ? (*d_n < n ? *d_n : n) : n, blockIdx.x, shift, nbits, s_h, drop_max != 0);
+    if (threadIdx.x < kRsBins) {
+        const uint32_t c = s_h[threadIdx.x];
+        cnt[(int64_t)blockIdx.x * kRsBins + threadIdx.x] = c;
+        if (c) atomicAdd(&grp[(int64_t)(blockIdx.x / kRsGroup) * kRsBins + threadIdx.x], c);
+    }
+}
+
+// The scatter with offsets from the grouped tables (arguments as k_rs_scatter's).
+template <class K>
+__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(6))) void k_rs_scatter_grouped(
+    const K* __restrict__ kin, const int32_t* __restrict__ vin, K* __restrict__ kout,
+    int32_t* __restrict__ vout, int64_t n, int shift, int nbits, const uint32_t* __restrict__ cnt,
+    const uint32_t* __restrict__ grp, uint32_t* err, const int64_t* d_n, int drop_max, int64_t* d_kept,
+    RsGather gather) {
+    constexpr int kRsItems = RsTile<K>::kItems;
+    constexpr int kRsTile = RsTile<K>::kTile;
+    __shared__ uint32_t s_raw[rs_stage_words<K>()];
+    __shared__ uint32_t s_part[kRsBins];
+    const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
+    const int64_t tile = blockIdx.x;
+    if (d_n && *d_n < n) n = *d_n;
+    if (tile * kRsTile >= n) return;   // (uniform: past the keys)
+    const int32_t base = (int32_t)(tile * kRsTile);
+    const int32_t wbase = base + w * (kRsItems * kWave) + lane;
+    const int32_t nn = (int32_t)n;
+    K key[kRsItems];
+    int32_t val[kRsItems];
+    bool valid[kRsItems];
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) {
+        const int32_t i = wbase + k * kWave;
+        key[k] = i < nn ? kin[i] : (K)0;
+        val[k] = i < nn ? vin[i] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kRsItems; ++k) valid[k] = wbase + k * kWave < nn && !(drop_max && key[k] == (K)~(K)0);
+    uint32_t off_t, total_t;
+    rs_group_offsets(cnt, grp, tile, (n + kRsTile - 1) / kRsTile, off_t, total_t, s_part);
+    rs_scatter_tile<K>(key, val, valid, tile, n, shift, nbits, off_t, total_t, kout, vout, err,
                        drop_max ? d_kept : nullptr, s_raw, gather);
 }
 
@@ -406,7 +549,7 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
                      int32_t* alt_v, int64_t n, int begin_bit, int end_bit, void* temp,
                      size_t temp_bytes, hipStream_t stream, uint32_t* first_counts = nullptr,
                      uint32_t* err = nullptr, int64_t* kept_out = nullptr, const int64_t* d_count = nullptr,
-                     RsGather gather = {nullptr, nullptr}) {
+                     RsGather gather = {}) {
     const int passes = radix_passes(begin_bit, end_bit);
     const int width = radix_digit_bits(begin_bit, end_bit);
     if (n <= 0) return TDGS_OK;
@@ -457,7 +600,61 @@ int radix_sort_pairs(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K
         k_rs_scatter<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, src_v, dk, dv, n, shift, nbits, table,
                                                                      totals, tiles, err, d_n, drop,
                                                                      drop ? kept_out : nullptr,
-                                                                     p == passes - 1 ? gather : RsGather{nullptr, nullptr});
+                                                                     p == passes - 1 ? gather : RsGather{});
+        TDGS_LAUNCHED();
+        src_k = dk;
+        src_v = dv;
+    }
+    return TDGS_OK;
+}
+
+// Words of group sums radix_sort_pairs_grouped needs for n keys sorted on [begin_bit, end_bit).
+template <class K>
+inline int64_t radix_group_words(int64_t n, int begin_bit, int end_bit) {
+    return (int64_t)radix_passes(begin_bit, end_bit) * rs_groups(radix_tiles<K>(n)) * kRsBins;
+}
+
+// radix_sort_pairs (same arguments, without first_counts) with the grouped count tables: a
+// count and a scatter launch per pass. zgrp holds radix_group_words<K>(n, ...) words that are
+// zero on entry (an earlier launch on the stream clears them); they hold the group sums after.
+// Sorts of more than kRsMaxGroupedTiles tiles, or with too few words in zgrp, take
+// radix_sort_pairs' path (zgrp unused).
+template <class K>
+int radix_sort_pairs_grouped(const K* kin, K* kout, const int32_t* vin, int32_t* vout, K* alt_k, int32_t* alt_v,
+                             int64_t n, int begin_bit, int end_bit, void* temp, size_t temp_bytes, uint32_t* zgrp,
+                             int64_t zgrp_words, hipStream_t stream, uint32_t* err = nullptr,
+                             int64_t* kept_out = nullptr, const int64_t* d_count = nullptr, RsGather gather = {}) {
+    const int passes = radix_passes(begin_bit, end_bit);
+    const int width = radix_digit_bits(begin_bit, end_bit);
+    const int64_t tiles = radix_tiles<K>(n);
+    const int64_t gwords = rs_groups(tiles) * kRsBins;
+    if (n <= 0) return TDGS_OK;
+    if (passes == 0 || n > (int64_t)INT32_MAX || tiles > kRsMaxGroupedTiles || zgrp == nullptr ||
+        zgrp_words < passes * gwords)
+        return radix_sort_pairs<K>(kin, kout, vin, vout, alt_k, alt_v, n, begin_bit, end_bit, temp, temp_bytes,
+                                   stream, nullptr, err, kept_out, d_count, gather);
+    if (temp_bytes < radix_temp_bytes(n) || temp == nullptr) {
+        set_error("radix sort scratch too small (%zu bytes for %lld keys)", temp_bytes, (long long)n);
+        return TDGS_ERR_CAPACITY;
+    }
+    uint32_t* cnt = (uint32_t*)temp;   // tiles x kRsBins <= the count table's size
+    if (!err) err = radix_totals(temp, n) + kRsBins;
+    const K* src_k = kin;
+    const int32_t* src_v = vin;
+    for (int p = 0; p < passes; ++p) {
+        const int shift = begin_bit + width * p;
+        const int nbits = end_bit - shift < width ? end_bit - shift : width;
+        const bool to_out = ((passes - 1 - p) % 2) == 0;
+        K* dk = to_out ? kout : alt_k;
+        int32_t* dv = to_out ? vout : alt_v;
+        uint32_t* grp = zgrp + p * gwords;
+        const int64_t* d_n = kept_out ? (p > 0 ? kept_out : nullptr) : d_count;
+        const int drop = (kept_out && p == 0) ? 1 : 0;
+        k_rs_count_grouped<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(src_k, n, shift, nbits, cnt, grp, d_n, drop);
+        TDGS_LAUNCHED();
+        k_rs_scatter_grouped<K><<<(unsigned)tiles, kRsThreads, 0, stream>>>(
+            src_k, src_v, dk, dv, n, shift, nbits, cnt, grp, err, d_n, drop, drop ? kept_out : nullptr,
+            p == passes - 1 ? gather : RsGather{});
         TDGS_LAUNCHED();
         src_k = dk;
         src_v = dv;
