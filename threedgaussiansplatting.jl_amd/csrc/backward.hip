@@ -153,17 +153,30 @@ struct BackBlendArgs {
 
 // SEP: the 2D gradients are the reference's four arrays (component addresses by select);
 // otherwise the interleaved 9 x capacity array (base[0] + 9 f + k).
-template <bool SEP>
-__global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
+// PX pixels per lane: lane l of wavefront w takes pixels 64 PX w + 64 p + l, p < PX, of the
+// tile (NB = blockDim.x = NT / PX rounded up to whole wavefronts; a pixel index past NT is
+// off), so the per-entry record reads, votes, slot bookkeeping and transpose-sum serve 64 PX
+// pixels per wavefront; with tiles of 8 x 8 pixel blocks a wavefront holds PX consecutive
+// blocks. A batch holds NB entries. Four pixels per lane at four wavefronts per SIMD (128
+// VGPRs; a few per-batch values go to scratch) measured 345 us against 378 us for two pixels
+// per lane at 1M Gaussians, 1080p (three wavefronts per SIMD at 142 VGPRs: 365 us).
+constexpr int kBackPx = 4;
+// PW: per-wavefront copies of the LDS sums (workgroups of at most kBackPwThreads threads; the
+// copies grow with the square of the workgroup size), else one copy shared by LDS atomics.
+constexpr int kBackPwThreads = 256;
+template <bool SEP, int PX, bool PW>
+__global__ __launch_bounds__(1024 / kBackPx) __attribute__((amdgpu_waves_per_eu(4))) void k_backward_blend(
+    BackBlendArgs a) {
     extern __shared__ float4 s_raw4[];
-    // Two pixels per lane: thread t takes pixels t and t + NB of the tile (NB = blockDim.x =
-    // NT / 2 rounded up to whole wavefronts; a pixel index past NT is off), so the per-entry
-    // record reads, votes, slot bookkeeping and transpose-sum serve 128 pixels per wavefront.
-    // A batch holds NB entries.
     const int NT = a.TW * a.TH;
     const int NB = (int)blockDim.x;
     BackRec* s_rec = reinterpret_cast<BackRec*>(s_raw4);
-    float* s_acc = reinterpret_cast<float*>(s_rec + NB);  // [NB][9]
+    // PW: per-wavefront sums [wave][NB][9]. A wavefront takes each entry into at most one
+    // slot, so its transposed sums are plain stores (an LDS atomic's round trip sat in front of
+    // the next entry's record reads); the flush adds the wavefronts' copies.
+    const int NW = PW ? NB / kWave : 1;
+    float* s_acc = reinterpret_cast<float*>(s_rec + NB);
+    float* s_accw = PW ? s_acc + (threadIdx.x / kWave) * (NB * 9) : s_acc;
     __shared__ int s_max_last;
     const int t = threadIdx.x;
     const int lane = __lane_id();
@@ -180,12 +193,12 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
     if (beg < 0) beg = 0;
     if (beg > end) beg = end;
 
-    float T[2], gpsi[2], g[2][3], cu[2], cv[2];
-    int32_t last[2];
-    bool on[2];
+    float T[PX], gpsi[PX], g[PX][3], cu[PX], cv[PX];
+    int32_t last[PX];
+    bool on[PX];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const int q = t + p * NB;
+    for (int p = 0; p < PX; ++p) {
+        const int q = (t / kWave) * (kWave * PX) + p * kWave + (t % kWave);
         int u_in = 1, v_in = 1;
         if (q < NT) tile_pixel(q, a.TW, a.TH, &u_in, &v_in);
         const int U = u_in + (tx - 1) * a.TW, V = v_in + (ty - 1) * a.TH;
@@ -209,9 +222,12 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
     const int partner = comp == 0 ? lane + 1 : comp == 1 ? lane - 1 : lane;
     const float scale = comp == 4 ? -1.0f : (comp == 3 || comp == 5) ? -0.5f : 1.0f;
     // entries past the last contributor of every pixel of the wavefront / tile are skipped
-    const int wave_last = wave_max_i32(last[0] > last[1] ? last[0] : last[1]);
+    int lane_last = last[0];
+#pragma unroll
+    for (int p = 1; p < PX; ++p) lane_last = last[p] > lane_last ? last[p] : lane_last;
+    const int wave_last = wave_max_i32(lane_last);
     if (t == 0) s_max_last = 0;
-    for (int k = t; k < NB * 9; k += NB) s_acc[k] = 0.0f;
+    for (int k = t; k < NW * NB * 9; k += NB) s_acc[k] = 0.0f;
     __syncthreads();
     if (lane == 0) atomicMax(&s_max_last, wave_last);
     __syncthreads();
@@ -247,7 +263,9 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
         if (lo > beg) gather(lo - NB > beg ? lo - NB : beg, (int)(lo - (lo - NB > beg ? lo - NB : beg)));
         const int jtop = (int)((int64_t)wave_last - lo < nb ? (int64_t)wave_last - lo : nb);
         // entry jj of the batch is before pixel p's last contributor iff jj < last_rel[p]
-        const int last_rel[2] = {(int)((int64_t)last[0] - lo), (int)((int64_t)last[1] - lo)};
+        int last_rel[PX];
+#pragma unroll
+        for (int p = 0; p < PX; ++p) last_rel[p] = (int)((int64_t)last[p] - lo);
         // Entries back to front; the 9 contributions of up to kSlots consecutive contributing
         // entries are kept per lane and summed over the wavefront in one transpose-sum, after
         // which lane l holds component l % 9 of slot l / 9 and adds it to the tile's LDS sum.
@@ -265,11 +283,11 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
                     const int jj = j--;
                     const float4 ra = s_rec[jj].a, rb = s_rec[jj].b;
                     const float2 rc = *reinterpret_cast<const float2*>(&s_rec[jj].c);
-                    float du[2], dv[2], x[2];
-                    bool live[2];
-                    uint64_t any = 0;
+                    float du[PX], dv[PX], x[PX];
+                    bool live[PX];
+                    uint64_t any[PX], any_all = 0;
 #pragma unroll
-                    for (int p = 0; p < 2; ++p) {
+                    for (int p = 0; p < PX; ++p) {
                         du[p] = cu[p] - ra.x;
                         dv[p] = cv[p] - ra.y;
                         x[p] = fmaf(fmaf(ra.z, du[p], ra.w * dv[p]), du[p], rb.x * dv[p] * dv[p]);
@@ -278,12 +296,23 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
                         live[p] = before & above;
                         // the vote as masks of the two compares (the mask of their conjunction
                         // takes two more instructions)
-                        any |= __builtin_amdgcn_ballot_w64(before) & __builtin_amdgcn_ballot_w64(above);
+                        any[p] = __builtin_amdgcn_ballot_w64(before) & __builtin_amdgcn_ballot_w64(above);
+                        any_all |= any[p];
                     }
-                    if (any == 0) continue;
+                    if (any_all == 0) continue;
                     const float c[3] = {rb.w, rc.x, rc.y};
 #pragma unroll
-                    for (int p = 0; p < 2; ++p) {
+                    for (int p = 0; p < PX; ++p) {
+                        // A pixel slot no lane of the wavefront is live in is skipped as a whole
+                        // (a wave-uniform branch): its steps would leave T, g . psi and the sums
+                        // unchanged. When it is the first slot, the others add to zeroed sums.
+                        if (any[p] == 0) {
+                            if (p == 0) {
+#pragma unroll
+                                for (int k = 0; k < 9; ++k) o[k] = 0.0f;
+                            }
+                            continue;
+                        }
                         // G by the hardware base-2 exponential (v_exp_f32, ~1 ulp over the whole
                         // float range): the gradients are checked at relative L2, and the forward
                         // pass's bit-exact exp_f decides the contributors
@@ -324,7 +353,12 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
             const float2 m2 = *reinterpret_cast<const float2*>(&s_rec[je].d);   // M21 M22
             const float mixed = fmaf(comp == 0 ? m11 : m2.y, sum, m2.x * other);
             const float val = comp < 2 ? mixed : sum * scale;
-            if (lane < 9 * kSlots && jl >= 0) atomicAdd(&s_acc[9 * jl + comp], val);
+            if (lane < 9 * kSlots && jl >= 0) {
+                if (PW)
+                    s_accw[9 * jl + comp] = val;
+                else
+                    atomicAdd(&s_accw[9 * jl + comp], val);
+            }
         }
         __syncthreads();
         // Flush with lane i on component i % 9 of entry i / 9: one atomic instruction covers
@@ -333,9 +367,17 @@ __global__ __launch_bounds__(512) void k_backward_blend(BackBlendArgs a) {
         for (int i = t; i < 9 * nb; i += NB) {
             int ii = i;
             asm volatile("" : "+v"(ii));   // (keeps the element index 32-bit: no 64-bit induction variables)
-            const float v = s_acc[ii];
+            float v = 0.0f;
+            bool nz = false;
+            for (int w = 0; w < NW; ++w) {
+                const float x = s_acc[w * (NB * 9) + ii];
+                v += x;
+                nz |= x != 0.0f;
+            }
+            if (nz) {
+                for (int w = 0; w < NW; ++w) s_acc[w * (NB * 9) + ii] = 0.0f;
+            }
             if (v != 0.0f) {
-                s_acc[ii] = 0.0f;
                 const int e = ii / 9, k = ii - 9 * e;
                 const int32_t f = __builtin_bit_cast(int32_t, s_rec[e].c.z);
                 unsafeAtomicAdd(SEP ? a.g2.at_dynamic(k, f) : a.g2.base[0] + (9 * (int64_t)f + k), v);
@@ -732,14 +774,23 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
     a.m = buf->key_capacity;
     a.tiles_end = buf->tiles_end; a.sorted_f = buf->sorted_values; a.f2d = buf->f2d;
     a.rgb_grad = rgb_grad; a.T = out->T; a.last = out->last; a.g2 = g2v;
-    // two pixels per thread, in whole wavefronts (the transpose-sum reads all 64 lanes; the
-    // pixels past the tile's are off)
-    const int nt = ((tiling->tile_width * tiling->tile_height + 1) / 2 + kWave - 1) / kWave * kWave;
-    const size_t lds = (size_t)nt * (sizeof(BackRec) + 9 * sizeof(float));
-    if (grads->grads2d)
-        k_backward_blend<false><<<dim3(tiling->nb_tiles_x, tiling->nb_tiles_y), nt, lds, s>>>(a);
-    else
-        k_backward_blend<true><<<dim3(tiling->nb_tiles_x, tiling->nb_tiles_y), nt, lds, s>>>(a);
+    // kBackPx pixels per thread, in whole wavefronts (the transpose-sum reads all 64 lanes;
+    // the pixels past the tile's are off)
+    const int nt = ((tiling->tile_width * tiling->tile_height + kBackPx - 1) / kBackPx + kWave - 1) / kWave * kWave;
+    const bool pw = nt <= kBackPwThreads;
+    const size_t lds = (size_t)nt * (sizeof(BackRec) + (size_t)(pw ? nt / kWave : 1) * 9 * sizeof(float));
+    const dim3 grid(tiling->nb_tiles_x, tiling->nb_tiles_y);
+    if (grads->grads2d) {
+        if (pw)
+            k_backward_blend<false, kBackPx, true><<<grid, nt, lds, s>>>(a);
+        else
+            k_backward_blend<false, kBackPx, false><<<grid, nt, lds, s>>>(a);
+    } else {
+        if (pw)
+            k_backward_blend<true, kBackPx, true><<<grid, nt, lds, s>>>(a);
+        else
+            k_backward_blend<true, kBackPx, false><<<grid, nt, lds, s>>>(a);
+    }
     TDGS_LAUNCHED();
     return TDGS_OK;
 }

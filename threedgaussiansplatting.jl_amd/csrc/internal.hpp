@@ -141,7 +141,7 @@ inline int check_tiling(const tdgs_tiling* t, const tdgs_camera* cam) {
     TDGS_REQUIRE(t && cam, "null tiling or camera");
     TDGS_REQUIRE(t->tile_width > 0 && t->tile_height > 0, "bad tile size");
     // any tile shape the reference's Tiling accepts (forward_structs.jl:340-424) whose pixels fit
-    // one workgroup: the kernels run one thread per pixel (two in the backward pass)
+    // one workgroup: the kernels run one thread per pixel (one per four in the backward pass)
     const int64_t nt = (int64_t)t->tile_width * t->tile_height;
     TDGS_REQUIRE(nt <= 1024, "tile of %lld pixels: at most 1024 are supported", (long long)nt);
     TDGS_REQUIRE(cam->width > 0 && cam->height > 0, "bad image size");
