@@ -1083,43 +1083,58 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
     }
 }
 
-// One workgroup: tiles_end = inclusive scan of the tiles' totals (each thread a contiguous run
-// of 4k tiles, read as int4). The total must equal the key count M (*expect, or
+// One workgroup: tiles_end = inclusive scan of the tiles' totals, 4096 tiles per step (four
+// per thread, read as int4 from the array padded to 4k and written as int4 where all four are
+// tiles and tiles_end is 16-byte aligned), with a running carry. The total must equal the key count M (*expect, or
 // expect_value; else *err is set: the lists would be incomplete).
 __global__ __launch_bounds__(1024) void k_bin_scan(const int32_t* __restrict__ totals, int32_t nt,
                                                    int32_t* __restrict__ tiles_end, const int64_t* expect,
                                                    int64_t expect_value, uint32_t* err) {
-    __shared__ int64_t s_w[1024 / kWave];
+    __shared__ int64_t s_w[2][1024 / kWave];
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
-    const int per = ((nt + 1023) / 1024 + 3) & ~3;
-    const int lo = t * per;
-    int64_t sum = 0;
-#pragma unroll 4
-    for (int k = 0; k < per; k += 4) {
-        if (lo + k < nt) {
-            const int4 v = *reinterpret_cast<const int4*>(totals + lo + k);   // (the array is padded to 4k)
-            sum += (int64_t)(lo + k < nt ? v.x : 0) + (lo + k + 1 < nt ? v.y : 0) + (lo + k + 2 < nt ? v.z : 0) +
-                   (lo + k + 3 < nt ? v.w : 0);
+    int64_t carry = 0;
+    int step = 0;
+    for (int base = 0; base < nt; base += 4096, step ^= 1) {
+        const int i = base + 4 * t;
+        int4 v = make_int4(0, 0, 0, 0);
+        if (i < nt) {
+            v = *reinterpret_cast<const int4*>(totals + i);
+            if (i + 1 >= nt) v.y = 0;
+            if (i + 2 >= nt) v.z = 0;
+            if (i + 3 >= nt) v.w = 0;
+        }
+        const int64_t sum = (int64_t)v.x + v.y + v.z + v.w;
+        int64_t incl = sum;
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int64_t o = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += o;
+        }
+        if (lane == kWave - 1) s_w[step][w] = incl;   // (alternate buffers: one barrier a step)
+        __syncthreads();
+        int64_t off = carry, total = 0;
+        for (int k = 0; k < 1024 / kWave; ++k) {
+            const int64_t x = s_w[step][k];
+            if (k < w) off += x;
+            total += x;
+        }
+        carry += total;
+        if (i < nt) {
+            int4 e;
+            e.x = (int32_t)(off + incl - sum + v.x);
+            e.y = e.x + v.y;
+            e.z = e.y + v.z;
+            e.w = e.z + v.w;
+            if (i + 3 < nt && (reinterpret_cast<uintptr_t>(tiles_end) & 15) == 0) {
+                *reinterpret_cast<int4*>(tiles_end + i) = e;
+            } else {
+                tiles_end[i] = e.x;
+                if (i + 1 < nt) tiles_end[i + 1] = e.y;
+                if (i + 2 < nt) tiles_end[i + 2] = e.z;
+                if (i + 3 < nt) tiles_end[i + 3] = e.w;
+            }
         }
     }
-    int64_t incl = sum;
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int64_t o = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += o;
-    }
-    if (lane == kWave - 1) s_w[w] = incl;
-    __syncthreads();
-    int64_t off = 0, total = 0;
-    for (int k = 0; k < 1024 / kWave; ++k) {
-        if (k < w) off += s_w[k];
-        total += s_w[k];
-    }
-    int64_t run = off + incl - sum;
-    for (int i = lo; i < lo + per && i < nt; ++i) {
-        run += totals[i];
-        tiles_end[i] = (int32_t)run;
-    }
-    if (t == 0 && total != (expect ? *expect : expect_value)) atomicOr(err, 1u);
+    if (t == 0 && carry != (expect ? *expect : expect_value)) atomicOr(err, 1u);
 }
 
 // The sorted keys (tile << 32 | depth bits) of the tile lists: the tile of list entry i is the
