@@ -61,6 +61,9 @@ def parse():
     p.add_argument("--no-extra-configs", action="store_true",
                    help="skip the config 1 / 3 training and config 4 stress legs")
     p.add_argument("--cfg3-iterations", type=int, default=3000)
+    p.add_argument("--no-in-flight", action="store_true",
+                   help="skip the frames-in-flight legs (kernel profiles: their concurrent launches "
+                        "would mix into the single-stream kernel durations)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 10 device-to-device copies of 1 GiB (HBM counter calibration)")
     return p.parse_args()
@@ -448,11 +451,13 @@ def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles, mc=0):
         # non-empty; depth key + value slots of the culled
         return 44 * n + 12 * h * nb + (4 + 4 + 36 + 8) * nf + 20 * nb + 8 * (n - nf)
     if stage == "depth_sort":            # first pass over all N depth keys (count + scatter of the
-        # kept), three more over the N_b non-empty ones: count 4, scatter 8 in + 8 out
-        return 4 * n + 8 * n + 8 * nb + 3 * (4 + 16) * nb
-    if stage == "count_scan":            # sorted fgidx, their counts and rectangles in (reduce +
-        # apply: tiles and blocks per Gaussian), packed scan out
-        return 2 * (4 + 4 + 16) * nb + 8 * nb
+        # kept), three more over the N_b non-empty ones: count 4, scatter 8 in + 8 out; the last
+        # pass gathers each rectangle into depth order (16 in + 16 out; it also sums the count
+        # scan's tiles)
+        return 4 * n + 8 * n + 8 * nb + 3 * (4 + 16) * nb + 32 * nb
+    if stage == "count_scan":            # one pass: the rectangles in depth order in (tiles and
+        # blocks per Gaussian), the scan out
+        return (16 + 4) * nb
     if stage == "emit":                  # scan, fgidx, rectangle of the non-empty in (block ids counted)
         return (8 + 4 + 16) * nb
     if stage == "tile_sort":             # the same in again; (16-bit block id, 32-bit value) per entry out
@@ -476,17 +481,19 @@ def measured_traffic():
     return {k: v.get("bytes_per_launch") for k, v in t.get("kernels", {}).items()}
 
 
-# the counter-summary kernels of each survey row (sums of their per-launch bytes)
+# the counter-summary kernels of each survey row with their launches per frame (or step): the
+# row's bytes are the sum of per-launch bytes times launches (the depth presort runs its count
+# and scatter kernels once per 8-bit pass, four passes over the 32-bit depth keys)
 MEASURED_KERNELS = {
-    "K1_project": ["keep_counts", "project"],
-    "K2_scan_keys": ["count_scan_reduce", "count_scan_apply", "emit_count"],
-    "K3_K4_sort_ranges": ["depth_sort_count", "depth_sort_scatter", "coarse_sort_scatter", "block_ends",
-                          "bin_count", "bin_scan", "bin_write"],
-    "K5_blend": ["blend"],
-    "K6_backward_blend": ["backward_blend"],
-    "K7_backward_project": ["backward_project"],
-    "K8_adam": ["adam"],
-    "K7_K8_fused": ["backward_project_adam"],
+    "K1_project": [("keep_counts", 1), ("project", 1)],
+    "K2_scan_keys": [("count_scan_apply", 1), ("emit_count", 1)],
+    "K3_K4_sort_ranges": [("depth_sort_count", 4), ("depth_sort_scatter", 4), ("coarse_sort_scatter", 1),
+                          ("bin_count", 1), ("bin_scan", 1), ("bin_write", 1)],
+    "K5_blend": [("blend", 1)],
+    "K6_backward_blend": [("backward_blend", 1)],
+    "K7_backward_project": [("backward_project", 1)],
+    "K8_adam": [("adam", 1)],
+    "K7_K8_fused": [("backward_project_adam", 1)],
 }
 
 
@@ -536,8 +543,8 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit,
             row["impl_bytes"] = int(sum(ib))
             row["impl_hbm_frac"] = round(sum(ib) / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         mk = MEASURED_KERNELS.get(k)
-        if mk and all(measured.get(x) for x in mk):
-            mb = sum(measured[x] for x in mk)
+        if mk and all(measured.get(x) for x, _ in mk):
+            mb = sum(measured[x] * c for x, c in mk)
             row["measured_bytes"] = int(mb)
             row["measured_hbm_frac"] = round(mb / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         if flop:
@@ -653,7 +660,9 @@ def main():
     core.check(L.tdgs_profile_end(ms, cnt))
     assert int(mon[2]) == overflows0, "a frame's keys did not fit the key arrays"
 
-    in_flight = [render_in_flight(core, g, cams, tiling, opts, buf.key_capacity, args.steps, s) for s in (2, 3)]
+    in_flight = None
+    if not args.no_in_flight:
+        in_flight = [render_in_flight(core, g, cams, tiling, opts, buf.key_capacity, args.steps, s) for s in (2, 3)]
 
     st = frame_stats(core, g, cams, tiling, opts, buf, used)
     n = len(g)
