@@ -31,6 +31,10 @@
  *     last failure on the calling host thread. No exception crosses the ABI.
  *   - Calls that report a count back to the host (number of filtered Gaussians, number of
  *     duplicated keys, number of Gaussians after densification) synchronise their stream.
+ *   - A context (tdgs_ctx_create) holds the device counters of the frame in progress: frames
+ *     rendered concurrently on several streams each need their own context, render buffers
+ *     and outputs (the Gaussians may be shared); calls on one context are ordered on one
+ *     stream.
  */
 #ifndef TDGS_H
 #define TDGS_H
