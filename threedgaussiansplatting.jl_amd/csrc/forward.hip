@@ -411,6 +411,27 @@ struct EmitGrid {
         *t0 = x0 + 1 + y0 * ntx;
         *wx = x1 - x0 + 1;
     }
+    // rect() with, for the blocks' tile masks (at most 255 blocks, blocks of at most 16 x 16
+    // tiles), the rectangle's first and last tile column inside its first and last block
+    // column, the same for rows, and its block rows less one, packed with the width:
+    // wx | ox0 << 8 | ox1 << 12 | oy0 << 16 | oy1 << 20 | (rows - 1) << 24
+    __device__ __forceinline__ void rect_packed(const int4 r, int32_t* t0, int32_t* pk) const {
+        const int32_t x0 = (r.x - 1) >> sx, y0 = (r.y - 1) >> sy, x1 = (r.z - 1) >> sx, y1 = (r.w - 1) >> sy;
+        const int32_t bwm = (1 << sx) - 1, bhm = (1 << sy) - 1;
+        *t0 = x0 + 1 + y0 * ntx;
+        *pk = (x1 - x0 + 1) | (((r.x - 1) & bwm) << 8) | (((r.z - 1) & bwm) << 12) | (((r.y - 1) & bhm) << 16) |
+              (((r.w - 1) & bhm) << 20) | ((y1 - y0) << 24);
+    }
+    // The tiles of block (column rx, row q of the rectangle's blocks) that the rectangle
+    // covers, as bit masks relative to the block: columns in bits 0-15, rows in bits 16-31.
+    __device__ __forceinline__ uint32_t block_mask(int32_t pk, int32_t q, int32_t rx) const {
+        const int32_t bwm = (1 << sx) - 1, bhm = (1 << sy) - 1;
+        const int32_t cx0 = rx == 0 ? (pk >> 8) & 15 : 0;
+        const int32_t cx1 = rx == (pk & 0xff) - 1 ? (pk >> 12) & 15 : bwm;
+        const int32_t cy0 = q == 0 ? (pk >> 16) & 15 : 0;
+        const int32_t cy1 = q == ((pk >> 24) & 0xff) ? (pk >> 20) & 15 : bhm;
+        return ((2u << cx1) - (1u << cx0)) | (((2u << cy1) - (1u << cy0)) << 16);
+    }
 };
 static_assert(kEmitStage + 1 + 3 * kEmitStage <= kEmitTile + 1, "staging fits the scan buffer");
 
@@ -424,19 +445,22 @@ __device__ __forceinline__ int emit_slot(int k) {
 
 // The tile ids and values of keys d0 + ITEMS t + i (i < ITEMS) of emission block `block`
 // (d0 = block THREADS ITEMS), computed by thread t of a THREADS-thread workgroup into
-// tile[] and val[] (zeros past m). s_buf holds THREADS ITEMS + 1 ints of LDS; ends with a
-// workgroup barrier after its last use of s_buf and s_range.
-template <int THREADS, int ITEMS>
+// tile[] and val[] (zeros past m); with MASK (a coarse grid of at most 255 blocks) also
+// mask[]: the tiles of the entry's block that its rectangle covers (EmitGrid::block_mask).
+// s_buf holds THREADS ITEMS + 1 ints of LDS; ends with a workgroup barrier after its last use
+// of s_buf and s_range.
+template <int THREADS, int ITEMS, bool MASK = false>
 __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t block, const int32_t* __restrict__ sorted_f,
                                               const int32_t* __restrict__ cs, const int32_t* __restrict__ blk_first,
                                               const int4* __restrict__ srect, EmitGrid grid, int32_t* s_buf,
-                                              int64_t* s_range, int32_t (&tile)[ITEMS], int32_t (&val)[ITEMS]) {
+                                              int64_t* s_range, int32_t (&tile)[ITEMS], int32_t (&val)[ITEMS],
+                                              uint32_t* mask = nullptr) {
     constexpr int kBlock = THREADS * ITEMS;
     static_assert(kBlock == kEmitTile, "emission blocks of kEmitTile keys");
     int32_t* const s_cs = s_buf;                      // [0, cnt]: scan values of the span
     int32_t* const s_f = s_buf + kEmitStage + 1;      // staged Gaussians: fgidx,
     int32_t* const s_t0 = s_f + kEmitStage;           // tile id of the rectangle's first tile,
-    int32_t* const s_wx = s_t0 + kEmitStage;          // rectangle width in tiles
+    int32_t* const s_wx = s_t0 + kEmitStage;          // rectangle width in tiles (MASK: packed)
     const int t = threadIdx.x;
     const int64_t d0 = block * kBlock;
     // Gaussians owning the block's first and last keys: from the block table of the count scan
@@ -468,7 +492,10 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
             s_cs[k] = j < 0 ? 0 : cs[j];
             if (full && k < cnt) {
                 s_f[k] = sorted_f[j + 1];
-                grid.rect(srect[j + 1], &s_t0[k], &s_wx[k]);
+                if (MASK)
+                    grid.rect_packed(srect[j + 1], &s_t0[k], &s_wx[k]);
+                else
+                    grid.rect(srect[j + 1], &s_t0[k], &s_wx[k]);
             }
         }
     }
@@ -487,13 +514,20 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
             if (start_of(mid) <= first) lo = mid; else hi = mid;
         }
         int64_t nxt = start_of(lo + 1);
-        int32_t f, t0, wx;
+        int32_t f, t0, wx, pk = 0;
         auto load = [&](int64_t k) {
             if (full) {
                 f = s_f[k]; t0 = s_t0[k]; wx = s_wx[k];
             } else {
                 f = sorted_f[j_lo + k];
-                grid.rect(srect[j_lo + k], &t0, &wx);
+                if (MASK)
+                    grid.rect_packed(srect[j_lo + k], &t0, &wx);
+                else
+                    grid.rect(srect[j_lo + k], &t0, &wx);
+            }
+            if (MASK) {
+                pk = wx;
+                wx &= 0xff;
             }
         };
         load(lo);
@@ -511,6 +545,7 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
             }
             tile[i] = t0 + q * grid.ntx + rx;
             val[i] = f;
+            if (MASK) mask[i] = grid.block_mask(pk, q, rx);
             if (++rx == wx) {
                 rx = 0;
                 ++q;
@@ -518,7 +553,10 @@ __device__ __forceinline__ void emit_generate(int64_t nb, int64_t m, int64_t blo
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < ITEMS; ++i) tile[i] = val[i] = 0;
+        for (int i = 0; i < ITEMS; ++i) {
+            tile[i] = val[i] = 0;
+            if (MASK) mask[i] = 0;
+        }
     }
     __syncthreads();   // s_buf is free again
 }
@@ -652,22 +690,25 @@ __device__ __forceinline__ int emit_sort_slot(int k) {
     return t * kEmitSortItems + ((i + t) & (kEmitSortItems - 1));
 }
 
-// One emission block of k_emit_scatter.
+// One emission block of k_emit_scatter (MASK: each entry's block mask goes along to mout).
+template <bool MASK>
 __device__ __forceinline__ void emit_scatter_block(int64_t blk, int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f,
                                                    const int32_t* __restrict__ cs, const int32_t* __restrict__ blk_first,
                                                    const int4* __restrict__ srect, EmitGrid grid, int nbits0,
                                                    const uint32_t* __restrict__ offsets,
                                                    uint32_t* __restrict__ totals, int64_t count_tiles,
                                                    const uint32_t* __restrict__ grp, uint16_t* __restrict__ kout,
-                                                   int32_t* __restrict__ vout, uint32_t* err, int32_t* s_buf,
-                                                   int64_t* s_range, uint32_t* s_part) {
+                                                   int32_t* __restrict__ vout, uint32_t* __restrict__ mout,
+                                                   uint32_t* err, int32_t* s_buf, int64_t* s_range, uint32_t* s_part) {
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const int64_t d0 = blk * kEmitTile;
     int32_t tile[kEmitSortItems], val[kEmitSortItems];
-    emit_generate<kEmitSortThreads, kEmitSortItems>(nb, m, blk, sorted_f, cs, blk_first, srect, grid, s_buf, s_range,
-                                                    tile, val);
+    uint32_t msk[kEmitSortItems];
+    emit_generate<kEmitSortThreads, kEmitSortItems, MASK>(nb, m, blk, sorted_f, cs, blk_first, srect, grid, s_buf,
+                                                          s_range, tile, val, MASK ? msk : nullptr);
     uint16_t key[kEmitSortItems];
     int32_t v[kEmitSortItems];
+    uint32_t mv[kEmitSortItems];
     bool valid[kEmitSortItems];
 #pragma unroll
     for (int i = 0; i < kEmitSortItems; ++i) s_buf[t * kEmitSortItems + ((i + t) & (kEmitSortItems - 1))] = tile[i];
@@ -684,6 +725,16 @@ __device__ __forceinline__ void emit_scatter_block(int64_t blk, int64_t nb, int6
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kEmitSortItems; ++k) v[k] = s_buf[emit_sort_slot(w * (kEmitSortItems * kWave) + k * kWave + lane)];
+    if (MASK) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kEmitSortItems; ++i)
+            s_buf[t * kEmitSortItems + ((i + t) & (kEmitSortItems - 1))] = (int32_t)msk[i];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kEmitSortItems; ++k)
+            mv[k] = (uint32_t)s_buf[emit_sort_slot(w * (kEmitSortItems * kWave) + k * kWave + lane)];
+    }
     uint32_t off_t = 0, total_t = 0;
     if (grp) {
         rs_group_offsets(offsets, grp, blk, (m + kEmitTile - 1) / kEmitTile, off_t, total_t, s_part);
@@ -693,20 +744,21 @@ __device__ __forceinline__ void emit_scatter_block(int64_t blk, int64_t nb, int6
         total_t = totals[t];
     }
     // (rs_scatter_tile reuses s_buf for its staging after its first barrier)
-    rs_scatter_tile<uint16_t>(key, v, valid, blk, m, 0, nbits0, off_t, total_t, kout, vout, err, nullptr,
-                              reinterpret_cast<uint32_t*>(s_buf));
+    rs_scatter_tile<uint16_t, MASK>(key, v, valid, blk, m, 0, nbits0, off_t, total_t, kout, vout, err, nullptr,
+                                    reinterpret_cast<uint32_t*>(s_buf), RsGather{}, MASK ? mv : nullptr, mout);
 }
 
 // LOOP: a capped grid walks the emission blocks blockIdx.x, + gridDim.x, ... (a device-count
 // render whose capacity-sized block count exceeds the cap; the loop costs registers: 134
 // VGPRs against 73, so the grid is one block per workgroup otherwise).
-template <bool LOOP>
+// MASK: the entries' block masks are sorted along into mout (one radix pass only).
+template <bool LOOP, bool MASK>
 __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
     int64_t nb, int64_t m, const int32_t* __restrict__ sorted_f, const int32_t* __restrict__ cs,
     const int32_t* __restrict__ blk_first, const int4* __restrict__ srect, EmitGrid grid, int nbits0,
     const uint32_t* __restrict__ offsets, uint32_t* __restrict__ totals, int64_t count_tiles,
-    const uint32_t* __restrict__ grp, uint16_t* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err,
-    const int64_t* dc) {
+    const uint32_t* __restrict__ grp, uint16_t* __restrict__ kout, int32_t* __restrict__ vout,
+    uint32_t* __restrict__ mout, uint32_t* err, const int64_t* dc) {
     __shared__ int32_t s_buf[kEmitTile + 1];
     __shared__ int64_t s_range[2];
     __shared__ uint32_t s_part[kRsBins];
@@ -718,13 +770,13 @@ __global__ __launch_bounds__(kEmitSortThreads) void k_emit_scatter(
     if (grp && m == 0 && blockIdx.x == 0 && threadIdx.x < kRsBins) totals[threadIdx.x] = 0;
     if (!LOOP) {
         if ((int64_t)blockIdx.x * kEmitTile < m)
-            emit_scatter_block(blockIdx.x, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals,
-                               count_tiles, grp, kout, vout, err, s_buf, s_range, s_part);
+            emit_scatter_block<MASK>(blockIdx.x, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals,
+                                     count_tiles, grp, kout, vout, mout, err, s_buf, s_range, s_part);
         return;
     }
     for (int64_t blk = blockIdx.x; blk * kEmitTile < m; blk += gridDim.x) {
-        emit_scatter_block(blk, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals, count_tiles, grp,
-                           kout, vout, err, s_buf, s_range, s_part);
+        emit_scatter_block<MASK>(blk, nb, m, sorted_f, cs, blk_first, srect, grid, nbits0, offsets, totals, count_tiles,
+                                 grp, kout, vout, mout, err, s_buf, s_range, s_part);
         __syncthreads();   // s_buf is reused by the next block
     }
 }
@@ -914,6 +966,7 @@ struct BinArgs {
     int64_t mc;                // entries of cvals (launch bound)
     const int64_t* dmc;        // entries used (device counts), or null
     const int32_t* ranges;     // tile rectangles [x0, y0, x1, y1] (1-based, inclusive) by fgidx
+    const uint32_t* cmask;     // or null: each entry's tiles of its block (EmitGrid::block_mask)
     int32_t* table;            // COUNT writes the Gaussians of each segment covering each tile
     int32_t* tile_totals;      // COUNT adds them up per tile (zeroed beforehand)
     const int32_t* tiles_end;  // WRITE: inclusive ends of the tiles' lists
@@ -1023,26 +1076,41 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) cnt[i] = WRITE ? __builtin_amdgcn_readlane(start, i) : 0;
-            // candidates cb + t + blockDim q (q < kBinPer): the loads issue together
+            // candidates cb + t + blockDim q (q < kBinPer): the loads issue together. Their
+            // masks come sorted along with them (cmask), else from the rectangles.
             int32_t f[kBinPer];
+            uint32_t mk[kBinPer];
+            if (a.cmask) {
 #pragma unroll
-            for (int q = 0; q < kBinPer; ++q) {
-                const int64_t e = cb + t + (int64_t)blockDim.x * q;
-                f[q] = e < ce ? a.cvals[e] : 0;
+                for (int q = 0; q < kBinPer; ++q) {
+                    const int64_t e = cb + t + (int64_t)blockDim.x * q;
+                    f[q] = WRITE && e < ce ? a.cvals[e] : 0;
+                    mk[q] = e < ce ? a.cmask[e] : 0u;
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kBinPer; ++q) {
+                    const int64_t e = cb + t + (int64_t)blockDim.x * q;
+                    f[q] = e < ce ? a.cvals[e] : 0;
+                }
+                int4 r[kBinPer];
+#pragma unroll
+                for (int q = 0; q < kBinPer; ++q)
+                    r[q] = f[q] > 0 ? reinterpret_cast<const int4*>(a.ranges)[f[q] - 1] : make_int4(1, 1, 0, 0);
+#pragma unroll
+                for (int q = 0; q < kBinPer; ++q) {
+                    // columns in bits 0-15, rows in bits 16-31 (of the block); none for an empty slot
+                    const int cx0 = max(r[q].x - 1 - x0b, 0), cx1 = min(r[q].z - 1 - x0b, BW - 1);
+                    const int cy0 = max(r[q].y - 1 - y0b, 0), cy1 = min(r[q].w - 1 - y0b, BH - 1);
+                    const uint32_t cm = cx1 >= cx0 ? (2u << cx1) - (1u << cx0) : 0u;
+                    const uint32_t rm = cy1 >= cy0 ? (2u << cy1) - (1u << cy0) : 0u;
+                    mk[q] = cm | (rm << 16);
+                }
             }
-            int4 r[kBinPer];
-#pragma unroll
-            for (int q = 0; q < kBinPer; ++q)
-                r[q] = f[q] > 0 ? reinterpret_cast<const int4*>(a.ranges)[f[q] - 1] : make_int4(1, 1, 0, 0);
 #pragma unroll
             for (int q = 0; q < kBinPer; ++q) {
-                // columns in bits 0-15, rows in bits 16-31 (of the block); none for an empty slot
-                const int cx0 = max(r[q].x - 1 - x0b, 0), cx1 = min(r[q].z - 1 - x0b, BW - 1);
-                const int cy0 = max(r[q].y - 1 - y0b, 0), cy1 = min(r[q].w - 1 - y0b, BH - 1);
-                const uint32_t cm = cx1 >= cx0 ? (2u << cx1) - (1u << cx0) : 0u;
-                const uint32_t rm = cy1 >= cy0 ? (2u << cy1) - (1u << cy0) : 0u;
                 s_f[t + blockDim.x * q] = f[q];
-                s_m[t + blockDim.x * q] = cm | (rm << 16);
+                s_m[t + blockDim.x * q] = mk[q];
             }
             __syncthreads();
             const int nk = (int)(ce - cb);
@@ -1865,6 +1933,9 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     const int64_t mb = dc ? kc : mc;   // launch bound of the entries
     uint16_t* c16 = reinterpret_cast<uint16_t*>(buf->keys);
     uint16_t* c16_alt = c16 + kc;
+    // with one pass the entries' block masks are sorted along, into the keys array's second
+    // half (the 16-bit ids take its first): the binning then reads no rectangles
+    uint32_t* cmask = one_pass ? reinterpret_cast<uint32_t*>(buf->keys) + kc : nullptr;
     const EmitGrid cg{bg.nbx, bg.sx, bg.sy};
     // (with device counts the blocks are bounded by the key capacity; a capped grid walks them)
     constexpr int64_t kEmitMaxGrid = 4096;
@@ -1895,17 +1966,27 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
             k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals, d_used, kEmitTile);
             TDGS_LAUNCHED();
         }
-        if ((int64_t)egrid < eblocks)
-            k_emit_scatter<true><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
-                                                                    cg, nbits0, table, totals, count_tiles, grp,
-                                                                    one_pass ? c16 : c16_alt,
-                                                                    one_pass ? buf->values : buf->sorted_values, d_err, dc);
-        else
-            k_emit_scatter<false><<<egrid, kEmitSortThreads, 0, s>>>(nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect,
-                                                                     cg, nbits0, table, totals, count_tiles, grp,
-                                                                     one_pass ? c16 : c16_alt,
-                                                                     one_pass ? buf->values : buf->sorted_values, d_err,
-                                                                     dc);
+        uint16_t* ek = one_pass ? c16 : c16_alt;
+        int32_t* ev = one_pass ? buf->values : buf->sorted_values;
+        if ((int64_t)egrid < eblocks) {
+            if (cmask)
+                k_emit_scatter<true, true><<<egrid, kEmitSortThreads, 0, s>>>(
+                    nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg, nbits0, table, totals, count_tiles, grp, ek, ev,
+                    cmask, d_err, dc);
+            else
+                k_emit_scatter<true, false><<<egrid, kEmitSortThreads, 0, s>>>(
+                    nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg, nbits0, table, totals, count_tiles, grp, ek, ev,
+                    nullptr, d_err, dc);
+        } else {
+            if (cmask)
+                k_emit_scatter<false, true><<<egrid, kEmitSortThreads, 0, s>>>(
+                    nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg, nbits0, table, totals, count_tiles, grp, ek, ev,
+                    cmask, d_err, dc);
+            else
+                k_emit_scatter<false, false><<<egrid, kEmitSortThreads, 0, s>>>(
+                    nb, mc, r.sorted_f, r.cs, r.blk_first, r.srect, cg, nbits0, table, totals, count_tiles, grp, ek, ev,
+                    nullptr, d_err, dc);
+        }
         TDGS_LAUNCHED();
         if (!one_pass)
             TDGS_TRY(radix_sort_pairs<uint16_t>(c16_alt, c16, buf->sorted_values, buf->values, c16_alt,
@@ -1926,7 +2007,7 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     ba.nblocks = nblocks;
     ba.cvals = buf->values; ba.cend = r.block_end; ba.mc = mb; ba.dmc = d_used;
     ba.totals = one_pass ? totals : nullptr;
-    ba.ranges = buf->tile_ranges; ba.table = r.tile_counts; ba.tile_totals = r.tile_totals;
+    ba.ranges = buf->tile_ranges; ba.cmask = cmask; ba.table = r.tile_counts; ba.tile_totals = r.tile_totals;
     ba.tiles_end = buf->tiles_end;
     ba.out = buf->sorted_values; ba.cap = (int32_t)(kc < INT32_MAX ? kc : INT32_MAX); ba.err = d_err;
     const unsigned bthreads = 4u << (bg.sx + bg.sy);

@@ -240,13 +240,15 @@ __device__ __forceinline__ void wave_run_add(int64_t key, int64_t v, int64_t* ds
 }
 
 // off_t and total_t (read by the digit owners, threads t < kRsBins): the tile's offset inside
-// digit t's output (digit t's keys in earlier tiles) and digit t's total.
-template <class K>
+// digit t's output (digit t's keys in earlier tiles) and digit t's total. With V2 a second
+// 32-bit payload (val2, one per key) is moved along to vout2.
+template <class K, bool V2 = false>
 __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems], const int32_t (&val)[RsTile<K>::kItems],
                                                 const bool (&valid)[RsTile<K>::kItems], int64_t tile, int64_t n,
                                                 int shift, int nbits, uint32_t off_t, uint32_t total_t,
                                                 K* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err,
-                                                int64_t* d_kept, uint32_t* s_raw, RsGather gather = {}) {
+                                                int64_t* d_kept, uint32_t* s_raw, RsGather gather = {},
+                                                const uint32_t* val2 = nullptr, uint32_t* __restrict__ vout2 = nullptr) {
     constexpr int kRsItems = RsTile<K>::kItems;
     constexpr int kRsTile = RsTile<K>::kTile;
     // Keys narrower than 32 bits are staged as 32-bit words: lanes storing 16-bit keys to
@@ -353,6 +355,18 @@ __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems
         }
         // (consecutive lanes hold consecutive outputs of a digit's run: few runs per wavefront)
         if (gather.sums) wave_run_add(opos[k] >= 0 ? (int64_t)(opos[k] >> kRsSumShift) : -1, item, gather.sums);
+    }
+    if constexpr (V2) {
+        __syncthreads();   // every value is read: s_val takes the second payload
+#pragma unroll
+        for (int k = 0; k < kRsItems; ++k) {
+            if (valid[k] && pos[k] < (uint32_t)kRsTile) s_val[pos[k]] = (int32_t)val2[k];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kRsItems; ++k) {
+            if (opos[k] >= 0) vout2[opos[k]] = (uint32_t)s_val[k * kRsThreads + t];
+        }
     }
 }
 
