@@ -1362,12 +1362,18 @@ struct BlendArgs {
 // last record. Valid only when every live exponent lies in [-87, 88] (the batch is not
 // `checked`). v39-v63 are its scratch registers (the kernel stays within 64 VGPRs, 8
 // wavefronts per SIMD). Returns the mask of the lanes that did not stop.
+// the literals of blend_batch's exponential are exp_poly's coefficients
+static_assert(__builtin_bit_cast(uint32_t, kExpC6) == 0x3ab51223u && __builtin_bit_cast(uint32_t, kExpC4) == 0x3d2aac79u &&
+                  __builtin_bit_cast(uint32_t, kExpC3) == 0x3e2aaa49u && __builtin_bit_cast(uint32_t, kExpC2) == 0x3efffffeu &&
+                  __builtin_bit_cast(uint32_t, -kLn2Hi) == 0xbf317200u && __builtin_bit_cast(uint32_t, -kLn2Lo) == 0xb5bfbe8eu &&
+                  __builtin_bit_cast(uint32_t, kLog2e) == 0x3fb8aa3bu,
+              "blend_batch constants");
 template <bool DEPTH, bool LAST>
 __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0, int32_t idx_end, float uu,
                                                 float vv, float uv, float cu, float cv, float e_cut,
                                                 float max_alpha, float min_alpha, float min_T, float& T,
                                                 float& C0, float& C1, float& C2, float& D, int32_t& last) {
-    const float c6 = 1.38888888888889e-3f;   // exp_f_core's coefficient of r^6 (a VGPR operand)
+    const float c5 = kExpC5;   // exp_poly's coefficient of r^5 (a VGPR operand)
     uint64_t act, live, ctb, stp, sav;
     int32_t idx;
 #define TDGS_BLEND_ASM(DEPTH_FMA, READ_C, LAST_MOV)                                                                  \
@@ -1396,11 +1402,10 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_rndne_f32 v61, v61\n"                                                                   \
         "v_fmac_f32 v60, 0xbf317200, v61\n"                                                        \
         "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                        \
-        "v_fmamk_f32 v62, v60, 0x39500d01, %[c6]\n"                                                \
-        "v_fmaak_f32 v62, v62, v60, 0x3c088889\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3d2aaaab\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3e2aaaab\n"                                                  \
-        "v_fma_f32 v62, v62, v60, 0.5\n"                                                           \
+        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                  \
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_cvt_i32_f32 v61, v61\n"                                                                 \
@@ -1444,11 +1449,10 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_rndne_f32 v61, v61\n"                                                                   \
         "v_fmac_f32 v60, 0xbf317200, v61\n"                                                        \
         "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                        \
-        "v_fmamk_f32 v62, v60, 0x39500d01, %[c6]\n"                                                \
-        "v_fmaak_f32 v62, v62, v60, 0x3c088889\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3d2aaaab\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3e2aaaab\n"                                                  \
-        "v_fma_f32 v62, v62, v60, 0.5\n"                                                           \
+        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                  \
+        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                  \
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
         "v_cvt_i32_f32 v61, v61\n"                                                                 \
@@ -1483,7 +1487,7 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
           [idx] "=&s"(idx), [T] "+v"(T), [C0] "+v"(C0), [C1] "+v"(C1), [C2] "+v"(C2), [D] "+v"(D),   \
           [last] "+v"(last)                                                                         \
         : [addr] "v"(lds_addr), [i0] "s"(idx0), [iend] "s"(idx_end), [uu] "v"(uu), [vv] "v"(vv),     \
-          [uv] "v"(uv), [cu] "v"(cu), [cv] "v"(cv), [c6] "v"(c6), [cut] "s"(e_cut),                  \
+          [uv] "v"(uv), [cu] "v"(cu), [cv] "v"(cv), [c5] "v"(c5), [cut] "s"(e_cut),                  \
           [maxa] "s"(max_alpha), [mina] "s"(min_alpha), [minT] "s"(min_T)                           \
         : "v39", "v40", "v41", "v42", "v43", "v44", "v45", "v46", "v47", "v48", "v49", "v50", "v51",  \
           "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60", "v61", "v62", "v63", "vcc",    \
