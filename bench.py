@@ -460,11 +460,12 @@ def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles, mc=0):
         return (16 + 4) * nb
     if stage == "emit":                  # scan, fgidx, rectangle of the non-empty in (block ids counted)
         return (8 + 4 + 16) * nb
-    if stage == "tile_sort":             # the same in again; (16-bit block id, 32-bit value) per entry out
-        return (8 + 4 + 16) * nb + 6 * mc
-    if stage == "tile_ranges":           # block ends (ids in); count and write passes read value +
-        # rectangle per entry; per-(segment, tile) counts scanned; the M list entries out
-        return 2 * mc + 2 * (4 + 16) * mc + 8 * ntiles + 4 * m
+    if stage == "tile_sort":             # the same in again; (16-bit block id, 32-bit value, 32-bit
+        # block tile masks) per entry out
+        return (8 + 4 + 16) * nb + 10 * mc
+    if stage == "tile_ranges":           # count pass: masks in; write pass: masks + values in;
+        # per-(segment, tile) counts scanned; the M list entries out
+        return 4 * mc + 8 * mc + 8 * ntiles + 4 * m
     if stage == "blend":                 # metric's K5: 40 per key, 20 per pixel
         return 40 * m + 20 * npx
     return None
