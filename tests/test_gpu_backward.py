@@ -76,7 +76,7 @@ FILTER = {"clip_mode": 1}   # TDGS_CLIP_FILTER (BoundaryFilter)
     (1, 20_000, (16, 16), False, {}), (1, 20_000, (16, 16), True, {}),
     (2, 60_000, (16, 32), False, {}), (0, None, (16, 16), False, {}),
     (0, None, (32, 32), False, {}), (0, None, (8, 8), False, {}),
-    # 192 pixels: 128 threads, so the second pixel of lanes 64-127 lies past the tile
+    # 192 pixels: one wavefront of four-pixel lanes whose fourth pixel slot lies past the tile
     (0, None, (24, 8), False, {}), (0, None, (8, 24), False, {}),
     # antialiasing (forward_core.jl:450-462, backward_core.jl:331-341, 480) and the
     # BoundaryFilter clip mode (forward_core.jl:343, backward_core.jl:373-381)

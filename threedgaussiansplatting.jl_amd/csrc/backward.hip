@@ -161,28 +161,26 @@ struct BackBlendArgs {
 // VGPRs; a few per-batch values go to scratch) measured 345 us against 378 us for two pixels
 // per lane at 1M Gaussians, 1080p (three wavefronts per SIMD at 142 VGPRs: 365 us).
 constexpr int kBackPx = 4;
-// PW: per-wavefront copies of the LDS sums (workgroups of at most kBackPwThreads threads; the
-// copies grow with the square of the workgroup size), else one copy shared by LDS atomics.
-constexpr int kBackPwThreads = 256;
 // BPC > 0 (tile sides multiples of 8, BPC = TH / 8 blocks of 8 x 8 pixels per block column,
 // BPC dividing PX): slot p's pixels are slot 0's moved by the constant (8 (p / BPC), 8 (p %
 // BPC)), so only slot 0's coordinates are kept per lane and the others' offsets from the
 // record are slot 0's plus a constant (three fewer register pairs: 323 us against 349 us at 1M
 // Gaussians, 1080p, where the loop's scratch spills went from 52 to 12 bytes per lane). The
 // subtraction order differs from the per-pixel form by rounding only. BPC = 0: any tile.
-template <bool SEP, int PX, bool PW, int BPC>
+template <bool SEP, int PX, int BPC>
 __global__ __launch_bounds__(1024 / kBackPx) __attribute__((amdgpu_waves_per_eu(4))) void k_backward_blend(
     BackBlendArgs a) {
     extern __shared__ float4 s_raw4[];
     const int NT = a.TW * a.TH;
     const int NB = (int)blockDim.x;
     BackRec* s_rec = reinterpret_cast<BackRec*>(s_raw4);
-    // PW: per-wavefront sums [wave][NB][9]. A wavefront takes each entry into at most one
-    // slot, so its transposed sums are plain stores (an LDS atomic's round trip sat in front of
-    // the next entry's record reads); the flush adds the wavefronts' copies.
-    const int NW = PW ? NB / kWave : 1;
+    // Per-wavefront sums [wave][NB][9] (at most 4 wavefronts: 1024 / PX threads). A wavefront
+    // takes each entry into at most one slot, so its transposed sums are plain stores (an LDS
+    // atomic's round trip sat in front of the next entry's record reads); the flush adds the
+    // wavefronts' copies.
+    const int NW = NB / kWave;
     float* s_acc = reinterpret_cast<float*>(s_rec + NB);
-    float* s_accw = PW ? s_acc + (threadIdx.x / kWave) * (NB * 9) : s_acc;
+    float* s_accw = s_acc + (threadIdx.x / kWave) * (NB * 9);
     __shared__ int s_max_last;
     const int t = threadIdx.x;
     const int lane = __lane_id();
@@ -366,12 +364,7 @@ __global__ __launch_bounds__(1024 / kBackPx) __attribute__((amdgpu_waves_per_eu(
             const float2 m2 = *reinterpret_cast<const float2*>(&s_rec[je].d);   // M21 M22
             const float mixed = fmaf(comp == 0 ? m11 : m2.y, sum, m2.x * other);
             const float val = comp < 2 ? mixed : sum * scale;
-            if (lane < 9 * kSlots && jl >= 0) {
-                if (PW)
-                    s_accw[9 * jl + comp] = val;
-                else
-                    atomicAdd(&s_accw[9 * jl + comp], val);
-            }
+            if (lane < 9 * kSlots && jl >= 0) s_accw[9 * jl + comp] = val;
         }
         __syncthreads();
         // Flush with lane i on component i % 9 of entry i / 9: one atomic instruction covers
@@ -790,18 +783,21 @@ int tdgs_backward_render_tiles(void* stream, tdgs_gradients* grads, const float*
     // kBackPx pixels per thread, in whole wavefronts (the transpose-sum reads all 64 lanes;
     // the pixels past the tile's are off)
     const int nt = ((tiling->tile_width * tiling->tile_height + kBackPx - 1) / kBackPx + kWave - 1) / kWave * kWave;
-    const bool pw = nt <= kBackPwThreads;
-    const size_t lds = (size_t)nt * (sizeof(BackRec) + (size_t)(pw ? nt / kWave : 1) * 9 * sizeof(float));
+    const size_t lds = (size_t)nt * (sizeof(BackRec) + (size_t)(nt / kWave) * 9 * sizeof(float));
     const dim3 grid(tiling->nb_tiles_x, tiling->nb_tiles_y);
-    // 16-pixel-high tiles in 8 x 8 blocks (the usual ones) take the constant slot offsets
-    const bool bpc2 = tiling->tile_width % 8 == 0 && tiling->tile_height == 16;
-#define TDGS_BB(SEP_, PW_, BPC_) k_backward_blend<SEP_, kBackPx, PW_, BPC_><<<grid, nt, lds, s>>>(a)
+    // tiles of 8 x 8 pixel blocks with 1, 2 or 4 blocks per column take the constant slot offsets
+    const int bpc = tiling->tile_width % 8 == 0 && tiling->tile_height % 8 == 0 ? tiling->tile_height / 8 : 0;
+#define TDGS_BB(SEP_, BPC_) k_backward_blend<SEP_, kBackPx, BPC_><<<grid, nt, lds, s>>>(a)
     if (grads->grads2d) {
-        if (pw) { if (bpc2) TDGS_BB(false, true, 2); else TDGS_BB(false, true, 0); }
-        else { if (bpc2) TDGS_BB(false, false, 2); else TDGS_BB(false, false, 0); }
+        if (bpc == 1) TDGS_BB(false, 1);
+        else if (bpc == 2) TDGS_BB(false, 2);
+        else if (bpc == 4) TDGS_BB(false, 4);
+        else TDGS_BB(false, 0);
     } else {
-        if (pw) { if (bpc2) TDGS_BB(true, true, 2); else TDGS_BB(true, true, 0); }
-        else { if (bpc2) TDGS_BB(true, false, 2); else TDGS_BB(true, false, 0); }
+        if (bpc == 1) TDGS_BB(true, 1);
+        else if (bpc == 2) TDGS_BB(true, 2);
+        else if (bpc == 4) TDGS_BB(true, 4);
+        else TDGS_BB(true, 0);
     }
 #undef TDGS_BB
     TDGS_LAUNCHED();
