@@ -179,3 +179,32 @@ def test_trainer_skips_overflowing_step_and_grows_keys(gpu):
     assert status == abi.TDGS_FRAME_OK and m <= tr.render_buffers.key_capacity
     assert not torch.equal(before[0], g.means_opacity)
     assert np.isfinite(tr.current_loss())
+
+
+@pytest.mark.parametrize("device_counts", [False, True])
+def test_kept_but_nothing_on_screen(gpu, oracle, device_counts):
+    """Gaussians in front of the camera but far to its side: all kept (clamp mode keeps by
+    depth alone, forward_core.jl:326-355), none with a tile rectangle on the screen, so the
+    depth presort keeps no pair, M = 0 and the frame is the background."""
+    import copy
+    w = synthetic.config(0, n=5000)
+    cam = w.cameras[0]
+    g_host = copy.deepcopy(w.gaussians)
+    g_host.means_opacity[:, :3] += np.float32(1000.0) * cam.R_c2w[:, 0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.25, 0.5, 0.75))
+    r = oracle.render(g_host, cam, t, opts)
+    assert r["nb_fgaussians"] > 0 and r["nb_keys"] == 0
+    g = gpu.TrainableGaussiansVector.from_host(g_host, 0)
+    if device_counts:
+        out, buf = _device_render(gpu, g, cam, t, opts, key_capacity=1024)
+        assert buf.frame_counts() == (r["nb_fgaussians"], 0, 0, abi.TDGS_FRAME_OK)
+    else:
+        out = gpu.RenderOutputs.for_camera(cam, 0, include_depth=True)
+        buf = gpu.RenderBuffers(len(g), t, 0)
+        gpu.render_(out, g, cam, t, opts, buf)
+        torch.cuda.synchronize()
+        assert (buf.nb_fgaussians, buf.nb_keys) == (r["nb_fgaussians"], 0)
+    np.testing.assert_array_equal(out.rgb.cpu().numpy(), r["rgb"])
+    np.testing.assert_array_equal(out.T.cpu().numpy(), r["T"])
+    assert np.all(out.T.cpu().numpy() == 1) and np.all(out.last.cpu().numpy() == 0)
