@@ -81,6 +81,30 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_each": 1 << 30, "copies": 10}))
 
 
+def hbm_practical():
+    """What streaming kernels reach on this part (context for the HBM fractions, which are
+    quoted against the 8 TB/s peak): a 1 GiB device copy (read + write) and a 1 GiB reduction
+    (read), each timed with HIP events over 5 repetitions after 2."""
+    import torch
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    out = {}
+    for name, fn, moved in (("copy", lambda: dst.copy_(src), 2 * 4 * n), ("read", lambda: src.sum(), 4 * n)):
+        for _ in range(2):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(5):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(5 * moved / (e0.elapsed_time(e1) * 1e-3) / 1e9, 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch of a kernel from the committed rocprofv3 counter summary
     (profiles/hbm_traffic.json, written from two --pmc runs), or None."""
@@ -698,6 +722,8 @@ def main():
                              "detailed_frac": round(flop_detailed / (stage_ms[dom] * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
                              "hbm_frac": round(achieved / HBM_PEAK_GBS, 4)})
 
+    hbm_ref = hbm_practical()
+
     cpu = None
     if not args.no_cpu_baseline:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -745,6 +771,7 @@ def main():
         "stage_ms": {k: round(v, 4) for k, v in stage_ms.items()},
         "stage_algorithmic_GBs": {k: round(v, 1) for k, v in stage_gbs.items()},
         "roofline": roofline,
+        "hbm_practical_GBs": hbm_ref,
         "survey_kernels": survey_kernels(stage_ms, train["stage_ms"] if train else None, n, nf, nb, m, npx, h,
                                          tiling.nb_tiles, tiling.end_bit(), evals, evals_back, mc),
         "cpu_baseline": cpu,

@@ -3,27 +3,34 @@
 //
 // Reference: src/forward_core.jl:196-993, src/forward_structs.jl:743-757.
 //
-// Pipeline of tdgs_render (one host synchronisation, to learn N_f and M):
-//   1. keep flags + kept counts per 256 and 1024  k_keep_counts
+// Pipeline of tdgs_render with at most 65535 tiles (host counts: one synchronisation, after
+// step 5, to learn N_f and M; with TDGS_FLAG_DEVICE_COUNTS none):
+//   1. keep flags + kept counts per 256 and 1024 k_keep_counts (also clears the frame's
+//                                                 zeroed scratch: group sums, scan tile sums)
 //   2-3. compaction + projection, gidx order      k_project (each kept Gaussian's fgidx from
 //                                                 its block's offset, summed from the counts,
 //                                                 and its rank), also writes N_f and a 32-bit
-//                                                 depth key
-//   4. stable sort of (depth bits, fgidx)         radix, bits [0, 32)
-//   5. scan of tile counts in depth order -> M    scan (SortedCounts)
-//   6. key emission in depth order                k_emit_depth_order (16-bit tile ids when
-//                                                 the tiling has at most 65535 tiles, else
-//                                                 64-bit keys)
-//   7. stable sort by tile                        radix on the tile bits
-//   8. tile ranges                                k_tile_ranges
+//                                                 depth key (all ones when its box is empty)
+//   4. depth presort: stable sort of (depth bits, k_rs_count_grouped + k_rs_scatter_grouped,
+//      fgidx) of the non-empty Gaussians          4 passes; the last gathers the tile
+//                                                 rectangles into depth order and sums the
+//                                                 count scan's tiles
+//   5. tiles and coarse blocks per Gaussian in    k_scan_apply -> M and the coarse offsets
+//      depth order, scanned
+//   6. coarse emission: one entry per (Gaussian,  k_emit_count (block-id histograms)
+//      block of 8 x 8 .. 16 x 16 tiles touched)
+//   7. coarse sort: the entries generated again   k_emit_scatter (one radix pass; each entry's
+//      and scattered by block id                  tile masks of its block go along)
+//   8. tile lists                                 k_bin_tiles<COUNT>, k_bin_scan,
+//                                                 k_bin_tiles<WRITE>
 //   9. blending                                   k_render_tiles
-// Steps 4-7 give exactly CUB's result on the reference's emission order: a Gaussian emits at
-// most one key per tile, so the reference's stable sort by (tile, depth bits) breaks ties by
-// ascending fgidx, i.e. it orders keys by (tile, depth bits, fgidx). Sorting the Gaussians by
-// (depth bits, fgidx) first and then stably by tile yields that same total order while
-// sorting only the tile bits of the M duplicated keys (2 passes instead of 6). Since the
-// depth order is already in place, the tile sort needs only the tile ids: it moves 6 bytes
-// per key instead of 12, and the 64-bit keys are assembled only on request
+// With more than 65535 tiles, steps 6-8 are the reference's 64-bit keys emitted in depth order
+// (k_emit_depth_order), sorted stably on their tile bits and ranged.
+// Why the lists equal CUB's result on the reference's emission order: a Gaussian emits at most
+// one key per tile, so the reference's stable sort by (tile, depth bits) orders the keys by
+// (tile, depth bits, fgidx). Distributing the Gaussians, sorted by (depth bits, fgidx), to
+// coarse blocks and then to tiles, each step keeping their order, yields the same lists
+// without sorting the M keys; the 64-bit keys are assembled only on request
 // (tdgs_render_sorted_keys).
 #include <mutex>
 
