@@ -4,15 +4,15 @@
 // Reference: src/backward_core.jl:37-452 (+ helpers :465-964), src/backward_structs.jl:250-257.
 //
 // Backward blending (backward_render_tiles_kernel!, :96-293): one workgroup per tile, one
-// thread per two pixels. The reference lets every pixel start at its own last contributor and
+// thread per four pixels. The reference lets every pixel start at its own last contributor and
 // issues 9 float atomics per (pixel, Gaussian) pair. Here the wavefront walks the tile's
 // sorted list back to front in lock step (a lane whose last contributor lies before the
 // current entry contributes zero), so every pixel meets its entries in the reference's order;
 // the per-pair arithmetic is regrouped (backward_pair_sums) with the same gradients up to
 // rounding.
 // The 9 gradient contributions of 7 contributing entries at a time are summed over the
-// wavefront in one transpose-sum (permlane swaps and DPP, one add per value), over the
-// workgroup's wavefronts with LDS atomics, and reach global memory once per
+// wavefront in one transpose-sum (permlane swaps and DPP, one add per value), stored per
+// wavefront in LDS, added over the workgroup's wavefronts, and reach global memory once per
 // (tile, Gaussian) — 9 atomics per tile instead of 9 per pixel.
 #include "internal.hpp"
 
@@ -91,7 +91,7 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 //   dmu = M (sum out[0], sum out[1]),  dM11 = -sum out[3] / 2,  dM21 = -sum out[4],
 //   dM22 = -sum out[5] / 2.
 // out += [aa du, aa dv, G dalpha, aa du du, aa du dv, aa dv dv, T alpha g] with aa = alpha dalpha
-// (out = ... when first: the first of the lane's two pixels starts the sums).
+// (out = ... when first: the first of the lane's pixels the step runs for starts the sums).
 __device__ __forceinline__ void backward_pair_sums(bool first, float alpha, float inv1ma, float G, float du, float dv,
                                                    const float c[3], const float g[3], float* T, float* gpsi,
                                                    float out[9]) {
