@@ -323,6 +323,12 @@ class GroundTruthImages:
             return
         slot = self.next_slot
         self.next_slot ^= 1
+        # the host waits until the device has released the buffer the copy overwrites (the
+        # loss of the step before the current one): that keeps it one step ahead of the
+        # device. Left to run ahead without bound, the copies and events it queues made the
+        # runtime stall the host for 8-10 ms at a time (measured at cfg2), after which the
+        # device ran dry: 750-790 it/s instead of 868, against 877 with device images.
+        self.released[slot].synchronize()
         with torch.cuda.stream(self.copy_stream):
             self.copy_stream.wait_event(self.released[slot])
             self.buffers[slot].copy_(self.pinned[k], non_blocking=True)
