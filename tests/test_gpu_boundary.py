@@ -145,6 +145,19 @@ def test_ctx_check_after_render(gpu):
     gpu.ctx_check(0)
 
 
+def test_ctx_create_destroy_keep_current_device(gpu):
+    """tdgs_ctx_create / tdgs_ctx_destroy work on the context's device and leave the caller's
+    current device as it was; a device beyond the count is rejected with TDGS_ERR_INVALID."""
+    L = gpu.lib()
+    before = torch.cuda.current_device()
+    h = C.c_void_p()
+    assert L.tdgs_ctx_create(torch.cuda.device_count(), C.byref(h)) == abi.TDGS_ERR_INVALID and not h
+    assert L.tdgs_ctx_create(before, C.byref(h)) == abi.TDGS_OK and h
+    assert torch.cuda.current_device() == before
+    assert L.tdgs_ctx_destroy(h) == abi.TDGS_OK
+    assert torch.cuda.current_device() == before
+
+
 @pytest.mark.parametrize("w,h,tile", [(64, 48, (10, 10)), (100, 70, (12, 20)), (33, 29, (5, 7)), (2, 2, (1, 1)),
                                       (40, 40, (40, 25))])
 def test_tiles_of_any_pixel_count(gpu, oracle, w, h, tile):

@@ -73,6 +73,23 @@ void profile_mark(int stage, bool start, hipStream_t stream) {
 
 }  // namespace tdgs
 
+namespace tdgs {
+
+// Makes `device` current for the scope and restores the caller's current device after it.
+struct DeviceScope {
+    int prev = -1;
+    hipError_t err;
+    explicit DeviceScope(int device) {
+        err = hipGetDevice(&prev);
+        if (err == hipSuccess) err = hipSetDevice(device);
+    }
+    ~DeviceScope() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+}  // namespace tdgs
+
 using namespace tdgs;
 
 extern "C" {
@@ -87,7 +104,8 @@ int tdgs_ctx_create(int device, tdgs_ctx** ctx_out) {
     int count = 0;
     TDGS_HIP(hipGetDeviceCount(&count));
     TDGS_REQUIRE(device >= 0 && device < count, "device %d out of range (%d devices)", device, count);
-    TDGS_HIP(hipSetDevice(device));
+    DeviceScope scope(device);   // the caller's current device is left as it was
+    TDGS_HIP(scope.err);
     tdgs_ctx* c = new tdgs_ctx();
     c->device = device;
     hipError_t e = hipMalloc((void**)&c->d_counters, sizeof(int64_t) * (kCounters + kMonitor));
@@ -110,6 +128,8 @@ int tdgs_ctx_create(int device, tdgs_ctx** ctx_out) {
 
 int tdgs_ctx_destroy(tdgs_ctx* ctx) {
     if (!ctx) return TDGS_OK;
+    DeviceScope scope(ctx->device);   // wait for the context's device, not the caller's current one
+    TDGS_HIP(scope.err);
     TDGS_HIP(hipDeviceSynchronize());
     TDGS_HIP(hipFree(ctx->d_counters));
     TDGS_HIP(hipHostFree(ctx->h_counters));
