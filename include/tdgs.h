@@ -228,6 +228,8 @@ enum {
 /* ---- context, errors, device memory plumbing --------------------------------------- */
 int tdgs_abi_version(void);
 const char* tdgs_last_error(void);
+/* Both work on the context's device and leave the caller's current device unchanged;
+ * tdgs_ctx_destroy first waits for that device's work to finish. */
 int tdgs_ctx_create(int device, tdgs_ctx** ctx_out);
 int tdgs_ctx_destroy(tdgs_ctx* ctx);
 int tdgs_malloc(void** ptr_out, size_t bytes);
