@@ -375,10 +375,12 @@ enum { TDGS_FRAME_OK = 0, TDGS_FRAME_KEY_CAPACITY = 1, TDGS_FRAME_KEY_RANGE = 2 
 int tdgs_render_counts(void* stream, const tdgs_render_buffers* buf, int64_t* counts_out);
 
 /* Frame monitor of the context's TDGS_FLAG_DEVICE_COUNTS renders, in pinned host memory that
- * the device updates at every such frame: [frames, largest key count, frames whose keys did
- * not fit the key arrays, last key count]. Readable at any time without synchronisation (the
- * frames still in flight are not counted yet); lets a training loop grow its key arrays ahead
- * of need. No reference counterpart. */
+ * the device updates at every such frame (when its blending starts): [frames, largest key
+ * count, frames whose keys did not fit the key arrays, last key count, device error flags
+ * pending at the last frame (non-zero: tdgs_ctx_check reports TDGS_ERR_DEVICE)]. Readable at
+ * any time without synchronisation (the frames still in flight are not counted yet); lets a
+ * training loop grow its key arrays ahead of need and re-run a frame whose keys did not fit.
+ * No reference counterpart. */
 int tdgs_ctx_frame_monitor(tdgs_ctx* ctx, const int64_t** monitor_out);
 
 /* The sorted keys of the last tdgs_render with these buffers and tiling (nb_keys keys), as
@@ -475,8 +477,10 @@ int tdgs_adc_reset_stats(void* stream, tdgs_adc_buffers* adc, int32_t n);
 
 /* L1 part of the loss and its gradient (training.jl:206-215):
  * grad = (rendered > gt ? w : -w) + dssim_weight * dssim_grad (dssim_grad may be null),
- * w = l1_weight / count. Adds sum |rendered - gt| to *l1_sum_dev (device double, may be
- * null; the caller zeroes it). */
+ * w = l1_weight / count; a tie (rendered == gt) takes -w as the reference's ifelse does, and
+ * the product is rounded before the sum (no fused multiply-add), as the reference's broadcast.
+ * Adds sum |rendered - gt| to *l1_sum_dev (device double, may be null; the caller zeroes it).
+ * The trainer uses it when the D-SSIM weight is 0. */
 int tdgs_l1_loss_grad(void* stream, const float* rendered, const float* gt, int64_t count,
                       float l1_weight, float dssim_weight, const float* dssim_grad,
                       float* grad_out, double* l1_sum_dev);

@@ -548,7 +548,10 @@ void oracle_adc_remap_fgidx(const tdgs_adc_buffers* adc, int32_t* fgidx_to_gidx,
     }
 }
 
-// L1 loss gradient (training.jl:206-215).
+// L1 loss gradient (training.jl:206-215): the pixel weight l1_px_weight = (1 - w) / length
+// (:213, l1_weight = 1 - w), +weight where rendered > gt and -weight otherwise (ties included,
+// :214-215), plus w times the D-SSIM gradient as a separate product and sum (Julia's broadcast
+// `ifelse.(...) .+ weight .* grad` rounds the product, then the sum; no fused multiply-add).
 double oracle_l1_loss_grad(const float* rendered, const float* gt, int64_t count, float l1_weight,
                            float dssim_weight, const float* dssim_grad, float* grad_out) {
     const float w = l1_weight / (float)count;
@@ -556,7 +559,7 @@ double oracle_l1_loss_grad(const float* rendered, const float* gt, int64_t count
     for (int64_t i = 0; i < count; ++i) {
         acc += std::fabs((double)rendered[i] - (double)gt[i]);
         const float base = rendered[i] > gt[i] ? w : -w;
-        grad_out[i] = dssim_grad ? fmaf(dssim_weight, dssim_grad[i], base) : base;
+        grad_out[i] = dssim_grad ? base + dssim_weight * dssim_grad[i] : base;
     }
     return acc;
 }

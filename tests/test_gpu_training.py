@@ -90,8 +90,7 @@ def test_adc_bit_exact(gpu, oracle):
     gd = gpu.TrainableGaussiansVector.from_host(g, 0)
     adc = training.AdaptiveDensityControlBuffers(n, 0)
     adc.accum.copy_(torch.from_numpy(adc_h.accum))
-    adc.counts.copy_(torch.from_numpy(rng.integers(0, 1, 1).astype(np.int32)).expand(0) if False else
-                     torch.from_numpy(adc_h.counts))
+    adc.counts.copy_(torch.from_numpy(adc_h.counts))
     nn = training.adc_plan_(adc, gd, *args)
     assert nn == nn_h
     for a, b in ((adc.prune, adc_h.prune), (adc.densify, adc_h.densify), (adc.clone, adc_h.clone),
@@ -163,7 +162,8 @@ def _ssim_torch(x, y):
     return ((2 * mx * my + c1) * (2 * sxy + c2)) / ((mx ** 2 + my ** 2 + c1) * (sxx + syy + c2))
 
 
-@pytest.mark.parametrize("W,H,w", [(64, 48, 0.2), (123, 77, 0.2), (320, 240, 0.5)])
+@pytest.mark.parametrize("W,H,w", [(64, 48, 0.2), (123, 77, 0.2), (320, 240, 0.5), (1297, 840, 0.2),
+                                   (1920, 1080, 0.2)])
 def test_loss_grad_against_textbook_ssim(gpu, W, H, w):
     from tdgs_amd import training
     gen = torch.Generator().manual_seed(W * H)
@@ -186,6 +186,33 @@ def test_loss_grad_against_textbook_ssim(gpu, W, H, w):
     assert abs(s[1] - float(ssim)) <= 1e-4 * abs(float(ssim))
     got = grad.cpu().numpy()
     assert np.linalg.norm(got - ref_grad) <= 1e-3 * np.linalg.norm(ref_grad)
+
+
+@pytest.mark.parametrize("with_dssim", [False, True])
+def test_l1_loss_grad_against_oracle(gpu, oracle, with_dssim):
+    """tdgs_l1_loss_grad (training.jl:206-215) bit for bit against the oracle, on an image with
+    a quarter of its values tied (a tie takes -w), and its L1 sum."""
+    from tdgs_amd import training
+    W, H = 257, 131
+    rng = np.random.default_rng(21 + with_dssim)
+    r = rng.random((W, H, 3), dtype=np.float32)
+    gt = np.where(rng.random((W, H, 3)) < 0.25, r, rng.random((W, H, 3), dtype=np.float32)).astype(np.float32)
+    dg = (rng.standard_normal((W, H, 3)) * 1e-3).astype(np.float32) if with_dssim else None
+    weight = 0.2
+    l1_w = float(np.float32(1) - np.float32(weight))
+    s_ref, ref = oracle.l1_loss_grad(r, gt, l1_w, weight if with_dssim else 0.0, dg)
+    out = torch.empty((W, H, 3), dtype=torch.float32, device=DEV)
+    l1 = torch.zeros(1, dtype=torch.float64, device=DEV)
+    training.l1_loss_grad_(torch.from_numpy(r).to(DEV), torch.from_numpy(gt).to(DEV), out, l1_w,
+                           weight if with_dssim else 0.0, None if dg is None else torch.from_numpy(dg).to(DEV), l1)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    assert abs(float(l1) - s_ref) <= 1e-12 * s_ref
+    ties = r == gt
+    assert ties.sum() > 0.2 * r.size
+    if not with_dssim:
+        w = np.float32(np.float32(l1_w) / np.float32(r.size))
+        assert bool((out.cpu().numpy()[ties] == -w).all())
 
 
 def test_opacity_reset_and_sh_resize(gpu):

@@ -302,8 +302,11 @@ class RenderBuffers:
         return self.temp[:32].view(torch.int64)
 
     def ensure_capacity(self, n):
+        """Grows the per-Gaussian arrays to n entries; the key arrays grow in proportion (a
+        frame of n Gaussians duplicates about n / capacity times as many keys)."""
         if n > self.capacity:
-            self.__init__(n, self.tiling, self.device.index, self.key_capacity, self.keep is not None)
+            keys = int(self.key_capacity * (n / max(self.capacity, 1))) + 1024
+            self.__init__(n, self.tiling, self.device.index, keys, self.keep is not None)
 
     def struct(self):
         b = abi.RenderBuffersC()

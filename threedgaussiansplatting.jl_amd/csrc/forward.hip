@@ -1559,7 +1559,8 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
             a.frame[2] = a.dcount[4];
             a.frame[3] = status;
             const int64_t mon[kMonitor] = {a.mon[0] + 1, a.mon[1] > keys ? a.mon[1] : keys,
-                                           a.mon[2] + (status != kFrameOk ? 1 : 0), keys};
+                                           a.mon[2] + (status != kFrameOk ? 1 : 0), keys,
+                                           a.dcount[kErrSlot] & 0xffffffffll};
 #pragma unroll
             for (int k = 0; k < kMonitor; ++k) {
                 a.mon[k] = mon[k];

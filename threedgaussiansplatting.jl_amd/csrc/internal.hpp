@@ -17,9 +17,10 @@ namespace tdgs {
 
 constexpr int kCounters = 12;
 // Frame monitor of device-count renders: [frames, largest M, frames whose keys did not fit,
-// last M], kept on the device after the counters (d_counters + kCounters) and copied to the
-// host (h_monitor) by every such frame.
-constexpr int kMonitor = 4;
+// last M, the device error flags pending when the last frame blended], kept on the device
+// after the counters (d_counters + kCounters) and copied to the host (h_monitor) by every
+// such frame.
+constexpr int kMonitor = 5;
 // Slot of ctx->d_counters holding the sticky device error flags (low 32 bits): kernels OR
 // kErr* bits into it; every host synchronisation through read_counters reports and clears it.
 constexpr int kErrSlot = 7;

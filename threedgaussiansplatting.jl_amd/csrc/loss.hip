@@ -333,8 +333,8 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         const float dssim = -(f[c] + 2.0f * xv[c] * f[3 + c] + yv[c] * f[6 + c]);
-        const float s = xv[c] > yv[c] ? w_l1 : -w_l1;
-        grad[p + c] = fmaf(w_ssim, dssim, s);
+        const float s = xv[c] > yv[c] ? w_l1 : -w_l1;   // ties take -w_l1 (training.jl:214-215)
+        grad[p + c] = s + w_ssim * dssim;   // product rounded, then the sum, as the reference's broadcast
     }
 }
 

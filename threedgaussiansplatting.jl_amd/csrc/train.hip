@@ -313,8 +313,8 @@ __global__ __launch_bounds__(256) void k_l1_grad(const float* __restrict__ r, co
         if (i < count) {
             const float a = r[i], b = gt[i];
             acc += fabs((double)a - (double)b);
-            const float s = a > b ? w : -w;
-            grad[i] = dg ? fmaf(dw, dg[i], s) : s;
+            const float s = a > b ? w : -w;   // ties take -w (training.jl:214-215)
+            grad[i] = dg ? s + dw * dg[i] : s;   // product rounded, then the sum (no FMA)
         }
     }
     if (!l1) return;

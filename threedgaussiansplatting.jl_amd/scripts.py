@@ -282,6 +282,7 @@ def train(input_dir, output_dir, render_options_from_camera=None, training_optio
     result = TrainResult(trainer)
     while trainer.iteration_nb <= options.nb_iterations:
         if _should(trainer.iteration_nb, evaluation_iterations):
+            trainer.finish_()   # the last step complete (re-run if its keys did not fit), errors raised
             log(f"Losses after iteration {trainer.iteration_nb}:")
             for kind, group in (("Training", train_cwis), ("Validation", val_cwis)):
                 ev = evaluate_losses(trainer, group, tiling)
@@ -291,11 +292,16 @@ def train(input_dir, output_dir, render_options_from_camera=None, training_optio
                 log(f"  {kind}:\n    MSE (L2): {ev[0]}\n    MAE (L1): {ev[1]}\n    DSSIM:    {ev[2]}")
         trainer.training_step_()
         if _should(trainer.iteration_nb, save_iterations):
+            trainer.finish_()
             d = os.path.join(output_dir, "point_cloud", f"iteration_{trainer.iteration_nb}")
             os.makedirs(d, exist_ok=True)
             path = os.path.join(d, "point_cloud.ply")
             ply.save_3dgs_ply(path, trainer.gaussians.to_host())
             result.saved.append((trainer.iteration_nb, path))
             log(f"Saved Gaussians model after {trainer.iteration_nb} iterations to {path}")
+    trainer.finish_()
+    if trainer.replayed_steps:
+        log(f"{trainer.replayed_steps} device-count steps needed more keys than the key arrays held "
+            "and were run again with host counts")
     torch.cuda.synchronize(trainer.device)
     return result

@@ -9,14 +9,16 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import time
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 
 from . import abi
-from .core import (FilteredGaussiansGradientsVector, RenderBuffers, RenderOutputs, TrainableGaussiansVector,
-                   _dev, backward_, backward_render_tiles_, check, context, dptr, lib, render_, stream_ptr)
+from .core import (Context, FilteredGaussiansGradientsVector, RenderBuffers, RenderOutputs,
+                   TrainableGaussiansVector, _dev, backward_, backward_render_tiles_, check, context, ctx_check, dptr,
+                   lib, render_, stream_ptr)
 from .host import PinholeCamera, RenderOptions, Tiling, logit32
 
 f32 = np.float32
@@ -202,14 +204,28 @@ def adc_stats_(adc: AdaptiveDensityControlBuffers, fgradients, fgidx_to_gidx, nb
                                C.c_int32(camera.width), C.c_int32(camera.height)))
 
 
-def adc_plan_(adc, gaussians, prune_logit, use_max_scale, log_max_scale, grad_threshold, log_size_threshold):
-    """Masks, counts scan and ngidx_to_gidx (training.jl:325-397); returns the new count."""
+def adc_plan_(adc, gaussians, prune_logit, use_max_scale, log_max_scale, grad_threshold, log_size_threshold,
+              ctx=None):
+    """Masks, counts scan and ngidx_to_gidx (training.jl:325-397); returns the new count.
+    Synchronises and reports the device error flags of ctx (default: the device's context)."""
     dev = gaussians.device.index
     nn = C.c_int32(0)
-    check(lib().tdgs_adc_plan(context(dev), stream_ptr(dev), C.byref(adc.struct()), C.byref(gaussians.struct()),
+    check(lib().tdgs_adc_plan(context(dev) if ctx is None else ctx.handle, stream_ptr(dev), C.byref(adc.struct()), C.byref(gaussians.struct()),
                               C.c_float(prune_logit), C.c_int32(int(use_max_scale)), C.c_float(log_max_scale),
                               C.c_float(grad_threshold), C.c_float(log_size_threshold), C.byref(nn)))
     return int(nn.value)
+
+
+def adc_plan_thresholds(iteration_nb: int, options: TrainingOptions):
+    """The arguments of adc_plan_ after the Gaussians at an ADC step (training.jl:327-350):
+    (logit(pruning_min_opacity), whether the max-scale prune applies, log(pruning_3d_max_scale),
+    the gradient threshold, log(densification_size_threshold)), in float32 as the reference
+    computes them. The max-scale prune applies only once iteration_nb > opacity_reset_interval
+    (:337-349)."""
+    o = options
+    return (float(logit32(o.pruning_min_opacity)), iteration_nb > o.opacity_reset_interval,
+            float(np.log(f32(o.pruning_3d_max_scale))), o.densification_mean2d_grad_norm_threshold_ndc,
+            float(np.log(f32(o.densification_size_threshold))))
 
 
 def adaptive_density_control_(adc, gaussians: TrainableGaussiansVector, optimizer: AdamOptimizer, n_new,
@@ -368,16 +384,25 @@ class Trainer:
                  seed: int = 0, device=0, fuse_optimizer: bool = True, record_adc: bool = False,
                  device_counts: bool = True):
         self.device = _dev(device)
-        # device_counts: steps without density control (with the fused optimiser) render with
-        # TDGS_FLAG_DEVICE_COUNTS, so they issue no host synchronisation; the key arrays are
-        # grown ahead of need from the context's frame monitor (pinned memory the device
-        # updates), and a step whose keys did not fit is skipped by the device and counted in
-        # skipped_steps
+        # the trainer's own library context: its frame monitor counts this trainer's
+        # device-count frames only, and its error flags are this trainer's
+        self.ctx = Context(self.device.index)
+        # device_counts: steps without density control or opacity reset (with the fused
+        # optimiser) render with TDGS_FLAG_DEVICE_COUNTS, so they wait for no count on the host.
+        # Before the next step is issued, the host waits until the context's frame monitor
+        # (pinned memory the device writes when the frame's blending starts, with a whole
+        # step of kernels still queued behind it) shows that frame. A frame whose keys did not
+        # fit rendered as render_void! and left the parameters and moments untouched; it is
+        # then run again with host counts (which grow the key arrays), from the same state, so
+        # no step is dropped (replayed_steps counts them). The key arrays are also grown ahead
+        # of need from the monitor's key counts.
         self.device_counts = device_counts
-        self.skipped_steps = 0
+        self.replayed_steps = 0
         self._monitor = None
-        # the monitor's frames and overflow frames before this trainer's first frame
-        self._monitor_frames0, _, self._monitor_seen, _ = self.frame_monitor() if device_counts else (0, 0, 0, 0)
+        self._monitor_frames0 = 0      # a new context: no frame before this trainer's
+        self._monitor_seen = 0         # overflow frames already handled
+        self._dc_frames = 0            # device-count frames issued
+        self._unconfirmed = None       # (camera index, camera) of the last device-count step
         self._largest_keys = 0   # largest key count of this trainer's frames seen on the monitor
         # record_adc: keep per density-control step the counts of pruned, cloned and split
         # Gaussians in adc_history (three reductions and a synchronisation per ADC step)
@@ -419,6 +444,7 @@ class Trainer:
 
     def training_step_(self):
         """training_step! (training.jl:173-244)."""
+        self.confirm_device_count_step_()
         self.iteration_nb += 1
         self.cameras_order_idx += 1
         if self.cameras_order_idx >= len(self.cameras_order):
@@ -433,16 +459,32 @@ class Trainer:
         cam = self.cameras[k]
         self.last_camera = cam
         dev_counts = (self.device_counts and self.fuse_optimizer and not self.adc_step_due()
+                      and not self.opacity_reset_due()
                       and self.fgradients.capacity >= self.render_buffers.capacity
                       and self.tiling.nb_tiles <= 65535)
+        in_adc = self._render_to_update_(k, cam, dev_counts)
+        if in_adc:
+            self.complete_adc_step_()
+        self.maybe_opacity_reset_()
+
+    def _render_to_update_(self, k, cam, dev_counts):
+        """The part of training_step! from render! to update! (training.jl:186-236) with
+        camera k; True when density control ran."""
         if dev_counts:
             self._grow_keys_from_monitor()
         render_(self.render_outputs, self.gaussians, cam, self.tiling, self.render_options, self.render_buffers,
-                device_counts=dev_counts)
+                device_counts=dev_counts, ctx=self.ctx)
+        if dev_counts:
+            self._dc_frames += 1
+            self._unconfirmed = (k, cam)
         self.loss_sums.zero_()
         gt = self.images.acquire(k)
-        loss_grad_(self.render_outputs.rgb, gt, self.rgb_image_grad,
-                   self.options.loss_dssim_vs_L1_weight, self.loss_sums, self.loss_temp)
+        w = self.options.loss_dssim_vs_L1_weight
+        if w == 0:
+            # L1 only: the reference still evaluates D-SSIM with weight 0 (training.jl:202-215)
+            l1_loss_grad_(self.render_outputs.rgb, gt, self.rgb_image_grad, 1.0, 0.0, None, self.loss_sums[0:1])
+        else:
+            loss_grad_(self.render_outputs.rgb, gt, self.rgb_image_grad, w, self.loss_sums, self.loss_temp)
         self.images.release(k)
         if self.fuse_optimizer and not self.adc_step_due():
             # no density control between the backward pass and update!: the backward
@@ -459,35 +501,64 @@ class Trainer:
             self.update_learning_rates_()
             self.optimizer.update_(self.fgradients, self.render_buffers.fgidx_to_gidx,
                                    self.render_buffers.nb_fgaussians, self.render_options.sh_degree)
-        if in_adc:
-            self.complete_adc_step_()
-        self.maybe_opacity_reset_()
+        return in_adc
+
+    def confirm_device_count_step_(self, timeout_s: float = 60.0):
+        """Waits until the frame monitor shows the last device-count step's frame (its
+        blending has started, so the rest of that step is still queued on the device), raises
+        on device error flags, and re-runs that step with host counts when its keys did not
+        fit (the device left the parameters and moments untouched; update! counted the step,
+        so the count is taken back first). Every step is thereby applied exactly once, in
+        order. training_step_ calls it first; call it after the last step (finish_)."""
+        if self._unconfirmed is None:
+            return
+        k, cam = self._unconfirmed
+        self._unconfirmed = None
+        target = self._monitor_frames0 + self._dc_frames
+        mon = self.frame_monitor()
+        if mon[0] < target:
+            t0 = time.monotonic()
+            while mon[0] < target:
+                if time.monotonic() - t0 > timeout_s:
+                    ctx_check(self.device.index, self.ctx)   # raises on a device-side error
+                    raise RuntimeError(f"frame {target} of the trainer's context did not start blending "
+                                       f"within {timeout_s} s (monitor {mon})")
+                time.sleep(0)
+                mon = self.frame_monitor()
+        if mon[4]:
+            ctx_check(self.device.index, self.ctx)   # reports and clears the flags
+            raise RuntimeError(f"device error flags {mon[4]:#x} at training iteration {self.iteration_nb}")
+        if mon[2] > self._monitor_seen:
+            self._monitor_seen = mon[2]
+            self._largest_keys = max(self._largest_keys, mon[3])
+            self.replayed_steps += 1
+            self.optimizer.update_count -= 1
+            self._render_to_update_(k, cam, False)
+
+    def finish_(self):
+        """Confirms the last step (see confirm_device_count_step_) and checks the context's
+        device error flags (synchronises)."""
+        self.confirm_device_count_step_()
+        ctx_check(self.device.index, self.ctx)
 
     def frame_monitor(self):
-        """The context's frame monitor (tdgs_ctx_frame_monitor): [frames, largest key count,
-        frames whose keys did not fit, last key count] of the device-count renders so far, read
-        without synchronisation."""
+        """The trainer context's frame monitor (tdgs_ctx_frame_monitor): [frames, largest key
+        count, frames whose keys did not fit, last key count, pending device error flags] of
+        its device-count renders so far, read without synchronisation."""
         if self._monitor is None:
             p = C.POINTER(C.c_int64)()
-            check(lib().tdgs_ctx_frame_monitor(context(self.device.index), C.byref(p)))
+            check(lib().tdgs_ctx_frame_monitor(self.ctx.handle, C.byref(p)))
             self._monitor = p
-        return [int(self._monitor[i]) for i in range(4)]
+        return [int(self._monitor[i]) for i in range(5)]
 
     def _grow_keys_from_monitor(self):
         """Grows the key arrays to 1.5x the largest key count seen once it passes 80% of the
-        capacity (at least doubling them after a frame whose keys did not fit), and counts the
-        device-count frames whose keys did not fit (their steps were skipped on the device).
-        The monitor shows the frames completed so far, so the count of the last step may only
-        show at a later one."""
-        frames, _, overflows, last = self.frame_monitor()
+        capacity (the monitor shows the frames whose blending has started)."""
+        frames, _, _, last, _ = self.frame_monitor()
         if frames > self._monitor_frames0:
             self._largest_keys = max(self._largest_keys, last)
         b = self.render_buffers
         want = int(1.5 * self._largest_keys) + 1024 if self._largest_keys > 0.8 * b.key_capacity else 0
-        if overflows > self._monitor_seen:
-            self.skipped_steps += overflows - self._monitor_seen
-            self._monitor_seen = overflows
-            want = max(want, 2 * b.key_capacity)
         if want > b.key_capacity:
             b._alloc_keys(want)
 
@@ -523,12 +594,17 @@ class Trainer:
         m.sh = sh_resize(m.sh, d, 2)
         m.sh_degree = d
 
-    def maybe_opacity_reset_(self):
-        """maybe_opacity_reset! (training.jl:272-280)."""
+    def opacity_reset_due(self):
+        """Whether maybe_opacity_reset! resets the opacities at this iteration."""
         o = self.options
         it = self.iteration_nb
-        if o.opacity_reset_start_iteration_nb <= it <= o.opacity_reset_final_iteration_nb and \
-                it % o.opacity_reset_interval == 0:
+        return o.opacity_reset_start_iteration_nb <= it <= o.opacity_reset_final_iteration_nb and \
+            it % o.opacity_reset_interval == 0
+
+    def maybe_opacity_reset_(self):
+        """maybe_opacity_reset! (training.jl:272-280)."""
+        if self.opacity_reset_due():
+            o = self.options
             opacity_reset_(self.gaussians, o.opacity_reset_max_value, self.optimizer.moments.opacity)
 
     def update_learning_rates_(self):
@@ -546,10 +622,7 @@ class Trainer:
                    self.render_buffers)
         if not (it >= o.adc_start_iteration_nb and it % o.adc_interval == 0):
             return False
-        n_new = adc_plan_(self.adc, self.gaussians, float(logit32(o.pruning_min_opacity)),
-                          it > o.opacity_reset_interval, float(np.log(f32(o.pruning_3d_max_scale))),
-                          o.densification_mean2d_grad_norm_threshold_ndc,
-                          float(np.log(f32(o.densification_size_threshold))))
+        n_new = adc_plan_(self.adc, self.gaussians, *adc_plan_thresholds(it, o), ctx=self.ctx)
         if self.record_adc:
             n = len(self.gaussians)
             a = self.adc
