@@ -297,11 +297,13 @@ def train_cfg1(core, steps=100, warmup=5):
             "steps": steps, "loss_last": round(float(tr.current_loss()), 6)}
 
 
-def train_cfg3(core, iterations):
+def train_cfg3(core, iterations, grad_threshold=None):
     """Config 3: the full training loop from 500k Gaussians (1297x840, SH3, 100 orbit cameras,
     seeded uniform-noise targets) with the reference TrainingOptions defaults for
     `iterations` iterations: density control every 100 iterations from 600, opacity reset at
-    3000. Wall time of all iterations, densification and pruning included."""
+    3000. Wall time of all iterations, densification and pruning included. grad_threshold
+    replaces the densification threshold (2e-4): with uniform-noise targets the default keeps
+    the count near 500k, a lower one grows it past 1M as the config's "up to ~1.5M" says."""
     import torch
     from tdgs_amd import host, synthetic, training
     w = synthetic.config(3)
@@ -311,7 +313,8 @@ def train_cfg3(core, iterations):
     gen = torch.Generator(device="cuda").manual_seed(0x3D6503)
     images = [torch.rand((c.width, c.height, 3), generator=gen, device="cuda") for c in cams]
     opts = host.RenderOptions.for_camera(cams[0], 3)
-    to = training.TrainingOptions.for_scene(host.scene_radius(cams), nb_iterations=iterations)
+    kw = {} if grad_threshold is None else {"densification_mean2d_grad_norm_threshold_ndc": grad_threshold}
+    to = training.TrainingOptions.for_scene(host.scene_radius(cams), nb_iterations=iterations, **kw)
     tr = training.Trainer(g, cams, images, opts, tiling, to, seed=3, record_adc=True)
     n0 = len(tr.gaussians)
     torch.cuda.synchronize()
@@ -320,12 +323,62 @@ def train_cfg3(core, iterations):
     for _ in range(iterations):
         tr.training_step_()
         nmax = max(nmax, len(tr.gaussians))
+    tr.finish_()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    assert tr.optimizer.update_count == iterations
     return {"workload": w.name + f", {iterations} iterations with density control",
+            "densification_threshold": to.densification_mean2d_grad_norm_threshold_ndc,
             "train_it_per_s": round(iterations / dt, 2), "seconds": round(dt, 3), "iterations": iterations,
             "gaussians_initial": n0, "gaussians_final": len(tr.gaussians), "gaussians_max": nmax,
+            "steps_rerun_with_host_counts": tr.replayed_steps,
             "density_control": tr.adc_history, "loss_last": round(float(tr.current_loss()), 6)}
+
+
+def sort_pairs_bench(core, n=120_000_000, end_bit=46, repeats=5):
+    """tdgs_sort_pairs (the drop-in of cub_sort_pairs_wrapper.cu:31-43) on n random (tile, depth
+    bits) keys with end_bit 46 (cfg4's 16320 tiles), as forward_core.jl:618-660 calls it at
+    cfg4's scale: HIP events around each call, median. Bytes: this build's passes (8-bit
+    digits: per pass a count reading the keys, a scatter reading and writing keys and values,
+    8 + 2 (8 + 4) = 32 B per key) and CUB's onesweep passes over the same bits (reading and
+    writing keys and values, 2 (8 + 4) = 24 B per key and pass, plus one read of the keys for
+    its histograms)."""
+    import torch
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device="cuda").manual_seed(0x5047)
+    tile = torch.randint(1, 16321, (n,), generator=gen, device=dev, dtype=torch.int64)
+    depth = torch.randint(0x3c000000, 0x42000000, (n,), generator=gen, device=dev, dtype=torch.int64)
+    keys = (tile << 32) | depth
+    del tile, depth
+    vals = torch.arange(1, n + 1, dtype=torch.int32, device=dev)
+    L = core.lib()
+    tb = int(L.tdgs_sort_pairs_temp_bytes(n, end_bit))
+    temp = torch.empty(tb, dtype=torch.uint8, device=dev)
+    ko = torch.empty_like(keys)
+    vo = torch.empty_like(vals)
+    stream = core.stream_ptr(0)
+    times = []
+    for r in range(repeats + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        core.check(L.tdgs_sort_pairs(core.dptr(temp), tb, core.dptr(keys), core.dptr(ko), core.dptr(vals),
+                                     core.dptr(vo), n, end_bit, stream))
+        e1.record()
+        torch.cuda.synchronize()
+        if r > 0:
+            times.append(e0.elapsed_time(e1))
+    ms = float(np.median(times))
+    assert bool((ko[1:] >= ko[:-1]).all())
+    passes = -(-end_bit // 8)
+    impl = passes * 32 * n
+    cub = passes * 24 * n + 8 * n
+    del keys, vals, ko, vo, temp
+    torch.cuda.empty_cache()
+    return {"keys": n, "end_bit": end_bit, "passes": passes, "ms": round(ms, 3),
+            "keys_per_s": round(n / (ms * 1e-3), 1),
+            "impl_bytes": impl, "impl_GBs": round(impl / (ms * 1e-3) / 1e9, 1),
+            "impl_hbm_frac": round(impl / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "cub_equivalent_bytes": cub, "cub_equivalent_GBs": round(cub / (ms * 1e-3) / 1e9, 1)}
 
 
 def render_other_tiling(core, w, g, tile, frames=240, warmup=10):
@@ -751,7 +804,11 @@ def main():
         torch.cuda.empty_cache()
         extra["train_cfg3"] = train_cfg3(core, args.cfg3_iterations)
         torch.cuda.empty_cache()
+        extra["train_cfg3_growth"] = train_cfg3(core, args.cfg3_iterations, grad_threshold=3.5e-5)
+        torch.cuda.empty_cache()
         extra["stress_cfg4"] = stress_cfg4(core)
+        torch.cuda.empty_cache()
+        extra["sort_pairs_cfg4_scale"] = sort_pairs_bench(core)
 
     res = {
         "metric": "render fps + train it/s at 1M Gaussians 1080p SH3 (1 GPU); % HBM roofline",

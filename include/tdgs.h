@@ -310,8 +310,11 @@ int tdgs_scan_counts(tdgs_ctx* ctx, void* stream, const int32_t* counts, int32_t
  * calls no allocating routine and needs no context or scratch argument: the per-tile partial
  * sums live in a fixed static device array of 64 KiB (per GPU, held until the process ends),
  * so n may be at most TDGS_SCAN_NOALLOC_MAX_ITEMS (TDGS_ERR_INVALID beyond). It does not
- * synchronise: the total is written to total_dev (device memory, one int64). Calls that
- * overlap on one GPU (different streams or host threads) share that array and race. */
+ * synchronise: the total is written to total_dev (device memory, one int64). Unlike
+ * tdgs_scan_counts it cannot fail on a total of 2^31 or more (it does not look at the total
+ * on the host): counts_cs[i] then holds the inclusive sum modulo 2^32 as an int32, so a caller
+ * must check *total_dev < 2^31 before using counts_cs. Calls that overlap on one GPU
+ * (different streams or host threads) share that array and race. */
 #define TDGS_SCAN_NOALLOC_MAX_ITEMS 16777216
 int tdgs_scan_counts_noalloc(void* stream, const int32_t* counts, int32_t n, int32_t* counts_cs,
                              int64_t* total_dev);

@@ -154,6 +154,21 @@ def blend_tile(cam, tiling, opts, f2d, depths, entries, beg, tx, ty, rgb, T, dep
                             ptr(rgb), ptr(T), ptr(depth), ptr(last))
 
 
+def backward_tile(cam, tiling, opts, f2d, entries, beg, tx, ty, rgb_grad, T, last, acc):
+    """backward_render_tiles_kernel! (backward_core.jl:96-293) for tile (tx, ty) alone: its
+    sorted entries beg + 1, beg + 2, ... (1-based) are `entries` (1-based fgidx values); adds the
+    tile's 2D gradients into acc ((nb_f, 9) float64)."""
+    entries = np.ascontiguousarray(entries, np.int32)
+    f2d = np.ascontiguousarray(f2d, np.float32)
+    assert acc.dtype == np.float64 and acc.flags.c_contiguous and acc.shape[1] == 9
+    c_cam, c_t, c_o = cam.to_c(), tiling.to_c(), opts.to_c()
+    lib().oracle_backward_tile(C.byref(c_cam), C.byref(c_t), C.byref(c_o), ptr(f2d), ptr(entries),
+                               C.c_int64(beg), C.c_int64(beg + entries.size), C.c_int32(tx), C.c_int32(ty),
+                               ptr(np.ascontiguousarray(rgb_grad, np.float32)),
+                               ptr(np.ascontiguousarray(T, np.float32)), ptr(np.ascontiguousarray(last, np.int32)),
+                               ptr(acc))
+
+
 def fill_fgidx_to_gidx(keep):
     keep = np.ascontiguousarray(keep, dtype=np.uint8)
     n = keep.size

@@ -289,15 +289,47 @@ int64_t oracle_render(const tdgs_gaussians* g, const tdgs_camera* cam, const tdg
     return m;
 }
 
-// backward_render_tiles_kernel! (backward_core.jl:96-293): each pixel replays its tile's
-// list from its last contributor back to the first entry. Gradients are accumulated in
-// double precision per filtered Gaussian (grads2d_acc: 9 x nb_f doubles).
+// backward_render_tiles_kernel! (backward_core.jl:96-293) for tile (tx, ty): each pixel replays
+// the tile's list from its last contributor back to the first entry. The list's entries
+// first..end (1-based positions in the frame's sorted list) are list[first - base ..
+// end - base] (list[0] holds position base). Gradients are accumulated in double precision per
+// filtered Gaussian (acc: 9 x nb_f doubles).
+static void backward_tile(const tdgs_camera* cam, const tdgs_tiling* t, const tdgs_render_options* opt,
+                          const float* f2d, const int32_t* list, int64_t base, int64_t first, int64_t end, int tx,
+                          int ty, const float* rgb_grad, const float* T_img, const int32_t* last_img, double* acc) {
+    const int W = cam->width, H = cam->height, TW = t->tile_width, TH = t->tile_height;
+    for (int pv = 1; pv <= TH; ++pv) {
+        for (int pu = 1; pu <= TW; ++pu) {
+            const int U = pu + (tx - 1) * TW, Vv = pv + (ty - 1) * TH;
+            if (U > W || Vv > H) continue;
+            const int64_t px = (int64_t)(Vv - 1) + (int64_t)H * (U - 1);
+            float T = T_img[px];
+            const int64_t last = last_img[px];
+            const float g[3] = {rgb_grad[3 * px], rgb_grad[3 * px + 1], rgb_grad[3 * px + 2]};
+            float psi[3] = {T * opt->background[0], T * opt->background[1], T * opt->background[2]};
+            const float cu = (float)U - 0.5f, cv = (float)Vv - 0.5f;
+            const int64_t start = std::min(last, end);
+            for (int64_t s = start; s >= first; --s) {
+                const int64_t f = list[s - base] - 1;
+                const float* r = f2d + 9 * f;
+                float du, dv;
+                const float G = backward_gaussian(cu, cv, r[0], r[1], r[3], r[4], r[5], &du, &dv);
+                const float alpha = fminf(opt->max_alpha, r[2] * G);
+                if (alpha < opt->min_alpha) continue;
+                float o[9];
+                backward_pair(alpha, 1.0f / (1.0f - alpha), G, du, dv, r[3], r[4], r[5], r + 6, g, &T, psi, o);
+                for (int k = 0; k < 9; ++k) acc[9 * f + k] += (double)o[k];
+            }
+        }
+    }
+}
+
+// backward_render_tiles_kernel! (backward_core.jl:96-293) over every tile.
 void oracle_backward_render_tiles(const tdgs_camera* cam, const tdgs_tiling* t,
                                   const tdgs_render_options* opt, const float* f2d,
                                   const int32_t* sorted_values, const int32_t* tiles_end,
                                   const float* rgb_grad, const float* T_img,
                                   const int32_t* last_img, double* grads2d_acc) {
-    const int W = cam->width, H = cam->height, TW = t->tile_width, TH = t->tile_height;
     // nb_f is not passed: the accumulator covers the largest referenced fgidx
     int64_t nb_f = 0;
     const int64_t m = tiles_end[(int64_t)t->nb_tiles_x * t->nb_tiles_y - 1];
@@ -311,34 +343,19 @@ void oracle_backward_render_tiles(const tdgs_camera* cam, const tdgs_tiling* t,
             const int tile = tx + (ty - 1) * t->nb_tiles_x;
             const int64_t first = tile == 1 ? 1 : (int64_t)tiles_end[tile - 2] + 1;
             const int64_t end = tiles_end[tile - 1];
-            for (int pv = 1; pv <= TH; ++pv) {
-                for (int pu = 1; pu <= TW; ++pu) {
-                    const int U = pu + (tx - 1) * TW, Vv = pv + (ty - 1) * TH;
-                    if (U > W || Vv > H) continue;
-                    const int64_t px = (int64_t)(Vv - 1) + (int64_t)H * (U - 1);
-                    float T = T_img[px];
-                    const int64_t last = last_img[px];
-                    const float g[3] = {rgb_grad[3 * px], rgb_grad[3 * px + 1], rgb_grad[3 * px + 2]};
-                    float psi[3] = {T * opt->background[0], T * opt->background[1], T * opt->background[2]};
-                    const float cu = (float)U - 0.5f, cv = (float)Vv - 0.5f;
-                    const int64_t start = std::min(last, end);
-                    for (int64_t s = start; s >= first; --s) {
-                        const int64_t f = sorted_values[s - 1] - 1;
-                        const float* r = f2d + 9 * f;
-                        float du, dv;
-                        const float G = backward_gaussian(cu, cv, r[0], r[1], r[3], r[4], r[5], &du, &dv);
-                        const float alpha = fminf(opt->max_alpha, r[2] * G);
-                        if (alpha < opt->min_alpha) continue;
-                        float o[9];
-                        backward_pair(alpha, 1.0f / (1.0f - alpha), G, du, dv, r[3], r[4], r[5], r + 6, g, &T, psi, o);
-                        for (int k = 0; k < 9; ++k) acc[9 * f + k] += (double)o[k];
-                    }
-                }
-            }
+            backward_tile(cam, t, opt, f2d, sorted_values, 1, first, end, tx, ty, rgb_grad, T_img, last_img, acc);
         }
     });
     for (int k = 0; k < (int)part.size(); ++k)
         for (int64_t i = 0; i < 9 * nb_f; ++i) grads2d_acc[i] += part[k][i];
+}
+
+// The same for one tile whose sorted entries beg + 1 .. end (1-based) are list[0 .. end - beg)
+// (a replay on a list the GPU sorted); adds into acc (9 x nb_f doubles).
+void oracle_backward_tile(const tdgs_camera* cam, const tdgs_tiling* t, const tdgs_render_options* opt,
+                          const float* f2d, const int32_t* list, int64_t beg, int64_t end, int32_t tx, int32_t ty,
+                          const float* rgb_grad, const float* T_img, const int32_t* last_img, double* acc) {
+    backward_tile(cam, t, opt, f2d, list, beg + 1, beg + 1, end, tx, ty, rgb_grad, T_img, last_img, acc);
 }
 
 // backward_project_fgaussians_kernel! (backward_core.jl:309-452) + compute_sh_coeffs_grad!

@@ -127,3 +127,28 @@ def test_sh3_mean_gradient_and_jacobian_quirk(oracle, exact):
         assert worst < 1e-2
     else:
         assert worst > 5e-2
+
+
+def test_backward_tile_replay_sums_to_full_backward(oracle):
+    """The per-tile backward replay (oracle_backward_tile, which the GPU cfg4 check runs on
+    the GPU's sorted lists) summed over every tile equals the whole-frame backward pass."""
+    from tdgs_amd import synthetic
+    w = synthetic.config(1, n=3000)
+    cam = w.cameras[0]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, 3)
+    fwd = oracle.render(w.gaussians, cam, t, opts)
+    nf = fwd["nb_fgaussians"]
+    rng = np.random.default_rng(2)
+    grad = rng.normal(0, 1e-3, (cam.width, cam.height, 3)).astype(f32)
+    full = oracle.backward(w.gaussians, cam, t, opts, fwd, grad)["grads2d"]
+    acc = np.zeros((nf, 9), np.float64)
+    te = fwd["tiles_end"].astype(np.int64)
+    sv = fwd["sorted_values"]
+    for tile in range(1, t.nb_tiles + 1):
+        beg = int(te[tile - 2]) if tile > 1 else 0
+        end = int(te[tile - 1])
+        tx, ty = (tile - 1) % t.nb_tiles_x + 1, (tile - 1) // t.nb_tiles_x + 1
+        oracle.backward_tile(cam, t, opts, fwd["f2d"], sv[beg:end], beg, tx, ty, grad, fwd["T"], fwd["last"], acc)
+    assert np.abs(full).max() > 0 and fwd["nb_keys"] > 10_000
+    np.testing.assert_allclose(acc.astype(f32), full, rtol=1e-6, atol=1e-12)
