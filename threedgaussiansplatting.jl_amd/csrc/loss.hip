@@ -86,9 +86,13 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
         const bool in = k < kSsimIn * kSsimIn && v >= 0 && v < H && u >= 0 && u < W;
-        const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
-#pragma unroll
-        for (int c = 0; c < 3; ++c) xy[i][c] = in ? make_float2(x[p + c], y[p + c]) : make_float2(0.0f, 0.0f);
+        const int64_t p = (int64_t)v + (int64_t)H * u;
+        // one 12-byte load per pixel and image (the three channels are contiguous)
+        const float3 xp = in ? reinterpret_cast<const float3*>(x)[p] : make_float3(0.0f, 0.0f, 0.0f);
+        const float3 yp = in ? reinterpret_cast<const float3*>(y)[p] : make_float3(0.0f, 0.0f, 0.0f);
+        xy[i][0] = make_float2(xp.x, yp.x);
+        xy[i][1] = make_float2(xp.y, yp.y);
+        xy[i][2] = make_float2(xp.z, yp.z);
     }
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
@@ -172,7 +176,8 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     for (int q = 0; q < kQF; ++q) m[q] = s_out[(ou * kSsimT + ov) * kOutPitch + q];
     double ssum = 0.0;
     if (on) {
-        const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
+        const int64_t p = (int64_t)v + (int64_t)H * u;
+        const int64_t P = (int64_t)W * H;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const float mx = m[5 * c], my = m[5 * c + 1], sxx = m[5 * c + 2], syy = m[5 * c + 3], sxy = m[5 * c + 4];
@@ -180,13 +185,17 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
             const float a2 = 2.0f * (sxy - mx * my) + kC2;
             const float b1 = mx * mx + my * my + kC1;
             const float b2 = (sxx - mx * mx) + (syy - my * my) + kC2;
-            const float B = b1 * b2;
-            const float S = (a1 * a2) / B;
+            // two divisions per channel: 1/b1 and 1/b2 (B = b1 b2), the quotients as products
+            const float r1 = 1.0f / b1, r2 = 1.0f / b2;
+            const float rB = r1 * r2;
+            const float S = (a1 * a2) * rB;
             const float dA = 2.0f * my * (a2 - a1);
             const float dB = 2.0f * mx * (b2 - b1);
-            dmap[3 * p + c] = (dA - S * dB) / B;      // dS/dmu_x
-            dmap[3 * p + 3 + c] = -S / b2;            // dS/dE[x^2]
-            dmap[3 * p + 6 + c] = 2.0f * a1 / B;      // dS/dE[xy]
+            // planar maps (plane q of W H values, pixel order of the image): consecutive lanes
+            // (consecutive v) write consecutive words
+            dmap[c * P + p] = (dA - S * dB) * rB;     // dS/dmu_x
+            dmap[(3 + c) * P + p] = -S * r2;          // dS/dE[x^2]
+            dmap[(6 + c) * P + p] = 2.0f * a1 * rB;   // dS/dE[xy]
             ssum += (double)S;
         }
     }
@@ -257,10 +266,11 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
     const bool on = v < H && u < W;
     const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
     float xv[3], yv[3];
-#pragma unroll
-    for (int c = 0; c < 3; ++c) {
-        xv[c] = on ? x[p + c] : 0.0f;
-        yv[c] = on ? y[p + c] : 0.0f;
+    {
+        const float3 xp = on ? reinterpret_cast<const float3*>(x)[p / 3] : make_float3(0.0f, 0.0f, 0.0f);
+        const float3 yp = on ? reinterpret_cast<const float3*>(y)[p / 3] : make_float3(0.0f, 0.0f, 0.0f);
+        xv[0] = xp.x; xv[1] = xp.y; xv[2] = xp.z;
+        yv[0] = yp.x; yv[1] = yp.y; yv[2] = yp.z;
     }
     // the tile's nine maps: pixel k = t + 256 i (i < 3) of the 26 x 26 tile, all loads issued
     // before the first LDS store
@@ -272,9 +282,10 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
         const bool in = k < kSsimIn * kSsimIn && v >= 0 && v < H && u >= 0 && u < W;
-        const int64_t p = 9 * ((int64_t)v + (int64_t)H * u);
+        const int64_t p = (int64_t)v + (int64_t)H * u;
+        const int64_t P = (int64_t)W * H;
 #pragma unroll
-        for (int q = 0; q < kQB; ++q) dv[i][q] = in ? dmap[p + q] : 0.0f;
+        for (int q = 0; q < kQB; ++q) dv[i][q] = in ? dmap[q * P + p] : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
@@ -330,12 +341,14 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
     float f[kQB];
 #pragma unroll
     for (int q = 0; q < kQB; ++q) f[q] = s_out[(ou * kSsimT + ov) * kOutPitch + q];
+    float gr[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         const float dssim = -(f[c] + 2.0f * xv[c] * f[3 + c] + yv[c] * f[6 + c]);
         const float s = xv[c] > yv[c] ? w_l1 : -w_l1;   // ties take -w_l1 (training.jl:214-215)
-        grad[p + c] = s + w_ssim * dssim;   // product rounded, then the sum, as the reference's broadcast
+        gr[c] = s + w_ssim * dssim;   // product rounded, then the sum, as the reference's broadcast
     }
+    reinterpret_cast<float3*>(grad)[p / 3] = make_float3(gr[0], gr[1], gr[2]);
 }
 
 static SsimWindow gaussian_window() {
@@ -356,7 +369,8 @@ using namespace tdgs;
 
 extern "C" {
 
-// Scratch: the 9 SSIM partial-derivative maps, then one (|x - y|, S) sum pair per workgroup.
+// Scratch: the 9 SSIM partial-derivative maps (planar: map q of W H values, in the image's
+// pixel order), then one (|x - y|, S) sum pair per workgroup.
 static size_t loss_dmap_bytes(int32_t width, int32_t height) {
     return align_up((size_t)9 * sizeof(float) * (size_t)(width > 0 ? width : 1) * (size_t)(height > 0 ? height : 1));
 }
