@@ -68,6 +68,8 @@ def parse():
                         "would mix into the single-stream kernel durations)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run 10 device-to-device copies of 1 GiB (HBM counter calibration)")
+    p.add_argument("--only", choices=["stress_cfg4", "sort_pairs", "train_cfg3", "train_cfg3_growth"],
+                   help="only run one of the extra legs and print its JSON (kernel profiles of that leg)")
     return p.parse_args()
 
 
@@ -668,6 +670,15 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.only:
+        import torch
+        from tdgs_amd import core
+        torch.cuda.set_device(0)
+        legs = {"stress_cfg4": lambda: stress_cfg4(core), "sort_pairs": lambda: sort_pairs_bench(core),
+                "train_cfg3": lambda: train_cfg3(core, args.cfg3_iterations),
+                "train_cfg3_growth": lambda: train_cfg3(core, args.cfg3_iterations, grad_threshold=3.5e-5)}
+        print(json.dumps({args.only: legs[args.only]()}))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path would shard "

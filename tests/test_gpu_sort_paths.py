@@ -1,4 +1,5 @@
-"""The render pipeline's radix passes in both table layouts, through the C-ABI.
+"""The render pipeline's radix passes in both table layouts and the depth presort's buckets,
+through the C-ABI.
 
 The depth presort and the coarse emission pass take their offsets from grouped count tables
 (per-tile histogram rows plus 16-tile group sums, no scan launch) while the buffers' capacity
@@ -80,3 +81,50 @@ def test_sort_pairs_at_cfg4_scale_properties(gpu):
         del k, v, dk, eq
     assert ties > n // 10
     assert int(seen[0]) == 0 and bool((seen[1:] == 1).all())
+
+
+def test_depth_presort_bucket_past_capacity(gpu, oracle):
+    """The bucketed depth presort (dsort.hpp) takes its splitters from a sample of 4096 slots;
+    a bucket of more than 8192 Gaussians is sorted chunk by chunk through global memory. Here
+    the sampled slots keep the scene's depths while every other Gaussian lies in a narrow depth
+    band (relative width 1e-5) that no sampled key falls in: that band (~46k Gaussians, distinct
+    depths) lands in at most two buckets. The frame must equal the oracle bit for bit (tile lists,
+    images, last contributors), with host and with device counts."""
+    from tdgs_amd import synthetic
+    n = 50_000
+    w = synthetic.config(0, n=n)
+    cam = w.cameras[0]
+    g_host = w.gaussians
+    sampled = np.zeros(n, bool)
+    sampled[(np.arange(4096, dtype=np.int64) * n) // 4096] = True
+    rng = np.random.default_rng(11)
+    mo = g_host.means_opacity
+    fwd = cam.R_c2w[:, 2].astype(np.float64)
+    pos = np.asarray(cam.t_c2w, np.float64)
+    # every Gaussian inside the view (all kept: filtered index = index): the sampled ones at
+    # depths 2-4.8 or 5.2-8, the others in the band 5 .. 5 + 5e-5
+    d = np.where(sampled, np.where(rng.random(n) < 0.5, rng.uniform(2.0, 4.8, n), rng.uniform(5.2, 8.0, n)),
+                 5.0 + rng.uniform(0, 5e-5, n))
+    mo[:, :3] = (pos + d[:, None] * fwd + rng.uniform(-0.5, 0.5, (n, 1)) * cam.R_c2w[:, 0]
+                 + rng.uniform(-0.5, 0.5, (n, 1)) * cam.R_c2w[:, 1]).astype(np.float32)
+    mo[:, 3] = np.abs(mo[:, 3])   # opacities >= 1/2: none culled for its alpha
+    opts = host.RenderOptions.for_camera(cam, 0)
+    t = host.Tiling.for_camera(cam, 16, 16)
+    r = oracle.render(g_host, cam, t, opts)
+    nf = r["nb_fgaussians"]
+    assert nf == n
+    keys = r["depths"][:nf].view(np.uint32)[r["counts"][:nf] > 0]
+    lo, hi = np.float32(5.0).view(np.uint32), np.float32(5.00006).view(np.uint32)
+    in_band = (keys >= lo) & (keys <= hi)
+    assert in_band.sum() > 2 * 8192 + 100, in_band.sum()
+    samp_keys = r["depths"][:nf][sampled].view(np.uint32)
+    assert not bool(((samp_keys >= lo) & (samp_keys <= hi)).any())
+    g = gpu.TrainableGaussiansVector.from_host(g_host, 0)
+    for device_counts in (False, True):
+        buf = gpu.RenderBuffers(len(g), t, 0, r["nb_keys"] + 1024, keep_flags=True)
+        out = gpu.RenderOutputs.for_camera(cam, 0, include_depth=True)
+        gpu.render_(out, g, cam, t, opts, buf, device_counts=device_counts)
+        torch.cuda.synchronize()
+        if device_counts:
+            assert buf.frame_counts()[3] == abi.TDGS_FRAME_OK
+        _assert_forward_equal(r, out, buf)

@@ -34,6 +34,7 @@
 // (tdgs_render_sorted_keys).
 #include <mutex>
 
+#include "dsort.hpp"
 #include "internal.hpp"
 #include "scan.hpp"
 #include "sort.hpp"
@@ -126,6 +127,7 @@ struct ProjectArgs {
     int32_t* counts;
     uint32_t* depth_keys;     // depth bits by fgidx (0xffffffff when empty); culled: slots past N_f
     int32_t* depth_vals;      // fgidx (1-based); 0 for the slots past N_f
+    uint32_t* depth_sample;   // or null: the depth presort's sample of the depth keys (ds_sample_store)
 };
 
 // Tile ranges from tile rectangles (used when Gaussians cover many tiles, where reading the
@@ -327,11 +329,13 @@ __global__ __launch_bounds__(kProjThreads) void k_project(ProjectArgs a) {
         if (a.depth_keys) {
             a.depth_keys[f] = dk;
             a.depth_vals[f] = (int32_t)(f + 1);
+            if (a.depth_sample) ds_sample_store(a.depth_sample, n, f, dk);
         }
     } else if (gi < n && a.depth_keys) {
         const int64_t slot = nbf + (gi - f);   // culled Gaussians fill the slots past N_f
         a.depth_keys[slot] = 0xffffffffu;
         a.depth_vals[slot] = 0;
+        if (a.depth_sample) ds_sample_store(a.depth_sample, n, slot, 0xffffffffu);
     }
     // the block's records are one contiguous run of f2d: write it with consecutive lanes on
     // consecutive floats (36-byte strided stores from each thread split into many partial
@@ -1800,6 +1804,14 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(t ? ((int64_t)t->nb_tiles_x * t->nb_tiles_y + 3) / 4 * 4 : 0);   // tiles' totals
     ar.template take<int4>(cap);                                                  // rectangles in depth order
     ar.template take<uint32_t>(zero_words(cap, key_cap));                         // zeroed each frame
+    ar.template take<uint64_t>(kDsBuckets);                                       // presort: splitters
+    ar.template take<uint32_t>(kDsBuckets + 1);                                   // bucket starts
+    ar.template take<uint32_t>(kDsSample);                                        // sampled keys
+    ar.template take<uint8_t>(cap);                                               // bucket ids
+    ar.template take<uint64_t>(cap);                                              // bucket pass output
+    ar.template take<int32_t>(cap);
+    ar.template take<uint64_t>(cap);                                              // and its ping-pong partner
+    ar.template take<int32_t>(cap);
 }
 
 // The scratch arrays of tdgs_render / tdgs_project inside buf->temp (render_layout's order).
@@ -1827,6 +1839,7 @@ struct RenderScratch {
     uint32_t* egrp;   // emission pass group sums (negrp words; 0: not grouped)
     int64_t negrp;
     int64_t* scan_sums;   // count scan tile sums (kScanTile items each)
+    DsScratch ds;         // the bucketed depth presort
 };
 
 static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const tdgs_tiling* tiling) {
@@ -1865,6 +1878,14 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.egrp = r.dgrp + r.ndgrp;
     r.negrp = emit_group_words(buf->key_capacity);
     r.scan_sums = reinterpret_cast<int64_t*>(r.egrp + r.negrp);
+    r.ds.spl = ar.take<uint64_t>(kDsBuckets);
+    r.ds.bstart = ar.take<uint32_t>(kDsBuckets + 1);
+    r.ds.sample = ar.take<uint32_t>(kDsSample);
+    r.ds.bid = ar.take<uint8_t>(cap);
+    r.ds.bkey = ar.take<uint64_t>(cap);
+    r.ds.bval = ar.take<int32_t>(cap);
+    r.ds.akey = ar.take<uint64_t>(cap);
+    r.ds.aval = ar.take<int32_t>(cap);
     return r;
 }
 
@@ -1912,6 +1933,7 @@ static int launch_keep_and_project(hipStream_t s, const tdgs_gaussians* g, const
     pa.fgidx_to_gidx = buf->fgidx_to_gidx; pa.depths = buf->depths; pa.f2d = buf->f2d;
     pa.ranges = buf->tile_ranges; pa.counts = buf->counts;
     pa.depth_keys = depth_keys; pa.depth_vals = depth_vals;
+    pa.depth_sample = depth_keys && ds_applicable(n, r.ndgrp) ? r.ds.sample : nullptr;
     StageScope sc(TDGS_STAGE_PROJECT, s);
     if (g->kind == TDGS_TRAINABLE)
         k_project<TDGS_TRAINABLE><<<(unsigned)nblocks, kProjThreads, 0, s>>>(pa);
@@ -2264,18 +2286,23 @@ int tdgs_render(tdgs_ctx* ctx, void* stream, const tdgs_gaussians* g, const tdgs
     // 1-3: keep counts, compaction + projection
     TDGS_TRY(launch_keep_and_project(s, g, cam, tiling, opt, buf, r, d_nbf, dkey, dval));
     // 4: the N_b non-empty Gaussians by (depth bits, fgidx); empty and culled ones (all-ones
-    // depth key) are dropped by the first pass, the later passes sort N_b pairs
+    // depth key) are dropped. By sampled buckets (dsort.hpp), else (more slots than its grouped
+    // tables take) by a 4-pass LSD radix sort whose first pass drops them.
     int64_t* d_nb = ctx->d_counters + 4;
     {
         StageScope sc(TDGS_STAGE_DEPTH_SORT, s);
-        // (the last pass gathers the rectangles into depth order and, for the tile lists, sums
+        // (the output gathers the rectangles into depth order and, for the tile lists, sums
         // their packed tile and block counts per scan tile)
         const BinGeom bg = tile16 ? bin_geom(tiling) : BinGeom{};
-        TDGS_TRY(radix_sort_pairs_grouped<uint32_t>(
-            dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32, rtemp, rbytes, r.dgrp, r.ndgrp, s, d_err,
-            d_nb, nullptr,
-            RsGather{reinterpret_cast<const int4*>(buf->tile_ranges), r.srect, tile16 ? r.scan_sums : nullptr,
-                     bg.sx, bg.sy}));
+        const RsGather gather{reinterpret_cast<const int4*>(buf->tile_ranges), r.srect,
+                              tile16 ? r.scan_sums : nullptr, bg.sx, bg.sy};
+        if (ds_applicable(n, r.ndgrp))
+            TDGS_TRY(depth_sort_buckets(dkey, n, r.ds, radix_count_table(rtemp), r.dgrp, sorted_f, gather, d_err, d_nb,
+                                        s));
+        else
+            TDGS_TRY(radix_sort_pairs_grouped<uint32_t>(dkey, dkey_sorted, dval, sorted_f, dkey_alt, dval_alt, n, 0, 32,
+                                                        rtemp, rbytes, r.dgrp, r.ndgrp, s, d_err, d_nb, nullptr,
+                                                        gather));
     }
     if (tile16) {
         // 5: tiles and blocks touched, in depth order -> the blocks' entries (emission offsets)

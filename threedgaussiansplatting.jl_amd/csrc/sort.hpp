@@ -241,14 +241,16 @@ __device__ __forceinline__ void wave_run_add(int64_t key, int64_t v, int64_t* ds
 
 // off_t and total_t (read by the digit owners, threads t < kRsBins): the tile's offset inside
 // digit t's output (digit t's keys in earlier tiles) and digit t's total. With V2 a second
-// 32-bit payload (val2, one per key) is moved along to vout2.
+// 32-bit payload (val2, one per key) is moved along to vout2. bin_out (may be null): tile 0
+// writes each digit's start in the output there, and the keys sorted in all at kRsBins.
 template <class K, bool V2 = false>
 __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems], const int32_t (&val)[RsTile<K>::kItems],
                                                 const bool (&valid)[RsTile<K>::kItems], int64_t tile, int64_t n,
                                                 int shift, int nbits, uint32_t off_t, uint32_t total_t,
                                                 K* __restrict__ kout, int32_t* __restrict__ vout, uint32_t* err,
                                                 int64_t* d_kept, uint32_t* s_raw, RsGather gather = {},
-                                                const uint32_t* val2 = nullptr, uint32_t* __restrict__ vout2 = nullptr) {
+                                                const uint32_t* val2 = nullptr, uint32_t* __restrict__ vout2 = nullptr,
+                                                uint32_t* bin_out = nullptr) {
     constexpr int kRsItems = RsTile<K>::kItems;
     constexpr int kRsTile = RsTile<K>::kTile;
     // Keys narrower than 32 bits are staged as 32-bit words: lanes storing 16-bit keys to
@@ -299,6 +301,11 @@ __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems
         if (t == kRsBins - 1) {
             s_tile_n = local + tot;
             if (d_kept && tile == 0) *d_kept = (int64_t)bin + total_t;   // keys sorted in all
+        }
+        // the digits' starts in the output (and, at kRsBins, the keys sorted in all)
+        if (bin_out && tile == 0) {
+            bin_out[t] = bin;
+            if (t == kRsBins - 1) bin_out[kRsBins] = bin + total_t;
         }
     }
     __syncthreads();
