@@ -955,18 +955,22 @@ struct WriteBlockScan {
 // Work is dealt in chunks of the coarse list, not per block, so that every workgroup gets the
 // same number of entries however unevenly the Gaussians spread over the blocks: chunk k is
 // entries [k E, (k + 1) E) of the lists of all blocks one after the other (E = the
-// workgroup's threads x kBinPer). A chunk that straddles block boundaries is processed as one
+// workgroup's threads x bin_per). A chunk that straddles block boundaries is processed as one
 // segment per block; segment (k, b) has the unique index k + b (both grow along the list), and
 // its per-tile counts are table[(k + b) tpb + local tile] (tpb = tiles per block).
-constexpr int kBinPer = 2;   // candidates each thread stages per chunk (their loads in flight together)
+// Candidates each thread stages per chunk (their loads in flight together): 4 for blocks 16
+// tiles wide, where the write pass runs one tile at a time and longer runs per segment pay
+// (3840 x 2160, 3M Gaussians: 0.97 -> 0.91 ms for the lists), 2 for blocks 8 wide (1920 x 1080,
+// 1M Gaussians: 4 measured 45 -> 55 us).
+constexpr int bin_per(int sx) { return sx >= 4 ? 4 : 2; }
 constexpr int kBinMaxGrid = 2048;   // workgroups of a launch (a grid-stride loop covers the rest)
 
 // Entries of the segment count table for key capacity kc (the coarse entries never exceed
 // the keys: each Gaussian touches at least one tile of every block it is listed in): at most
-// 4 / (4 kBinPer) bytes per key. (Chunks of 2 entries per thread measured 70 -> 66 us for the
+// 4 / (4 bin_per) bytes per key. (Chunks of 2 entries per thread measured 70 -> 66 us for the
 // tile lists at 1M Gaussians, 1080p; 1 per thread 63 us, but twice the table.)
-inline int64_t bin_table_entries(int64_t kc, int32_t nblocks, int tpb) {
-    return (ceil_div(kc > 0 ? kc : 1, (int64_t)tpb * 4 * kBinPer) + nblocks + 1) * tpb;
+inline int64_t bin_table_entries(int64_t kc, const BinGeom& g) {
+    return (ceil_div(kc > 0 ? kc : 1, (int64_t)g.tpb() * 4 * bin_per(g.sx)) + g.nblocks() + 1) * g.tpb();
 }
 
 struct BinArgs {
@@ -988,24 +992,25 @@ struct BinArgs {
 
 // Workgroup: 4 threads per tile of a block of 2^SX x 2^sy tiles; wavefront w takes the
 // block's tiles 16 w .. 16 w + 15 (row-major, 2^SX per row). A segment's Gaussians go
-// through LDS, kBinPer per thread, as the tile rectangle clipped to the block in two bit
+// through LDS, bin_per(SX) per thread, as the tile rectangle clipped to the block in two bit
 // masks (columns, rows); a wavefront then tests 64 of them at a time against each of its
 // tiles with one ballot. COUNT counts the hits of each (segment, tile); WRITE writes each
 // hit at the tile's list start + the earlier segments' hits + the hits before it.
 // (Staging the writes in LDS rings and storing 64 entries at a time measured no faster.)
-// LDS (dynamic): the chunk's candidates, 2 kBinPer words per thread.
+// LDS (dynamic): the chunk's candidates, 2 bin_per(SX) words per thread.
 template <int SX, bool WRITE>
 __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
     extern __shared__ uint32_t s_dyn[];
     __shared__ int32_t s_cend[1024];   // the blocks' ends, when there are at most 1024 blocks
     __shared__ int32_t s_b[2];
-    int32_t* const s_f = reinterpret_cast<int32_t*>(s_dyn);
-    uint32_t* const s_m = s_dyn + blockDim.x * kBinPer;
+    constexpr int PER = bin_per(SX);
+    int32_t* const s_f = reinterpret_cast<int32_t*>(s_dyn);   // the candidates' fgidx
+    uint32_t* const s_m = s_dyn + blockDim.x * PER;           // and tile masks
     constexpr int BW = 1 << SX;
     const int BH = 1 << a.sy;
     const int tpb = BW * BH;
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
-    const int nt = (int)blockDim.x * kBinPer;   // entries per chunk
+    const int nt = (int)blockDim.x * PER;   // entries per chunk
     int64_t mc = a.mc;
     if (a.dmc && *a.dmc < mc) mc = *a.dmc;
     const int64_t nchunks = (mc + nt - 1) / nt;
@@ -1070,6 +1075,7 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
             int32_t* const row = a.table + (k + b) * (int64_t)tpb;
             int32_t cnt[16];   // COUNT: hits so far; WRITE: the next output index
             int32_t start = 0;
+            int32_t seg_hits = 0;   // WRITE, lane i < 16: this segment's hits of tile i (COUNT's row)
             if (WRITE) {
                 // tile i (i < 16) of the wavefront: its list start plus the block's earlier
                 // segments' hits, summed by lanes i, i + 16, i + 32, i + 48 over every fourth
@@ -1078,6 +1084,7 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
                 const int xs = x0b + (tl & (BW - 1)), ys = y0b + (tl >> SX);
                 if (xs < a.ntx && ys < a.nty) {
                     const int tile = xs + ys * a.ntx;
+                    if (part == 0) seg_hits = row[tl];
                     if (part == 0 && tile > 0) start = a.tiles_end[tile - 1];
 #pragma unroll 4
                     for (int64_t k2 = bb / nt + part; k2 < k; k2 += 4) start += a.table[(k2 + b) * (int64_t)tpb + tl];
@@ -1085,31 +1092,29 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
                 start += __shfl_xor(start, 16);
                 start += __shfl_xor(start, 32);
             }
-#pragma unroll
-            for (int i = 0; i < 16; ++i) cnt[i] = WRITE ? __builtin_amdgcn_readlane(start, i) : 0;
-            // candidates cb + t + blockDim q (q < kBinPer): the loads issue together. Their
+            // candidates cb + t + blockDim q (q < PER): the loads issue together. Their
             // masks come sorted along with them (cmask), else from the rectangles.
-            int32_t f[kBinPer];
-            uint32_t mk[kBinPer];
+            int32_t f[PER];
+            uint32_t mk[PER];
             if (a.cmask) {
 #pragma unroll
-                for (int q = 0; q < kBinPer; ++q) {
+                for (int q = 0; q < PER; ++q) {
                     const int64_t e = cb + t + (int64_t)blockDim.x * q;
                     f[q] = WRITE && e < ce ? a.cvals[e] : 0;
                     mk[q] = e < ce ? a.cmask[e] : 0u;
                 }
             } else {
 #pragma unroll
-                for (int q = 0; q < kBinPer; ++q) {
+                for (int q = 0; q < PER; ++q) {
                     const int64_t e = cb + t + (int64_t)blockDim.x * q;
                     f[q] = e < ce ? a.cvals[e] : 0;
                 }
-                int4 r[kBinPer];
+                int4 r[PER];
 #pragma unroll
-                for (int q = 0; q < kBinPer; ++q)
+                for (int q = 0; q < PER; ++q)
                     r[q] = f[q] > 0 ? reinterpret_cast<const int4*>(a.ranges)[f[q] - 1] : make_int4(1, 1, 0, 0);
 #pragma unroll
-                for (int q = 0; q < kBinPer; ++q) {
+                for (int q = 0; q < PER; ++q) {
                     // columns in bits 0-15, rows in bits 16-31 (of the block); none for an empty slot
                     const int cx0 = max(r[q].x - 1 - x0b, 0), cx1 = min(r[q].z - 1 - x0b, BW - 1);
                     const int cy0 = max(r[q].y - 1 - y0b, 0), cy1 = min(r[q].w - 1 - y0b, BH - 1);
@@ -1119,12 +1124,61 @@ __global__ __launch_bounds__(1024) void k_bin_tiles(BinArgs a) {
                 }
             }
 #pragma unroll
-            for (int q = 0; q < kBinPer; ++q) {
+            for (int q = 0; q < PER; ++q) {
                 s_f[t + blockDim.x * q] = f[q];
                 s_m[t + blockDim.x * q] = mk[q];
             }
             __syncthreads();
-            const int nk = (int)(ce - cb);
+            const int nk = __builtin_amdgcn_readfirstlane((int)(ce - cb));
+            int32_t wave_hits = seg_hits;
+            if (WRITE) {
+                for (int d = 16; d >= 1; d >>= 1) wave_hits += __shfl_xor(wave_hits, d);
+                wave_hits = __builtin_amdgcn_readfirstlane(wave_hits);
+            }
+            // WRITE with long runs (per tile and segment, on average 16 or more hits per 64
+            // candidates and 256 or more in all): one tile at a time, so that the wavefront's
+            // stores to a tile's list follow each other (one contiguous run of the list per
+            // segment) instead of interleaving sixteen lists; the segment's hits of each tile
+            // (counted by k_bin_tiles<COUNT>) skip the tiles without any and end a tile's walk
+            // at its last hit. Shorter runs take the candidate-major loop below (one LDS read
+            // per 64 candidates for all 16 tiles). (At 3840 x 2160, 3M Gaussians, runs average
+            // ~1100 entries: lists 1.31 -> 0.92 ms; at 1920 x 1080, 1M Gaussians, ~70, and the
+            // tile-major walk from 16 hits per 64 candidates alone measured 45 -> 49 us.)
+            if (WRITE && wave_hits >= 4 * nk && wave_hits >= 16 * 256) {
+                const int row0 = 16 + __builtin_amdgcn_readfirstlane(ly0);
+#pragma unroll 1
+                for (int i = 0; i < 16; ++i) {
+                    const int32_t nh = __builtin_amdgcn_readlane(seg_hits, i);
+                    if (nh <= 0) continue;
+                    const uint32_t need = (1u << (i & (BW - 1))) | (1u << (row0 + (i >> SX)));
+                    int32_t c = __builtin_amdgcn_readlane(start, i);
+                    const int32_t c_end = c + nh;
+                    // (entries past nk are zero: no hits)
+                    int32_t nf = s_f[lane];
+                    uint32_t nm = s_m[lane];
+                    for (int j0 = 0; j0 < nk && c < c_end; j0 += kWave) {
+                        const int32_t fv = nf;
+                        const uint32_t p = nm;
+                        if (j0 + kWave < nk) {   // read ahead, both words
+                            nf = s_f[j0 + kWave + lane];
+                            nm = s_m[j0 + kWave + lane];
+                        }
+                        asm volatile("" ::"v"(fv));   // not sunk into the branch below
+                        const bool hit = (p & need) == need;
+                        const uint64_t bal = __ballot(hit);
+                        if (hit) {
+                            const int32_t o = (int32_t)__builtin_amdgcn_mbcnt_hi(
+                                (uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, (uint32_t)c));
+                            a.out[o < a.cap ? o : a.cap - 1] = fv;
+                        }
+                        c += __popcll(bal);
+                    }
+                }
+                __syncthreads();   // s_f, s_m are free again
+                continue;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) cnt[i] = WRITE ? __builtin_amdgcn_readlane(start, i) : 0;
             for (int j0 = 0; j0 < nk; j0 += kWave) {
                 const uint32_t p = s_m[j0 + lane];   // (entries past nk are zero: no hits)
                 // the wavefront's 16 tiles as bits: 8 x 2 (SX = 3) or 16 x 1 (SX = 4)
@@ -1799,7 +1853,7 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<char>((int64_t)radix_temp_bytes(big));
     ar.template take<int32_t>(kRectCopies * rect_diff_size(t));   // tile-coverage difference arrays
     ar.template take<int32_t>(ceil_div(key_cap, kEmitTile) + 2);  // first Gaussian of each emission block
-    ar.template take<int32_t>(t ? bin_table_entries(key_cap, bin_geom(t).nblocks(), bin_geom(t).tpb()) : 0);   // per (segment, tile)
+    ar.template take<int32_t>(t ? bin_table_entries(key_cap, bin_geom(t)) : 0);   // per (segment, tile)
     ar.template take<int32_t>(t ? bin_geom(t).nblocks() : 0);                    // ends of the blocks' lists
     ar.template take<int32_t>(t ? ((int64_t)t->nb_tiles_x * t->nb_tiles_y + 3) / 4 * 4 : 0);   // tiles' totals
     ar.template take<int4>(cap);                                                  // rectangles in depth order
@@ -1866,7 +1920,7 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.nblk = ceil_div(buf->key_capacity, kEmitTile) + 2;
     r.blk_first = ar.take<int32_t>(r.nblk);
     r.tile_counts = ar.take<int32_t>(
-        tiling ? bin_table_entries(buf->key_capacity, bin_geom(tiling).nblocks(), bin_geom(tiling).tpb()) : 0);
+        tiling ? bin_table_entries(buf->key_capacity, bin_geom(tiling)) : 0);
     r.block_end = ar.take<int32_t>(tiling ? bin_geom(tiling).nblocks() : 0);
     r.ntt = tiling ? ((int64_t)tiling->nb_tiles_x * tiling->nb_tiles_y + 3) / 4 * 4 : 0;
     r.tile_totals = ar.take<int32_t>(r.ntt);
@@ -2045,9 +2099,10 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
     ba.tiles_end = buf->tiles_end;
     ba.out = buf->sorted_values; ba.cap = (int32_t)(kc < INT32_MAX ? kc : INT32_MAX); ba.err = d_err;
     const unsigned bthreads = 4u << (bg.sx + bg.sy);
-    const int64_t nchunks = ceil_div(mb > 0 ? mb : 1, (int64_t)bthreads * kBinPer);
+    const int per = bin_per(bg.sx);
+    const int64_t nchunks = ceil_div(mb > 0 ? mb : 1, (int64_t)bthreads * per);
     const unsigned bgrid = (unsigned)(nchunks < kBinMaxGrid ? nchunks : kBinMaxGrid);
-    const size_t lds = (size_t)bthreads * kBinPer * 2 * sizeof(uint32_t);
+    const size_t lds = (size_t)bthreads * per * 2 * sizeof(uint32_t);
     if (bg.sx == 3) k_bin_tiles<3, false><<<bgrid, bthreads, lds, s>>>(ba);
     else k_bin_tiles<4, false><<<bgrid, bthreads, lds, s>>>(ba);
     TDGS_LAUNCHED();
