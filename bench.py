@@ -35,6 +35,8 @@ __graft_entry__.load_package()
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3       # MI355X vector FP32 (published)
+# Gaussians up to which the depth presort is the bucket sort (kDsMaxSlots in csrc/dsort.hpp)
+DS_MAX_SLOTS = 1_400_000
 
 # FLOP of blending under the metric's accounting: 20 per (pixel, sorted entry) evaluation made
 # before the pixel's early exit (E_f) plus one exponential per evaluation; backward blending
@@ -70,6 +72,9 @@ def parse():
                    help="only run 10 device-to-device copies of 1 GiB (HBM counter calibration)")
     p.add_argument("--only", choices=["stress_cfg4", "sort_pairs", "train_cfg3", "train_cfg3_growth"],
                    help="only run one of the extra legs and print its JSON (kernel profiles of that leg)")
+    p.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"),
+                   help="print the HBM traffic summary (profiles/hbm_traffic.json) from the rocpd databases "
+                        "of rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this script and of --copy-calibration")
     return p.parse_args()
 
 
@@ -83,6 +88,70 @@ def copy_calibration():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_each": 1 << 30, "copies": 10}))
+
+
+# rocprofv3 kernel names -> the counter summary's keys (the first match wins; the blend is the
+# timed render's variant, without last-contributor output)
+TRAFFIC_KERNELS = [
+    ("k_render_tiles<true, false, false, false>", "blend"),
+    ("k_backward_blend<", "backward_blend"),
+    ("k_project<", "project"),
+    ("k_keep_counts", "keep_counts"),
+    ("k_adam(", "adam"),
+    ("k_emit_count<", "emit_count"),
+    ("k_emit_scatter<", "coarse_sort_scatter"),
+    ("k_backward_project<false>", "backward_project"),
+    ("k_backward_project<true>", "backward_project_adam"),
+    ("k_rs_scatter_grouped<unsigned int>", "depth_sort_scatter"),
+    ("k_rs_count_grouped<unsigned int>", "depth_sort_count"),
+    ("k_ds_splitters", "depth_sort_splitters"),
+    ("k_ds_count", "depth_sort_bucket_count"),
+    ("k_ds_scatter", "depth_sort_bucket_scatter"),
+    ("k_ds_buckets", "depth_sort_buckets"),
+    ("k_ssim_forward", "loss_ssim_forward"),
+    ("k_ssim_backward", "loss_ssim_backward"),
+    ("k_bin_tiles<3, false>", "bin_count"),
+    ("k_bin_tiles<3, true>", "bin_write"),
+    ("k_bin_tiles<4, false>", "bin_count_16x"),
+    ("k_bin_tiles<4, true>", "bin_write_16x"),
+    ("k_bin_scan", "bin_scan"),
+    ("k_scan_apply<tdgs::SortedTileBlockCounts", "count_scan_apply"),
+]
+
+
+def _pmc_means(db, counter):
+    """Mean value per dispatch of one counter, by kernel name, from a rocpd database."""
+    import sqlite3
+    con = sqlite3.connect(db)
+    per = {}
+    for name, value, did in con.execute(
+            "select name, counter_value, dispatch_id from pmc_events where counter_name = ?", (counter,)):
+        d = per.setdefault(name, {})
+        d[did] = d.get(did, 0.0) + value   # (summed over the counter's instances)
+    con.close()
+    return {k: (sum(v.values()) / len(v), len(v)) for k, v in per.items()}
+
+
+def traffic_summary(fetch_db, write_db, cfetch_db, cwrite_db):
+    """HBM bytes per launch of each kernel: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) scaled
+    by what they read for one device-to-device copy of 1 GiB (--copy-calibration)."""
+    fetch, write = _pmc_means(fetch_db, "FETCH_SIZE"), _pmc_means(write_db, "WRITE_SIZE")
+
+    def calib(db, counter):
+        m = {k: v for k, v in _pmc_means(db, counter).items() if "copy" in k.lower()}
+        name = max(m, key=lambda k: m[k][1])   # the copy run ten times
+        return (1 << 30) / (m[name][0] * 1024.0)
+
+    ff, wf = calib(cfetch_db, "FETCH_SIZE"), calib(cwrite_db, "WRITE_SIZE")
+    kernels = {}
+    for name in sorted(set(fetch) | set(write)):
+        key = next((k for pat, k in TRAFFIC_KERNELS if pat in name), None)
+        if key is None or key in kernels or name not in fetch or name not in write:
+            continue
+        fb, wb = fetch[name][0] * 1024.0 * ff, write[name][0] * 1024.0 * wf
+        kernels[key] = {"kernel": name, "dispatches": fetch[name][1], "fetch_bytes": int(fb),
+                        "write_bytes": int(wb), "bytes_per_launch": int(fb + wb)}
+    return {"calibration": {"fetch_factor": ff, "write_factor": wf}, "kernels": kernels}
 
 
 def hbm_practical():
@@ -531,6 +600,11 @@ def algorithmic_bytes(stage, n, nf, nb, m, npx, h, ntiles, mc=0):
         # fgidx, counts, record (36), depth key + value of the kept; depth and rectangle of the
         # non-empty; depth key + value slots of the culled
         return 44 * n + 12 * h * nb + (4 + 4 + 36 + 8) * nf + 20 * nb + 8 * (n - nf)
+    if stage == "depth_sort" and n <= DS_MAX_SLOTS:   # the bucket presort: bucket ids counted
+        # (4 per key in, 1 per slot out), the kept scattered to their buckets (4 + 1 in, 12 out
+        # per kept: 64-bit key, 32-bit fgidx), each bucket sorted (12 in, the 4-byte fgidx out)
+        # and the rectangles gathered into depth order (16 in + 16 out)
+        return 5 * n + 5 * n + 12 * nb + 12 * nb + 4 * nb + 32 * nb
     if stage == "depth_sort":            # first pass over all N depth keys (count + scatter of the
         # kept), three more over the N_b non-empty ones: count 4, scatter 8 in + 8 out; the last
         # pass gathers each rectangle into depth order (16 in + 16 out; it also sums the count
@@ -564,13 +638,17 @@ def measured_traffic():
 
 
 # the counter-summary kernels of each survey row with their launches per frame (or step): the
-# row's bytes are the sum of per-launch bytes times launches (the depth presort runs its count
-# and scatter kernels once per 8-bit pass, four passes over the 32-bit depth keys)
+# row's bytes are the sum of per-launch bytes times launches (up to DS_MAX_SLOTS Gaussians the
+# depth presort is the bucket sort, four launches; above, the radix passes run their count and
+# scatter kernels once per 8-bit pass, four passes over the 32-bit depth keys)
 MEASURED_KERNELS = {
     "K1_project": [("keep_counts", 1), ("project", 1)],
     "K2_scan_keys": [("count_scan_apply", 1), ("emit_count", 1)],
-    "K3_K4_sort_ranges": [("depth_sort_count", 4), ("depth_sort_scatter", 4), ("coarse_sort_scatter", 1),
+    "K3_K4_sort_ranges": [("depth_sort_splitters", 1), ("depth_sort_bucket_count", 1),
+                          ("depth_sort_bucket_scatter", 1), ("depth_sort_buckets", 1), ("coarse_sort_scatter", 1),
                           ("bin_count", 1), ("bin_scan", 1), ("bin_write", 1)],
+    "K3_K4_sort_ranges_radix": [("depth_sort_count", 4), ("depth_sort_scatter", 4), ("coarse_sort_scatter", 1),
+                                ("bin_count", 1), ("bin_scan", 1), ("bin_write", 1)],
     "K5_blend": [("blend", 1)],
     "K6_backward_blend": [("backward_blend", 1)],
     "K7_backward_project": [("backward_project", 1)],
@@ -624,7 +702,7 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit,
         if all(v is not None for v in ib) and src is stage_ms:
             row["impl_bytes"] = int(sum(ib))
             row["impl_hbm_frac"] = round(sum(ib) / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-        mk = MEASURED_KERNELS.get(k)
+        mk = MEASURED_KERNELS.get(k + "_radix" if k == "K3_K4_sort_ranges" and n > DS_MAX_SLOTS else k)
         if mk and all(measured.get(x) for x, _ in mk):
             mb = sum(measured[x] * c for x, c in mk)
             row["measured_bytes"] = int(mb)
@@ -670,6 +748,9 @@ def main():
     args = parse()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.traffic_summary:
+        print(json.dumps(traffic_summary(*args.traffic_summary), indent=1))
         return
     if args.only:
         import torch

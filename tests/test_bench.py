@@ -42,3 +42,37 @@ def test_measured_rows_have_profile_lines():
             assert name in kernels, (row, name)
             assert kernels[name]["bytes_per_launch"] > 0 and launches >= 1
     assert bench.traffic_from_profiles("blend") == kernels["blend"]["bytes_per_launch"]
+
+
+def test_traffic_summary_scales_by_the_copy(tmp_path):
+    """--traffic-summary: per-kernel means of FETCH_SIZE / WRITE_SIZE (KiB per dispatch, summed
+    over a dispatch's instances) times 1 GiB over the 1 GiB copy's counter value."""
+    import sqlite3
+
+    def db(name, rows):
+        p = str(tmp_path / name)
+        con = sqlite3.connect(p)
+        con.execute("create table pmc_events (name text, counter_name text, counter_value real, dispatch_id int)")
+        con.executemany("insert into pmc_events values (?, ?, ?, ?)", rows)
+        con.commit()
+        con.close()
+        return p
+
+    blend = "void tdgs::k_render_tiles<true, false, false, false>(tdgs::BlendArgs)"
+    other = "some_library_kernel"
+    # two dispatches of the blend, the second counted by two instances
+    fetch = db("f.db", [(blend, "FETCH_SIZE", 100.0, 1), (blend, "FETCH_SIZE", 150.0, 2),
+                        (blend, "FETCH_SIZE", 50.0, 2), (other, "FETCH_SIZE", 7.0, 3)])
+    write = db("w.db", [(blend, "WRITE_SIZE", 40.0, 1), (blend, "WRITE_SIZE", 60.0, 2)])
+    gib_kib = (1 << 30) / 1024.0
+    copy = "__amd_rocclr_copyBuffer"
+    cf = db("cf.db", [(copy, "FETCH_SIZE", gib_kib / 2, d) for d in range(10)] + [("fill", "FETCH_SIZE", 1.0, 11)])
+    cw = db("cw.db", [(copy, "WRITE_SIZE", gib_kib, d) for d in range(10)])
+    s = bench.traffic_summary(fetch, write, cf, cw)
+    assert s["calibration"] == {"fetch_factor": 2.0, "write_factor": 1.0}
+    k = s["kernels"]
+    assert set(k) == {"blend"}
+    assert k["blend"]["dispatches"] == 2
+    assert k["blend"]["fetch_bytes"] == int(150.0 * 1024 * 2.0)   # mean of 100 and 200 KiB, doubled
+    assert k["blend"]["write_bytes"] == int(50.0 * 1024)
+    assert k["blend"]["bytes_per_launch"] == k["blend"]["fetch_bytes"] + k["blend"]["write_bytes"]
