@@ -657,9 +657,29 @@ MEASURED_KERNELS = {
 }
 
 
-def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit, e_f, e_b, mc=0):
+def cold_stages(core, out, g, cams, tiling, opts, buf, frames):
+    """Stage times with the caches flushed before every frame: 1 GiB written (more than the
+    256 MB infinity cache and the 8 x 4 MB L2) between frames, outside the profiled stages."""
+    import torch
+    flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    L = core.lib()
+    core.check(L.tdgs_profile_begin(C.c_int32(16 * frames + 64)))
+    for k in range(frames):
+        flush.fill_(float(k))
+        core.render_(out, g, cams[k % len(cams)], tiling, opts, buf, device_counts=True)
+    torch.cuda.synchronize()
+    ms = (C.c_double * 13)()
+    cnt = (C.c_int64 * 13)()
+    core.check(L.tdgs_profile_end(ms, cnt))
+    del flush
+    torch.cuda.empty_cache()
+    return {STAGES[i]: ms[i] / cnt[i] for i in range(13) if cnt[i] > 0}
+
+
+def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit, e_f, e_b, mc=0, cold_ms=None):
     """Per-kernel roofline fractions. `bytes` follow the metric's accounting (K1 = cull,
-    compaction and projection: 16 N + (28 + 12h) N_f read, 8 N_f + 56 N_b written; K2 = count
+    compaction and projection: 16 N + (28 + 12h) N_f read, 8 N_f + 56 N_b written; K1_project_cold
+    = the same with the caches flushed before every frame (cold_ms, cold_stages); K2 = count
     scan and key emission: 8 N_f + 24 N_b + 12 M; K3 + K4 = the sort, priced as CUB's 8-bit-digit
     LSD sort of the 64-bit keys: 8 M + 24 M ceil(end_bit / 8), and the ranges: 8 M + 4 T, whose
     results this build obtains together from the depth presort and the coarse binning (stages
@@ -675,6 +695,9 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit,
     k7, k8 = (160 + 24 * h) * nf, 28 * g3 * nf + 4 * nf
     rows = {
         "K1_project": (16 * n + (28 + 12 * h) * nf + 8 * nf + 56 * nb, ["cull_compact", "project"], stage_ms, None),
+        # the same with the caches flushed before every frame (cold_stages)
+        "K1_project_cold": (16 * n + (28 + 12 * h) * nf + 8 * nf + 56 * nb, ["cull_compact", "project"],
+                            cold_ms or {}, None),
         "K2_scan_keys": (8 * nf + 24 * nb + 12 * m, ["count_scan", "emit"], stage_ms, None),
         "K3_K4_sort_ranges": (8 * m + 24 * m * math.ceil(end_bit / 8) + 8 * m + 4 * ntiles,
                               ["depth_sort", "tile_sort", "tile_ranges"], stage_ms, None),
@@ -699,10 +722,11 @@ def survey_kernels(stage_ms, train_stage, n, nf, nb, m, npx, h, ntiles, end_bit,
         row = {"stages": stages, "ms": round(t, 4), "bytes": int(b), "GBs": round(gbs, 1),
                "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
         ib = [impl.get(s_) for s_ in stages]
-        if all(v is not None for v in ib) and src is stage_ms:
+        if all(v is not None for v in ib) and (src is stage_ms or src is cold_ms):
             row["impl_bytes"] = int(sum(ib))
             row["impl_hbm_frac"] = round(sum(ib) / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-        mk = MEASURED_KERNELS.get(k + "_radix" if k == "K3_K4_sort_ranges" and n > DS_MAX_SLOTS else k)
+        mk = MEASURED_KERNELS.get({"K3_K4_sort_ranges": "K3_K4_sort_ranges_radix" if n > DS_MAX_SLOTS else k,
+                                   "K1_project_cold": "K1_project"}.get(k, k))
         if mk and all(measured.get(x) for x, _ in mk):
             mb = sum(measured[x] * c for x, c in mk)
             row["measured_bytes"] = int(mb)
@@ -831,6 +855,7 @@ def main():
     cnt = (C.c_int64 * 13)()
     core.check(L.tdgs_profile_end(ms, cnt))
     assert int(mon[2]) == overflows0, "a frame's keys did not fit the key arrays"
+    cold_stage_ms = cold_stages(core, out, g, cams, tiling, opts, buf, nextra)
 
     in_flight = None
     if not args.no_in_flight:
@@ -924,7 +949,9 @@ def main():
         "roofline": roofline,
         "hbm_practical_GBs": hbm_ref,
         "survey_kernels": survey_kernels(stage_ms, train["stage_ms"] if train else None, n, nf, nb, m, npx, h,
-                                         tiling.nb_tiles, tiling.end_bit(), evals, evals_back, mc),
+                                         tiling.nb_tiles, tiling.end_bit(), evals, evals_back, mc,
+                                         cold_ms=cold_stage_ms),
+        "stage_ms_cold_cache": {k: round(v, 4) for k, v in cold_stage_ms.items()},
         "cpu_baseline": cpu,
         "extra_configs": extra,
     }
