@@ -7,17 +7,17 @@
 // output index, the Gaussian's tile rectangle gathered alongside and the packed tile/block
 // counts summed per count-scan tile (RsGather).
 //
-// Four launches instead of the eight of a 4-pass LSD radix sort over the 32-bit keys, whose
+// Three launches instead of the eight of a 4-pass LSD radix sort over the 32-bit keys, whose
 // short, latency-bound passes cost ~8 us each whatever their work:
-//   k_ds_splitters  one workgroup histograms a sample of 4096 keys (strided over the slots,
-//                   written by the projection beside the keys)
-//                   in 4096 bins over its range and takes 255 splitters at bin edges near
+//   k_ds_count      every workgroup first takes 255 splitters from a sample of 4096 keys
+//                   (strided over the slots, written by the projection beside the keys):
+//                   histogrammed in 4096 bins over its range, splitters at bin edges near
 //                   equal ranks of its non-empty part, as composites (depth bits << 32 |
-//                   fgidx): every bucket then holds about 1/256 of the non-empty Gaussians,
-//                   however the depths are distributed
-//   k_ds_count      per 4096-key radix tile, each key's bucket id (a binary search in the
-//                   splitters, written as one byte per slot) and their histogram as a row of
-//                   the count table plus 16-tile group sums
+//                   fgidx), so that every bucket holds about 1/256 of the non-empty
+//                   Gaussians however the depths are distributed. Then, per 4096-key radix
+//                   tile, each key's bucket id (a binary search in the splitters, written as
+//                   one byte per slot) and their histogram as a row of the count table plus
+//                   16-tile group sums
 //   k_ds_scatter    the stable radix pass on the bucket id (grouped offsets, as
 //                   k_rs_scatter_grouped); tile 0 writes the buckets' starts
 //   k_ds_buckets    one workgroup per bucket sorts its Gaussians by depth bits: up to 8192
@@ -166,28 +166,29 @@ __device__ void ds_sort_regs(uint32_t (&k)[IT], int32_t (&v)[IT], int it, int n,
     }
 }
 
-// Splitters from the sample (one workgroup of kDsThreads): the non-empty keys among the
+// Splitters from the sample, by one workgroup of NTH threads: the non-empty keys among the
 // kDsSample sampled slots (ds_sample_store) are histogrammed in 4096 bins over their range
-// [kmin, kmax]; for
-// b < 255, spl[b] = (the lower edge of the bin holding the sample of rank (b + 1) ne / 256,
-// ne non-empty samples) << 32, a composite below every key of that bin and above every key of
-// the bins before it; spl[255] and, without a non-empty sample, every splitter are all ones.
-// (No sort: the splitters only balance the buckets, the order does not depend on them.)
+// [kmin, kmax]; for b < 255, spl[b] = (the lower edge of the bin holding the sample of rank
+// (b + 1) ne / 256, ne non-empty samples) << 32, a composite below every key of that bin and
+// above every key of the bins before it; spl[255] and, without a non-empty sample, every
+// splitter are all ones. (No sort: the splitters only balance the buckets, the order does not
+// depend on them.) spl, s_h (4096 words), s_mm (2) and s_w (NTH / 64) are LDS; the caller
+// waits at a barrier before reading spl.
 constexpr int kDsHistBits = 12;
-__global__ __launch_bounds__(kDsThreads) void k_ds_splitters(const uint32_t* __restrict__ sample, int64_t n,
-                                                             uint64_t* __restrict__ spl) {
+template <int NTH>
+__device__ __forceinline__ void ds_splitters(const uint32_t* __restrict__ sample, int64_t n, uint64_t* spl,
+                                             uint32_t* s_h, uint32_t* s_mm, uint32_t* s_w) {
     constexpr int kBins = 1 << kDsHistBits;
-    constexpr int kPer = kBins / kDsThreads;   // bins per thread
-    __shared__ uint32_t s_h[kBins];
-    __shared__ uint32_t s_mm[2];
-    __shared__ uint32_t s_w[kDsWaves];
+    constexpr int kPer = kBins / NTH;          // bins per thread
+    constexpr int kItems = kDsSample / NTH;    // sampled keys per thread
+    constexpr int kWaves = NTH / kWave;
     const int t = threadIdx.x, lane = __lane_id(), w = t / kWave;
     const int ns = (int)(n < kDsSample ? n : kDsSample);
-    uint32_t k[kDsSampleItems];
+    uint32_t k[kItems];
     uint32_t mn = 0xffffffffu, mx = 0u;
 #pragma unroll
-    for (int j = 0; j < kDsSampleItems; ++j) {
-        const int p = j * kDsThreads + t;
+    for (int j = 0; j < kItems; ++j) {
+        const int p = j * NTH + t;
         k[j] = 0xffffffffu;
         if (p < ns) k[j] = sample[p];
         if (k[j] != 0xffffffffu) {
@@ -196,7 +197,7 @@ __global__ __launch_bounds__(kDsThreads) void k_ds_splitters(const uint32_t* __r
         }
     }
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) s_h[q * kDsThreads + t] = 0;
+    for (int q = 0; q < kPer; ++q) s_h[q * NTH + t] = 0;
     if (t == 0) {
         s_mm[0] = 0xffffffffu;
         s_mm[1] = 0u;
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(kDsThreads) void k_ds_splitters(const uint32_t* __r
     }
     __syncthreads();
     const uint32_t kmin = s_mm[0], kmax = s_mm[1];
-    if (kmin > kmax) {   // no non-empty sample
+    if (kmin > kmax) {   // no non-empty sample (block-uniform)
         if (t < kDsBuckets) spl[t] = ~0ull;
         return;
     }
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(kDsThreads) void k_ds_splitters(const uint32_t* __r
     const int len = span ? 32 - __clz((int)span) : 0;
     const int shift = len > kDsHistBits ? len - kDsHistBits : 0;
 #pragma unroll
-    for (int j = 0; j < kDsSampleItems; ++j)
+    for (int j = 0; j < kItems; ++j)
         if (k[j] != 0xffffffffu) atomicAdd(&s_h[(k[j] - kmin) >> shift], 1u);
     __syncthreads();
     // thread t owns bins t kPer .. t kPer + kPer - 1: their exclusive prefix over all bins
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(kDsThreads) void k_ds_splitters(const uint32_t* __r
     __syncthreads();
     uint32_t before = incl - sum, ne = 0;
 #pragma unroll
-    for (int q = 0; q < kDsWaves; ++q) {
+    for (int q = 0; q < kWaves; ++q) {
         const uint32_t x = s_w[q];
         if (q < w) before += x;
         ne += x;
@@ -264,13 +265,17 @@ __global__ __launch_bounds__(kDsThreads) void k_ds_splitters(const uint32_t* __r
     if (t == 0) spl[kDsBuckets - 1] = ~0ull;
 }
 
-// Per 4096-key tile: each slot's bucket id in bid (0 for an empty key) and the histogram of the
-// non-empty keys' buckets, as row cnt[tile][.] and added into the group sums
+// Per 4096-key tile: the splitters (every workgroup computes them from the sample: cheaper
+// than a launch of their own), each slot's bucket id in bid (0 for an empty key) and the
+// histogram of the non-empty keys' buckets, as row cnt[tile][.] and added into the group sums
 // grp[tile / kRsGroup][.] (zero on entry).
 __global__ __launch_bounds__(kRsThreads) void k_ds_count(const uint32_t* __restrict__ keys, int64_t n,
-                                                         const uint64_t* __restrict__ spl, uint8_t* __restrict__ bid,
+                                                         const uint32_t* __restrict__ sample, uint8_t* __restrict__ bid,
                                                          uint32_t* __restrict__ cnt, uint32_t* __restrict__ grp) {
     __shared__ uint64_t s_spl[kDsBuckets];
+    __shared__ uint32_t s_hist[1 << kDsHistBits];
+    __shared__ uint32_t s_mm[2];
+    __shared__ uint32_t s_w[kRsThreads / kWave];
     __shared__ uint32_t s_h[kRsBins];
     const int t = threadIdx.x;
     constexpr int IT = DsTile::kItems;
@@ -281,10 +286,8 @@ __global__ __launch_bounds__(kRsThreads) void k_ds_count(const uint32_t* __restr
         const int64_t i = base + (int64_t)j * kRsThreads;
         key[j] = i < n ? keys[i] : 0xffffffffu;
     }
-    if (t < kDsBuckets) {
-        s_spl[t] = spl[t];
-        s_h[t] = 0;
-    }
+    if (t < kDsBuckets) s_h[t] = 0;
+    ds_splitters<kRsThreads>(sample, n, s_spl, s_hist, s_mm, s_w);
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < IT; ++j) {
@@ -526,7 +529,6 @@ __global__ __launch_bounds__(kDsThreads) void k_ds_buckets(uint64_t* bkey, int32
 // Scratch of the bucketed presort: splitters (256), bucket starts (257), the slots' bucket ids,
 // and the bucket pass's output and its ping-pong partner (slots each).
 struct DsScratch {
-    uint64_t* spl;
     uint32_t* bstart;
     uint32_t* sample;   // kDsSample sampled keys (written by the projection)
     uint8_t* bid;     // bucket id of every slot
@@ -553,9 +555,7 @@ inline bool ds_applicable(int64_t n, int64_t zgrp_words) {
 inline int depth_sort_buckets(const uint32_t* keys, int64_t n, const DsScratch& d, uint32_t* cnt, uint32_t* zgrp,
                               int32_t* sorted_f, RsGather g, uint32_t* err, int64_t* d_kept, hipStream_t s) {
     const int64_t tiles = ceil_div(n, DsTile::kTile);
-    k_ds_splitters<<<1, kDsThreads, 0, s>>>(d.sample, n, d.spl);
-    TDGS_LAUNCHED();
-    k_ds_count<<<(unsigned)tiles, kRsThreads, 0, s>>>(keys, n, d.spl, d.bid, cnt, zgrp);
+    k_ds_count<<<(unsigned)tiles, kRsThreads, 0, s>>>(keys, n, d.sample, d.bid, cnt, zgrp);
     TDGS_LAUNCHED();
     k_ds_scatter<<<(unsigned)tiles, kRsThreads, 0, s>>>(keys, n, d.bid, cnt, zgrp, d.bkey, d.bval, err, d_kept,
                                                          d.bstart);

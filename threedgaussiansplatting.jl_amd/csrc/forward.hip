@@ -1963,7 +1963,6 @@ static RenderScratch carve_render_scratch(const tdgs_render_buffers* buf, const 
     r.egrp = r.dgrp + r.ndgrp;
     r.negrp = emit_group_words(buf->key_capacity);
     r.scan_sums = reinterpret_cast<int64_t*>(r.egrp + r.negrp);
-    r.ds.spl = ar.take<uint64_t>(kDsBuckets);
     r.ds.bstart = ar.take<uint32_t>(kDsBuckets + 1);
     r.ds.sample = ar.take<uint32_t>(kDsSample);
     r.ds.bid = ar.take<uint8_t>(cap);
