@@ -55,6 +55,20 @@ struct SsimWindow {
     float w[2 * kSsimR + 1];
 };
 
+// The backward pass reads the derivative maps through a buffer descriptor: one uniform base,
+// 32-bit offsets (map q at the scalar offset 4 q P), and a range check that returns 0 for the
+// taps outside the image (offset kNoTap, past the buffer: tdgs_loss_grad takes images of fewer
+// than 2^31 / 36 pixels) instead of a select per load. Word 3 of the descriptor sets
+// DATA_FORMAT = 32 bits (0x00020000, as for raw buffers on the gfx9 family). Only 4-byte loads
+// at distinct scalar offsets go through it: a 12-byte buffer load with this descriptor (and
+// the compiler merges three adjacent 4-byte ones into one) returned the first word three
+// times, so the images keep plain loads.
+using Rsrc = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ Rsrc ssim_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kNoTap = 0x80000000u;
+
 // k_ssim_forward LDS: one buffer, in turn the input (x, y) pairs of the 26 x 26 tile per
 // (column, channel), the pass-1 values of the 15 quantities per (quantity, output row), columns
 // contiguous, and the pass-2 output (15 values per pixel). Each pass reads its inputs into
@@ -76,8 +90,9 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     ssim_tile((H + kSsimT - 1) / kSsimT, gridDim.x, &tv, &tu);
     const int v0 = tv * kSsimT - kSsimR, u0 = tu * kSsimT - kSsimR;
     // the tile's inputs: pixel k = t + 256 i (i < 3) of the 26 x 26 tile, all loads issued
-    // before the first LDS store
-    double l1 = 0.0;
+    // before the first LDS store (pixel indices are 32-bit: tdgs_loss_grad takes images of fewer
+    // than 2^31 / 9 pixels)
+    float l1 = 0.0f;   // this thread's |x - y| (at most 9 terms), summed in double over the workgroup
     constexpr int kLoads = (kSsimIn * kSsimIn + 255) / 256;
     float2 xy[kLoads][3];
 #pragma unroll
@@ -86,7 +101,7 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
         const bool in = k < kSsimIn * kSsimIn && v >= 0 && v < H && u >= 0 && u < W;
-        const int64_t p = (int64_t)v + (int64_t)H * u;
+        const uint32_t p = (uint32_t)(v + H * u);
         // one 12-byte load per pixel and image (the three channels are contiguous)
         const float3 xp = in ? reinterpret_cast<const float3*>(x)[p] : make_float3(0.0f, 0.0f, 0.0f);
         const float3 yp = in ? reinterpret_cast<const float3*>(y)[p] : make_float3(0.0f, 0.0f, 0.0f);
@@ -103,7 +118,7 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             s_in[(iu * 3 + c) * kRow + iv] = xy[i][c];
-            if (own) l1 += fabs((double)xy[i][c].x - (double)xy[i][c].y);   // (zero outside the image)
+            if (own) l1 += fabsf(xy[i][c].x - xy[i][c].y);   // (zero outside the image)
         }
     }
     __syncthreads();
@@ -128,9 +143,11 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
 #pragma unroll
         for (int o = 0; o < 6; ++o) {
             if (o >= no) break;
-            float m0 = 0.0f, m1 = 0.0f, m2 = 0.0f, m3 = 0.0f, m4 = 0.0f;
+            // (the first tap as a product: no zeroed accumulators)
+            const float w0 = win.w[0], a0 = a[o], b0 = b[o];
+            float m0 = w0 * a0, m1 = w0 * b0, m2 = w0 * (a0 * a0), m3 = w0 * (b0 * b0), m4 = w0 * (a0 * b0);
 #pragma unroll
-            for (int d = 0; d < 2 * kSsimR + 1; ++d) {
+            for (int d = 1; d < 2 * kSsimR + 1; ++d) {
                 const float wd = win.w[d], av = a[o + d], bv = b[o + d];
                 m0 = fmaf(wd, av, m0);
                 m1 = fmaf(wd, bv, m1);
@@ -161,9 +178,9 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     if (p2) {
 #pragma unroll
         for (int ou = 0; ou < kSsimT; ++ou) {
-            float m = 0.0f;
+            float m = win.w[0] * f[ou];
 #pragma unroll
-            for (int d = 0; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], f[ou + d], m);
+            for (int d = 1; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], f[ou + d], m);
             s_out[(ou * kSsimT + p2_ov) * kOutPitch + p2_q] = m;
         }
     }
@@ -174,10 +191,10 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
     float m[kQF];
 #pragma unroll
     for (int q = 0; q < kQF; ++q) m[q] = s_out[(ou * kSsimT + ov) * kOutPitch + q];
-    double ssum = 0.0;
+    float ssum = 0.0f;   // this thread's S (3 terms), summed in double over the workgroup
     if (on) {
-        const int64_t p = (int64_t)v + (int64_t)H * u;
-        const int64_t P = (int64_t)W * H;
+        const uint32_t p = (uint32_t)(v + H * u);
+        const uint32_t P = (uint32_t)W * (uint32_t)H;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const float mx = m[5 * c], my = m[5 * c + 1], sxx = m[5 * c + 2], syy = m[5 * c + 3], sxy = m[5 * c + 4];
@@ -193,19 +210,20 @@ __global__ __launch_bounds__(256) void k_ssim_forward(const float* __restrict__ 
             const float dB = 2.0f * mx * (b2 - b1);
             // planar maps (plane q of W H values, pixel order of the image): consecutive lanes
             // (consecutive v) write consecutive words
-            dmap[c * P + p] = (dA - S * dB) * rB;     // dS/dmu_x
-            dmap[(3 + c) * P + p] = -S * r2;          // dS/dE[x^2]
-            dmap[(6 + c) * P + p] = 2.0f * a1 * rB;   // dS/dE[xy]
-            ssum += (double)S;
+            (dmap + c * P)[p] = (dA - S * dB) * rB;     // dS/dmu_x
+            (dmap + (3 + c) * P)[p] = -S * r2;          // dS/dE[x^2]
+            (dmap + (6 + c) * P)[p] = 2.0f * a1 * rB;   // dS/dE[xy]
+            ssum += S;
         }
     }
+    double ssd = ssum, l1d = l1;
     for (int d = 32; d >= 1; d >>= 1) {
-        ssum += __shfl_xor(ssum, d, kWave);
-        l1 += __shfl_xor(l1, d, kWave);
+        ssd += __shfl_xor(ssd, d, kWave);
+        l1d += __shfl_xor(l1d, d, kWave);
     }
     if (__lane_id() == 0) {
-        s_red[0][t / kWave] = ssum;
-        s_red[1][t / kWave] = l1;
+        s_red[0][t / kWave] = ssd;
+        s_red[1][t / kWave] = l1d;
     }
     __syncthreads();
     if (t == 0) {
@@ -264,17 +282,19 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
     const int ov = t % kSsimT, ou = t / kSsimT;
     const int v = v0 + kSsimR + ov, u = u0 + kSsimR + ou;
     const bool on = v < H && u < W;
-    const int64_t p = 3 * ((int64_t)v + (int64_t)H * u);
+    const uint32_t p = (uint32_t)(v + H * u);   // (32-bit, as in k_ssim_forward)
+    const uint32_t P = (uint32_t)W * (uint32_t)H;
     float xv[3], yv[3];
     {
-        const float3 xp = on ? reinterpret_cast<const float3*>(x)[p / 3] : make_float3(0.0f, 0.0f, 0.0f);
-        const float3 yp = on ? reinterpret_cast<const float3*>(y)[p / 3] : make_float3(0.0f, 0.0f, 0.0f);
+        const float3 xp = on ? reinterpret_cast<const float3*>(x)[p] : make_float3(0.0f, 0.0f, 0.0f);
+        const float3 yp = on ? reinterpret_cast<const float3*>(y)[p] : make_float3(0.0f, 0.0f, 0.0f);
         xv[0] = xp.x; xv[1] = xp.y; xv[2] = xp.z;
         yv[0] = yp.x; yv[1] = yp.y; yv[2] = yp.z;
     }
     // the tile's nine maps: pixel k = t + 256 i (i < 3) of the 26 x 26 tile, all loads issued
     // before the first LDS store
     constexpr int kLoads = (kSsimIn * kSsimIn + 255) / 256;
+    const Rsrc rm = ssim_rsrc(dmap, 4u * kQB * P);
     float dv[kLoads][kQB];
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
@@ -282,10 +302,11 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         const int iv = k % kSsimIn, iu = k / kSsimIn;
         const int v = v0 + iv, u = u0 + iu;
         const bool in = k < kSsimIn * kSsimIn && v >= 0 && v < H && u >= 0 && u < W;
-        const int64_t p = (int64_t)v + (int64_t)H * u;
-        const int64_t P = (int64_t)W * H;
+        const uint32_t off = in ? 4u * (uint32_t)(v + H * u) : kNoTap;
+        // (off + 4 q P stays past the buffer for kNoTap)
 #pragma unroll
-        for (int q = 0; q < kQB; ++q) dv[i][q] = in ? dmap[q * P + p] : 0.0f;
+        for (int q = 0; q < kQB; ++q)
+            dv[i][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, off, 4u * q * P, 0));
     }
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
@@ -309,9 +330,9 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         const int iu = t / kQB, q = t % kQB;
 #pragma unroll
         for (int ov = 0; ov < kSsimT; ++ov) {
-            float m = 0.0f;
+            float m = win.w[0] * a[ov];
 #pragma unroll
-            for (int d = 0; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], a[ov + d], m);
+            for (int d = 1; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], a[ov + d], m);
             s_v[(q * kSsimT + ov) * kRow + iu] = m;
         }
     }
@@ -330,9 +351,9 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         const int ov = t % kSsimT, q = t / kSsimT;
 #pragma unroll
         for (int ou = 0; ou < kSsimT; ++ou) {
-            float m = 0.0f;
+            float m = win.w[0] * b[ou];
 #pragma unroll
-            for (int d = 0; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], b[ou + d], m);
+            for (int d = 1; d < 2 * kSsimR + 1; ++d) m = fmaf(win.w[d], b[ou + d], m);
             s_out[(ou * kSsimT + ov) * kOutPitch + q] = m;
         }
     }
@@ -348,7 +369,7 @@ __global__ __launch_bounds__(256) void k_ssim_backward(const float* __restrict__
         const float s = xv[c] > yv[c] ? w_l1 : -w_l1;   // ties take -w_l1 (training.jl:214-215)
         gr[c] = s + w_ssim * dssim;   // product rounded, then the sum, as the reference's broadcast
     }
-    reinterpret_cast<float3*>(grad)[p / 3] = make_float3(gr[0], gr[1], gr[2]);
+    reinterpret_cast<float3*>(grad)[p] = make_float3(gr[0], gr[1], gr[2]);
 }
 
 static SsimWindow gaussian_window() {
@@ -385,6 +406,7 @@ size_t tdgs_loss_temp_bytes(int32_t width, int32_t height) {
 int tdgs_loss_grad(void* stream, const float* rendered, const float* gt, int32_t width, int32_t height,
                    float dssim_weight, float* grad_out, double* sums_dev, void* temp, size_t temp_bytes) {
     TDGS_REQUIRE(width > 0 && height > 0, "bad image size");
+    TDGS_REQUIRE((int64_t)width * height * 36 < ((int64_t)1 << 31), "image too large for the loss kernels (32-bit offsets)");
     TDGS_REQUIRE(rendered && gt && grad_out && sums_dev && temp, "null arrays");
     TDGS_REQUIRE(temp_bytes >= tdgs_loss_temp_bytes(width, height), "loss scratch too small");
     hipStream_t s = (hipStream_t)stream;
