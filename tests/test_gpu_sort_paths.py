@@ -84,10 +84,10 @@ def test_sort_pairs_at_cfg4_scale_properties(gpu):
 
 
 def test_depth_presort_bucket_past_capacity(gpu, oracle):
-    """The bucketed depth presort (dsort.hpp) takes its splitters from a sample of 4096 slots;
+    """The bucketed depth presort (dsort.hpp) takes its splitters from a sample of 8192 slots;
     a bucket of more than 8192 Gaussians is sorted chunk by chunk through global memory. Here
     the sampled slots keep the scene's depths while every other Gaussian lies in a narrow depth
-    band (relative width 1e-5) that no sampled key falls in: that band (~46k Gaussians, distinct
+    band (relative width 1e-5) that no sampled key falls in: that band (~42k Gaussians, distinct
     depths) lands in at most two buckets. The frame must equal the oracle bit for bit (tile lists,
     images, last contributors), with host and with device counts."""
     from tdgs_amd import synthetic
@@ -96,7 +96,7 @@ def test_depth_presort_bucket_past_capacity(gpu, oracle):
     cam = w.cameras[0]
     g_host = w.gaussians
     sampled = np.zeros(n, bool)
-    sampled[(np.arange(4096, dtype=np.int64) * n) // 4096] = True
+    sampled[(np.arange(8192, dtype=np.int64) * n) // 8192] = True   # ds_sample_store's slots
     rng = np.random.default_rng(11)
     mo = g_host.means_opacity
     fwd = cam.R_c2w[:, 2].astype(np.float64)

@@ -9,7 +9,7 @@
 //
 // Three launches instead of the eight of a 4-pass LSD radix sort over the 32-bit keys, whose
 // short, latency-bound passes cost ~8 us each whatever their work:
-//   k_ds_count      every workgroup first takes 255 splitters from a sample of 4096 keys
+//   k_ds_count      every workgroup first takes 255 splitters from a sample of 8192 keys
 //                   (strided over the slots, written by the projection beside the keys):
 //                   histogrammed in 4096 bins over its range, splitters at bin edges near
 //                   equal ranks of its non-empty part, as composites (depth bits << 32 |
@@ -41,9 +41,12 @@ constexpr int kDsThreads = 1024;                        // splitter and bucket w
 constexpr int kDsWaves = kDsThreads / kWave;
 constexpr int kDsItems = 8;                             // keys per thread of a bucket sort (16: register spills)
 constexpr int kDsCap = kDsThreads * kDsItems;           // buckets of up to 8192 Gaussians sort in LDS
-constexpr int kDsSampleItems = 4;
-constexpr int kDsSample = kDsThreads * kDsSampleItems;  // 4096 sampled keys (2048: +3 us of sample
-                                                        // loads less, but buckets 3.6x the mean)
+constexpr int kDsSampleItems = 8;
+// 8192 sampled keys: ~17 non-empty samples per bucket at 1M Gaussians, 1080p, whose largest
+// bucket then holds fewer keys (the bucket sorts take as long as their largest bucket): presort
+// 53.3 -> 50.7 us against 4096 samples, no faster with 16384 (2048: +3 us of sample loads less,
+// but buckets up to 3.6x the mean)
+constexpr int kDsSample = kDsThreads * kDsSampleItems;
 using DsTile = RsTile<uint64_t>;                        // the bucket pass: 4096-key tiles, 512 threads
 constexpr int kDsDigit = 512;                           // bucket sorts: 9-bit digits (2 passes cover the
                                                         // 15-20 bits a bucket's keys typically span)
