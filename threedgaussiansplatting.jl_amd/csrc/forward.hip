@@ -2087,7 +2087,9 @@ static int bin_tile_lists(hipStream_t s, const tdgs_tiling* tiling, tdgs_render_
             k_rs_scan_rows<<<kRsBins, 256, 0, s>>>(table, count_tiles, totals, d_used, kEmitTile);
             TDGS_LAUNCHED();
         }
-        uint16_t* ek = one_pass ? c16 : c16_alt;
+        // (with one pass the sorted block ids are not written: the block ends come from the
+        // digit totals)
+        uint16_t* ek = one_pass ? nullptr : c16_alt;
         int32_t* ev = one_pass ? buf->values : buf->sorted_values;
         if ((int64_t)egrid < eblocks) {
             if (cmask)

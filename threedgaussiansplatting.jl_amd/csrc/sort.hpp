@@ -331,7 +331,7 @@ __device__ __forceinline__ void rs_scatter_tile(const K (&key)[RsTile<K>::kItems
             const uint32_t d = (uint32_t)(kk >> shift) & mask;
             const int32_t o = s_delta[d] + i;
             if (o >= 0 && o < nn) {
-                kout[o] = kk;
+                if (kout) kout[o] = kk;   // (null: a last pass whose sorted keys nothing reads)
                 opos[k] = o;
             } else {
                 atomicOr(err, 1u);   // inconsistent counts: never write out of bounds
