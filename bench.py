@@ -104,7 +104,6 @@ TRAFFIC_KERNELS = [
     ("k_backward_project<true>", "backward_project_adam"),
     ("k_rs_scatter_grouped<unsigned int>", "depth_sort_scatter"),
     ("k_rs_count_grouped<unsigned int>", "depth_sort_count"),
-    ("k_ds_splitters", "depth_sort_splitters"),
     ("k_ds_count", "depth_sort_bucket_count"),
     ("k_ds_scatter", "depth_sort_bucket_scatter"),
     ("k_ds_buckets", "depth_sort_buckets"),
@@ -639,14 +638,13 @@ def measured_traffic():
 
 # the counter-summary kernels of each survey row with their launches per frame (or step): the
 # row's bytes are the sum of per-launch bytes times launches (up to DS_MAX_SLOTS Gaussians the
-# depth presort is the bucket sort, four launches; above, the radix passes run their count and
+# depth presort is the bucket sort, three launches; above, the radix passes run their count and
 # scatter kernels once per 8-bit pass, four passes over the 32-bit depth keys)
 MEASURED_KERNELS = {
     "K1_project": [("keep_counts", 1), ("project", 1)],
     "K2_scan_keys": [("count_scan_apply", 1), ("emit_count", 1)],
-    "K3_K4_sort_ranges": [("depth_sort_splitters", 1), ("depth_sort_bucket_count", 1),
-                          ("depth_sort_bucket_scatter", 1), ("depth_sort_buckets", 1), ("coarse_sort_scatter", 1),
-                          ("bin_count", 1), ("bin_scan", 1), ("bin_write", 1)],
+    "K3_K4_sort_ranges": [("depth_sort_bucket_count", 1), ("depth_sort_bucket_scatter", 1), ("depth_sort_buckets", 1),
+                          ("coarse_sort_scatter", 1), ("bin_count", 1), ("bin_scan", 1), ("bin_write", 1)],
     "K3_K4_sort_ranges_radix": [("depth_sort_count", 4), ("depth_sort_scatter", 4), ("coarse_sort_scatter", 1),
                                 ("bin_count", 1), ("bin_scan", 1), ("bin_write", 1)],
     "K5_blend": [("blend", 1)],
