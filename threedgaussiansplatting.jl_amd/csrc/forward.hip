@@ -1892,7 +1892,6 @@ static void render_layout(A& ar, int64_t cap, int64_t key_cap, const tdgs_tiling
     ar.template take<int32_t>(t ? ((int64_t)t->nb_tiles_x * t->nb_tiles_y + 3) / 4 * 4 : 0);   // tiles' totals
     ar.template take<int4>(cap);                                                  // rectangles in depth order
     ar.template take<uint32_t>(zero_words(cap, key_cap));                         // zeroed each frame
-    ar.template take<uint64_t>(kDsBuckets);                                       // presort: splitters
     ar.template take<uint32_t>(kDsBuckets + 1);                                   // bucket starts
     ar.template take<uint32_t>(kDsSample);                                        // sampled keys
     ar.template take<uint8_t>(cap);                                               // bucket ids
