@@ -39,6 +39,18 @@ int hip_fail(hipError_t e, const char* what, const char* file, int line);
 
 constexpr int kWave = 64;
 
+// Workgroups are dealt to the 8 XCDs in turn by linear id (workgroup i runs on XCD i mod 8),
+// each XCD with its own L2.
+constexpr int kXcds = 8;
+// XCD-aware work order: the item (0-based) of workgroup i of a grid of n workgroups, XCD k
+// taking the contiguous items k q .. k q + q - 1 (q = n / 8) in order, so that neighbouring
+// items, which read much of the same data, meet in one L2. A bijection on the first 8 q ids;
+// the remaining n mod 8 keep their own index.
+__device__ __forceinline__ int xcd_band_item(int i, int n) {
+    const int q = n / kXcds;
+    return i < kXcds * q ? (i % kXcds) * q + i / kXcds : i;
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
 

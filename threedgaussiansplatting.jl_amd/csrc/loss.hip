@@ -38,15 +38,10 @@ constexpr int kQF = 15;                // forward filtered quantities: 5 per cha
 constexpr int kQB = 9;                 // backward filtered quantities: D1, D2, D3 per channel
 constexpr int kOutPitch = 17;          // pass-2 output: value q of pixel (ou, ov) at (ou*16+ov)*17+q
 
-// XCD-aware tile order: workgroups are handed to the 8 XCDs round-robin by linear id, so the
-// workgroups with id = x (mod 8) all run on XCD x. They get one contiguous band of tiles (v
-// fastest), whose shared halos then stay in that XCD's L2. A bijection on the first
-// 8 * floor(n / 8) ids; the remainder keeps its own index.
-constexpr int kXcds = 8;
+// XCD-aware tile order (xcd_band_item): each XCD takes one contiguous band of tiles (v
+// fastest), whose shared halos then stay in that XCD's L2.
 __device__ __forceinline__ void ssim_tile(int ntv, int n, int* tv, int* tu) {
-    const int b = blockIdx.x;
-    const int per = n / kXcds;
-    const int L = b < per * kXcds ? (b % kXcds) * per + b / kXcds : b;
+    const int L = xcd_band_item(blockIdx.x, n);
     *tv = L % ntv;
     *tu = L / ntv;
 }

@@ -59,12 +59,11 @@ constexpr int kRsWaves = kRsThreads / kWave;
 static_assert(kRsThreads >= kRsBins && kRsThreads % kRsBins == 0, "digit owners");
 
 // Column of radix tile `tile` in a row of the digit-major count table. Workgroups are dealt
-// round-robin to the 8 XCDs (each with its own L2), so tile t runs on XCD t % 8; the columns
+// round-robin to the kXcds XCDs (each with its own L2), so tile t runs on XCD t % 8; the columns
 // are grouped by XCD (tile t at (t % 8) * (pitch / 8) + t / 8) so that the cache lines one
 // XCD's count workgroups write, and its scatter workgroups read, are not shared with another
 // XCD's L2 (partial lines merged across XCDs cost 7x the table in write traffic). Rows are
 // rs_pitch(tiles) words apart.
-constexpr int kXcds = 8;
 __host__ __device__ inline int64_t rs_pitch(int64_t tiles) { return (tiles + kXcds - 1) / kXcds * kXcds; }
 __host__ __device__ inline int64_t rs_col(int64_t tile, int64_t tiles) {
     return (tile % kXcds) * (rs_pitch(tiles) / kXcds) + tile / kXcds;
