@@ -1456,10 +1456,11 @@ struct BlendArgs {
 // branch) when no lane is live, and the state update runs under exec = contributing and not
 // stopping lanes; the compiled loop needed about 30 scalar and 39 vector instructions per
 // live record against 10 and 32 here. The next record (all ten floats) is read from LDS into
-// a second register set while the current one is processed (the loop is unrolled twice), so
-// no step waits on LDS; the LDS array holds one record more than a batch for the read past the
-// last record. Valid only when every live exponent lies in [-87, 88] (the batch is not
-// `checked`). v39-v63 are its scratch registers (the kernel stays within 64 VGPRs, 8
+// a second register set while the current one is processed, so no step waits on LDS. Records
+// run in groups of four with one bound check per group (a scalar instruction costs a step about
+// as much as a vector one): after a batch of nb records the LDS array holds three records of
+// padding that no pixel is live for, and one more for the read past the last group. Valid only
+// when every live exponent lies in [-87, 88] (the batch is not `checked`). v39-v63 are its scratch registers (the kernel stays within 64 VGPRs, 8
 // wavefronts per SIMD). Returns the mask of the lanes that did not stop.
 // the literals of blend_batch's exponential are exp_poly's coefficients
 static_assert(__builtin_bit_cast(uint32_t, kExpC6) == 0x3ab51223u && __builtin_bit_cast(uint32_t, kExpC4) == 0x3d2aac79u &&
@@ -1467,6 +1468,16 @@ static_assert(__builtin_bit_cast(uint32_t, kExpC6) == 0x3ab51223u && __builtin_b
                   __builtin_bit_cast(uint32_t, -kLn2Hi) == 0xbf317200u && __builtin_bit_cast(uint32_t, -kLn2Lo) == 0xb5bfbe8eu &&
                   __builtin_bit_cast(uint32_t, kLog2e) == 0x3fb8aa3bu,
               "blend_batch constants");
+// A record no pixel is live for: every exponent coefficient 0 but the constant term, -inf
+// (colour and depth unused). The constants are made at the store (an asm the compiler does not
+// hoist), so that they hold no registers across the blending loop.
+__device__ __forceinline__ void blend_pad(BlendRec* r) {
+    float z, ninf;
+    asm volatile("v_mov_b32 %0, 0\n v_mov_b32 %1, 0xff800000" : "=v"(z), "=v"(ninf));
+    r->a = make_float4(z, z, z, z);
+    *reinterpret_cast<float2*>(&r->b) = make_float2(z, ninf);
+}
+
 template <bool DEPTH, bool LAST>
 __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0, int32_t idx_end, float uu,
                                                 float vv, float uv, float cu, float cv, float e_cut,
@@ -1475,113 +1486,198 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
     const float c5 = kExpC5;   // exp_poly's coefficient of r^5 (a VGPR operand)
     uint64_t act, live, ctb, stp, sav;
     int32_t idx;
-#define TDGS_BLEND_ASM(DEPTH_FMA, READ_C, LAST_MOV)                                                                  \
-    asm volatile(                                                                                  \
-        "s_and_b64 %[act], exec, exec\n"                                                           \
-        "s_cbranch_scc0 .Lend_%=\n"                                                                \
-        "s_mov_b32 %[idx], %[i0]\n"                                                                \
-        "v_mov_b32 v39, %[addr]\n"                                                                 \
-        "ds_read_b128 v[40:43], v39\n"                                                             \
-        "ds_read_b128 v[44:47], v39 offset:16\n"                                                   \
-        READ_C("v[48:49]", "v48", "32")                                                              \
-        ".Lstep_%=:\n"                                                                             \
-        "s_waitcnt lgkmcnt(0)\n"                                                                   \
-        "ds_read_b128 v[50:53], v39 offset:48\n"                                                   \
-        "ds_read_b128 v[54:57], v39 offset:64\n"                                                   \
-        READ_C("v[58:59]", "v58", "80")                                                              \
-        "v_fma_f32 v60, v44, %[cv], v45\n"                                                         \
-        "v_fmac_f32 v60, v43, %[cu]\n"                                                             \
-        "v_fmac_f32 v60, v42, %[uv]\n"                                                             \
-        "v_fmac_f32 v60, v41, %[vv]\n"                                                             \
-        "v_fmac_f32 v60, v40, %[uu]\n"                                                             \
-        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                         \
-        "s_and_b64 %[live], vcc, %[act]\n"                                                         \
-        "s_cbranch_scc0 .Lnexta_%=\n"                                                              \
-        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                         \
-        "v_rndne_f32 v61, v61\n"                                                                   \
-        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                        \
-        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                        \
-        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                \
-        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                  \
-        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
-        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
-        "v_cvt_i32_f32 v61, v61\n"                                                                 \
-        "v_ldexp_f32 v62, v62, v61\n"                                                              \
-        "v_min_f32 v62, %[maxa], v62\n"                                                            \
-        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                        \
-        "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
-        "v_sub_f32 v63, 1.0, v62\n"                                                                \
-        "v_mul_f32 v63, %[T], v63\n"                                                               \
-        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                         \
-        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                          \
-        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                     \
-        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                      \
-        "v_mul_f32 v61, %[T], v62\n"                                                               \
-        "v_fmac_f32 %[C0], v61, v46\n"                                                             \
-        "v_fmac_f32 %[C1], v61, v47\n"                                                             \
-        "v_fmac_f32 %[C2], v61, v48\n"                                                             \
-        DEPTH_FMA("v49")                                                                           \
-        "v_mov_b32 %[T], v63\n"                                                                    \
-        LAST_MOV                                                                                   \
-        "s_mov_b64 exec, %[sav]\n"                                                                 \
-        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
-        "s_cbranch_scc0 .Lend_%=\n"                                                                \
-        ".Lnexta_%=:\n"                                                                            \
-        "s_add_u32 %[idx], %[idx], 1\n"                                                            \
-        "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
-        "s_cbranch_scc0 .Lend_%=\n"                                                                \
-        "s_waitcnt lgkmcnt(0)\n"                                                                   \
-        "ds_read_b128 v[40:43], v39 offset:96\n"                                                   \
-        "ds_read_b128 v[44:47], v39 offset:112\n"                                                   \
-        READ_C("v[48:49]", "v48", "128")                                                              \
-        "v_fma_f32 v60, v54, %[cv], v55\n"                                                         \
-        "v_fmac_f32 v60, v53, %[cu]\n"                                                             \
-        "v_fmac_f32 v60, v52, %[uv]\n"                                                             \
-        "v_fmac_f32 v60, v51, %[vv]\n"                                                             \
-        "v_fmac_f32 v60, v50, %[uu]\n"                                                             \
-        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                         \
-        "s_and_b64 %[live], vcc, %[act]\n"                                                         \
-        "s_cbranch_scc0 .Lnextb_%=\n"                                                              \
-        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                         \
-        "v_rndne_f32 v61, v61\n"                                                                   \
-        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                        \
-        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                        \
-        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                \
-        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                  \
-        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                  \
-        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
-        "v_fma_f32 v62, v62, v60, 1.0\n"                                                           \
-        "v_cvt_i32_f32 v61, v61\n"                                                                 \
-        "v_ldexp_f32 v62, v62, v61\n"                                                              \
-        "v_min_f32 v62, %[maxa], v62\n"                                                            \
-        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                        \
-        "s_and_b64 %[ctb], vcc, %[live]\n"                                                         \
-        "v_sub_f32 v63, 1.0, v62\n"                                                                \
-        "v_mul_f32 v63, %[T], v63\n"                                                               \
-        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                         \
-        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                          \
-        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                     \
-        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                      \
-        "v_mul_f32 v61, %[T], v62\n"                                                               \
-        "v_fmac_f32 %[C0], v61, v56\n"                                                             \
-        "v_fmac_f32 %[C1], v61, v57\n"                                                             \
-        "v_fmac_f32 %[C2], v61, v58\n"                                                             \
-        DEPTH_FMA("v59")                                                                           \
-        "v_mov_b32 %[T], v63\n"                                                                    \
-        LAST_MOV                                                                                   \
-        "s_mov_b64 exec, %[sav]\n"                                                                 \
-        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                     \
-        "s_cbranch_scc0 .Lend_%=\n"                                                                \
-        ".Lnextb_%=:\n"                                                                            \
-        "v_add_u32 v39, 0x60, v39\n"                                                               \
-        "s_add_u32 %[idx], %[idx], 1\n"                                                            \
-        "s_cmp_lt_u32 %[idx], %[iend]\n"                                                           \
-        "s_cbranch_scc1 .Lstep_%=\n"                                                               \
-        ".Lend_%=:\n"                                                                              \
-        "s_waitcnt lgkmcnt(0)\n"                                                                   \
+#define TDGS_BLEND_ASM(DEPTH_FMA, READ_C, LAST_MOV)                                                         \
+    asm volatile(                                                                                           \
+        "s_and_b64 %[act], exec, exec\n"                                                                    \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                         \
+        "s_mov_b32 %[idx], %[i0]\n"                                                                         \
+        "v_mov_b32 v39, %[addr]\n"                                                                          \
+        "ds_read_b128 v[40:43], v39\n"                                                                      \
+        "ds_read_b128 v[44:47], v39 offset:16\n"                                                            \
+        READ_C("v[48:49]", "v48", "32")                                                                     \
+        ".Lstep_%=:\n"                                                                                      \
+        "s_waitcnt lgkmcnt(0)\n"                                                                            \
+        "ds_read_b128 v[50:53], v39 offset:48\n"                                                            \
+        "ds_read_b128 v[54:57], v39 offset:64\n"                                                            \
+        READ_C("v[58:59]", "v58", "80")                                                                     \
+        "v_fma_f32 v60, v44, %[cv], v45\n"                                                                  \
+        "v_fmac_f32 v60, v43, %[cu]\n"                                                                      \
+        "v_fmac_f32 v60, v42, %[uv]\n"                                                                      \
+        "v_fmac_f32 v60, v41, %[vv]\n"                                                                      \
+        "v_fmac_f32 v60, v40, %[uu]\n"                                                                      \
+        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
+        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
+        "s_cbranch_scc0 .Ls0_%=\n"                                                                          \
+        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
+        "v_rndne_f32 v61, v61\n"                                                                            \
+        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
+        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                                 \
+        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                         \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_cvt_i32_f32 v61, v61\n"                                                                          \
+        "v_ldexp_f32 v62, v62, v61\n"                                                                       \
+        "v_min_f32 v62, %[maxa], v62\n"                                                                     \
+        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
+        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
+        "v_sub_f32 v63, 1.0, v62\n"                                                                         \
+        "v_mul_f32 v63, %[T], v63\n"                                                                        \
+        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
+        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
+        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
+        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "v_mul_f32 v61, %[T], v62\n"                                                                        \
+        "v_fmac_f32 %[C0], v61, v46\n"                                                                      \
+        "v_fmac_f32 %[C1], v61, v47\n"                                                                      \
+        "v_fmac_f32 %[C2], v61, v48\n"                                                                      \
+        DEPTH_FMA("v49")                                                                                    \
+        "v_mov_b32 %[T], v63\n"                                                                             \
+        LAST_MOV("0")                                                                                       \
+        "s_mov_b64 exec, %[sav]\n"                                                                          \
+        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                         \
+        ".Ls0_%=:\n"                                                                                        \
+        "s_waitcnt lgkmcnt(0)\n"                                                                            \
+        "ds_read_b128 v[40:43], v39 offset:96\n"                                                            \
+        "ds_read_b128 v[44:47], v39 offset:112\n"                                                           \
+        READ_C("v[48:49]", "v48", "128")                                                                    \
+        "v_fma_f32 v60, v54, %[cv], v55\n"                                                                  \
+        "v_fmac_f32 v60, v53, %[cu]\n"                                                                      \
+        "v_fmac_f32 v60, v52, %[uv]\n"                                                                      \
+        "v_fmac_f32 v60, v51, %[vv]\n"                                                                      \
+        "v_fmac_f32 v60, v50, %[uu]\n"                                                                      \
+        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
+        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
+        "s_cbranch_scc0 .Ls1_%=\n"                                                                          \
+        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
+        "v_rndne_f32 v61, v61\n"                                                                            \
+        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
+        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                                 \
+        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                         \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_cvt_i32_f32 v61, v61\n"                                                                          \
+        "v_ldexp_f32 v62, v62, v61\n"                                                                       \
+        "v_min_f32 v62, %[maxa], v62\n"                                                                     \
+        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
+        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
+        "v_sub_f32 v63, 1.0, v62\n"                                                                         \
+        "v_mul_f32 v63, %[T], v63\n"                                                                        \
+        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
+        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
+        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
+        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "v_mul_f32 v61, %[T], v62\n"                                                                        \
+        "v_fmac_f32 %[C0], v61, v56\n"                                                                      \
+        "v_fmac_f32 %[C1], v61, v57\n"                                                                      \
+        "v_fmac_f32 %[C2], v61, v58\n"                                                                      \
+        DEPTH_FMA("v59")                                                                                    \
+        "v_mov_b32 %[T], v63\n"                                                                             \
+        LAST_MOV("1")                                                                                       \
+        "s_mov_b64 exec, %[sav]\n"                                                                          \
+        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                         \
+        ".Ls1_%=:\n"                                                                                        \
+        "s_waitcnt lgkmcnt(0)\n"                                                                            \
+        "ds_read_b128 v[50:53], v39 offset:144\n"                                                           \
+        "ds_read_b128 v[54:57], v39 offset:160\n"                                                           \
+        READ_C("v[58:59]", "v58", "176")                                                                    \
+        "v_fma_f32 v60, v44, %[cv], v45\n"                                                                  \
+        "v_fmac_f32 v60, v43, %[cu]\n"                                                                      \
+        "v_fmac_f32 v60, v42, %[uv]\n"                                                                      \
+        "v_fmac_f32 v60, v41, %[vv]\n"                                                                      \
+        "v_fmac_f32 v60, v40, %[uu]\n"                                                                      \
+        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
+        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
+        "s_cbranch_scc0 .Ls2_%=\n"                                                                          \
+        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
+        "v_rndne_f32 v61, v61\n"                                                                            \
+        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
+        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                                 \
+        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                         \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_cvt_i32_f32 v61, v61\n"                                                                          \
+        "v_ldexp_f32 v62, v62, v61\n"                                                                       \
+        "v_min_f32 v62, %[maxa], v62\n"                                                                     \
+        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
+        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
+        "v_sub_f32 v63, 1.0, v62\n"                                                                         \
+        "v_mul_f32 v63, %[T], v63\n"                                                                        \
+        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
+        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
+        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
+        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "v_mul_f32 v61, %[T], v62\n"                                                                        \
+        "v_fmac_f32 %[C0], v61, v46\n"                                                                      \
+        "v_fmac_f32 %[C1], v61, v47\n"                                                                      \
+        "v_fmac_f32 %[C2], v61, v48\n"                                                                      \
+        DEPTH_FMA("v49")                                                                                    \
+        "v_mov_b32 %[T], v63\n"                                                                             \
+        LAST_MOV("2")                                                                                       \
+        "s_mov_b64 exec, %[sav]\n"                                                                          \
+        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                         \
+        ".Ls2_%=:\n"                                                                                        \
+        "s_waitcnt lgkmcnt(0)\n"                                                                            \
+        "ds_read_b128 v[40:43], v39 offset:192\n"                                                           \
+        "ds_read_b128 v[44:47], v39 offset:208\n"                                                           \
+        READ_C("v[48:49]", "v48", "224")                                                                    \
+        "v_fma_f32 v60, v54, %[cv], v55\n"                                                                  \
+        "v_fmac_f32 v60, v53, %[cu]\n"                                                                      \
+        "v_fmac_f32 v60, v52, %[uv]\n"                                                                      \
+        "v_fmac_f32 v60, v51, %[vv]\n"                                                                      \
+        "v_fmac_f32 v60, v50, %[uu]\n"                                                                      \
+        "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
+        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
+        "s_cbranch_scc0 .Ls3_%=\n"                                                                          \
+        "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
+        "v_rndne_f32 v61, v61\n"                                                                            \
+        "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
+        "v_fmac_f32 v60, 0xb5bfbe8e, v61\n"                                                                 \
+        "v_fmamk_f32 v62, v60, 0x3ab51223, %[c5]\n"                                                         \
+        "v_fmaak_f32 v62, v62, v60, 0x3d2aac79\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3e2aaa49\n"                                                           \
+        "v_fmaak_f32 v62, v62, v60, 0x3efffffe\n"                                                           \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_fma_f32 v62, v62, v60, 1.0\n"                                                                    \
+        "v_cvt_i32_f32 v61, v61\n"                                                                          \
+        "v_ldexp_f32 v62, v62, v61\n"                                                                       \
+        "v_min_f32 v62, %[maxa], v62\n"                                                                     \
+        "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
+        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
+        "v_sub_f32 v63, 1.0, v62\n"                                                                         \
+        "v_mul_f32 v63, %[T], v63\n"                                                                        \
+        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
+        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
+        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
+        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "v_mul_f32 v61, %[T], v62\n"                                                                        \
+        "v_fmac_f32 %[C0], v61, v56\n"                                                                      \
+        "v_fmac_f32 %[C1], v61, v57\n"                                                                      \
+        "v_fmac_f32 %[C2], v61, v58\n"                                                                      \
+        DEPTH_FMA("v59")                                                                                    \
+        "v_mov_b32 %[T], v63\n"                                                                             \
+        LAST_MOV("3")                                                                                       \
+        "s_mov_b64 exec, %[sav]\n"                                                                          \
+        "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_cbranch_scc0 .Lend_%=\n"                                                                         \
+        ".Ls3_%=:\n"                                                                                        \
+        "v_add_u32 v39, 0xc0, v39\n"                                                                        \
+        "s_add_u32 %[idx], %[idx], 4\n"                                                                     \
+        "s_cmp_lt_u32 %[idx], %[iend]\n"                                                                    \
+        "s_cbranch_scc1 .Lstep_%=\n"                                                                        \
+        ".Lend_%=:\n"                                                                                       \
+        "s_waitcnt lgkmcnt(0)\n"                                                                            \
         : [act] "=&s"(act), [live] "=&s"(live), [ctb] "=&s"(ctb), [stp] "=&s"(stp), [sav] "=&s"(sav), \
           [idx] "=&s"(idx), [T] "+v"(T), [C0] "+v"(C0), [C1] "+v"(C1), [C2] "+v"(C2), [D] "+v"(D),   \
           [last] "+v"(last)                                                                         \
@@ -1597,8 +1693,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
 #define TDGS_READ_BD(PAIR, ONE, OFF) "ds_read_b64 " PAIR ", v39 offset:" OFF "\n"
 #define TDGS_READ_B(PAIR, ONE, OFF) "ds_read_b32 " ONE ", v39 offset:" OFF "\n"
 // the last contributing index is tracked only when it is an output
-#define TDGS_LAST_ON "v_mov_b32 %[last], %[idx]\n"
-#define TDGS_LAST_OFF ""
+#define TDGS_LAST_ON(K) "v_add_u32_e64 %[last], %[idx], " K "\n"
+#define TDGS_LAST_OFF(K) ""
     if constexpr (DEPTH && LAST)
         TDGS_BLEND_ASM(TDGS_DEPTH_ON, TDGS_READ_BD, TDGS_LAST_ON);
     else if constexpr (DEPTH)
@@ -1670,10 +1766,14 @@ __global__ __launch_bounds__(1024) void k_render_tiles(BlendArgs a) {
     int32_t last = 0;
     bool done = !on;
     unsigned long long evals = 0, live_n = 0, contrib_n = 0;
+    // blend_batch runs records in groups of four: up to three records after a batch are padding
+    // that no pixel is live for (exponent -inf), written where a batch ends
+    for (int k = t; k < 3; k += NT) blend_pad(s_rec + NT + k);   // (tiles of fewer than 3 pixels too)
     for (int64_t base = beg; base < end; base += NT) {
         if (__syncthreads_count(done ? 0 : 1) == 0) break;
         const int64_t s = base + t;
         bool big = false;   // opacity above 1e38: exponents may pass 88
+        if (s >= end && s < end + 3) blend_pad(s_rec + t);
         if (s < end) {
             const int64_t f = (int64_t)a.sorted_f[s] - 1;
             const float* r = a.f2d + 9 * f;
@@ -1813,7 +1913,8 @@ static int launch_render_tiles(hipStream_t s, const tdgs_camera* cam, const tdgs
     a.mon_host = mon_host;
     const int nt = t->tile_width * t->tile_height;
     const dim3 grid(t->nb_tiles_x, t->nb_tiles_y);
-    const size_t lds = (size_t)(nt + 1) * sizeof(BlendRec);   // + the record blend_batch prefetches past a batch
+    // + the padding after a batch and the record blend_batch reads past its last group of four
+    const size_t lds = (size_t)(nt + 4) * sizeof(BlendRec);
     if (evaluations) {
         k_render_tiles<false, false, true><<<grid, nt, lds, s>>>(a);
         TDGS_LAUNCHED();
