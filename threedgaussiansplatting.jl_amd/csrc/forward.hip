@@ -1450,18 +1450,21 @@ struct BlendArgs {
 // exp_f_core's sequence, min with max_alpha, 1 - alpha, the products and the colour fused
 // multiply-adds; exp_f_core's final product with 2^n is one v_ldexp_f32, which rounds exactly
 // as that product does, subnormal results included), so every result is bit for bit the
-// compiled loop's. What differs is the
-// bookkeeping: the lanes still blending (act), live, contributing and stopping lanes are
-// 64-bit lane masks combined with scalar instructions, the exponential is skipped (scalar
-// branch) when no lane is live, and the state update runs under exec = contributing and not
-// stopping lanes; the compiled loop needed about 30 scalar and 39 vector instructions per
-// live record against 10 and 32 here. The next record (all ten floats) is read from LDS into
-// a second register set while the current one is processed, so no step waits on LDS. Records
-// run in groups of four with one bound check per group (a scalar instruction costs a step about
-// as much as a vector one): after a batch of nb records the LDS array holds three records of
-// padding that no pixel is live for, and one more for the read past the last group. Valid only
-// when every live exponent lies in [-87, 88] (the batch is not `checked`). v39-v63 are its scratch registers (the kernel stays within 64 VGPRs, 8
-// wavefronts per SIMD). Returns the mask of the lanes that did not stop.
+// compiled loop's. What differs is the bookkeeping. Inside the loop exec holds the lanes still
+// blending (act), so every compare yields its mask restricted to them: the live lanes are the
+// compare with e_cut (the exponential is skipped, by a branch on VCC, when none is live), the
+// contributing lanes the compare with min_alpha under exec = live, the stopping lanes the
+// compare with min_T under exec = contributing, and the state update runs under exec =
+// contributing and not stopping; exec is restored on exit. That is 7 scalar and 31 vector
+// instructions per live record (the compiled loop needed about 30 and 39) and 1 scalar
+// instruction per skipped one. The next record (all ten floats) is read from LDS
+// into a second register set while the current one is processed, so no step waits on LDS.
+// Records run in groups of four with one bound check per group (a scalar instruction costs a
+// step about as much as a vector one): after a batch of nb records the LDS array holds three
+// records of padding that no pixel is live for, and one more for the read past the last group.
+// Valid only when every live exponent lies in [-87, 88] (the batch is not `checked`). v39-v63
+// are its scratch registers (the kernel stays within 64 VGPRs, 8 wavefronts per SIMD). Returns
+// the mask of the lanes that did not stop.
 // the literals of blend_batch's exponential are exp_poly's coefficients
 static_assert(__builtin_bit_cast(uint32_t, kExpC6) == 0x3ab51223u && __builtin_bit_cast(uint32_t, kExpC4) == 0x3d2aac79u &&
                   __builtin_bit_cast(uint32_t, kExpC3) == 0x3e2aaa49u && __builtin_bit_cast(uint32_t, kExpC2) == 0x3efffffeu &&
@@ -1484,10 +1487,11 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
                                                 float max_alpha, float min_alpha, float min_T, float& T,
                                                 float& C0, float& C1, float& C2, float& D, int32_t& last) {
     const float c5 = kExpC5;   // exp_poly's coefficient of r^5 (a VGPR operand)
-    uint64_t act, live, ctb, stp, sav;
+    uint64_t act, ent, stp;
     int32_t idx;
 #define TDGS_BLEND_ASM(DEPTH_FMA, READ_C, LAST_MOV)                                                         \
     asm volatile(                                                                                           \
+        "s_mov_b64 %[ent], exec\n"                                                                          \
         "s_and_b64 %[act], exec, exec\n"                                                                    \
         "s_cbranch_scc0 .Lend_%=\n"                                                                         \
         "s_mov_b32 %[idx], %[i0]\n"                                                                         \
@@ -1506,8 +1510,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 v60, v41, %[vv]\n"                                                                      \
         "v_fmac_f32 v60, v40, %[uu]\n"                                                                      \
         "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
-        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
-        "s_cbranch_scc0 .Ls0_%=\n"                                                                          \
+        "s_cbranch_vccz .Ls0_%=\n"                                                                          \
+        "s_mov_b64 exec, vcc\n"                                                                             \
         "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
         "v_rndne_f32 v61, v61\n"                                                                            \
         "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
@@ -1522,13 +1526,11 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_ldexp_f32 v62, v62, v61\n"                                                                       \
         "v_min_f32 v62, %[maxa], v62\n"                                                                     \
         "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
-        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
         "v_sub_f32 v63, 1.0, v62\n"                                                                         \
         "v_mul_f32 v63, %[T], v63\n"                                                                        \
-        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
-        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
-        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
-        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "s_mov_b64 exec, vcc\n"                                                                             \
+        "v_cmp_gt_f32 %[stp], %[minT], v63\n"                                                               \
+        "s_andn2_b64 exec, exec, %[stp]\n"                                                                  \
         "v_mul_f32 v61, %[T], v62\n"                                                                        \
         "v_fmac_f32 %[C0], v61, v46\n"                                                                      \
         "v_fmac_f32 %[C1], v61, v47\n"                                                                      \
@@ -1536,8 +1538,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         DEPTH_FMA("v49")                                                                                    \
         "v_mov_b32 %[T], v63\n"                                                                             \
         LAST_MOV("0")                                                                                       \
-        "s_mov_b64 exec, %[sav]\n"                                                                          \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_mov_b64 exec, %[act]\n"                                                                          \
         "s_cbranch_scc0 .Lend_%=\n"                                                                         \
         ".Ls0_%=:\n"                                                                                        \
         "s_waitcnt lgkmcnt(0)\n"                                                                            \
@@ -1550,8 +1552,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 v60, v51, %[vv]\n"                                                                      \
         "v_fmac_f32 v60, v50, %[uu]\n"                                                                      \
         "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
-        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
-        "s_cbranch_scc0 .Ls1_%=\n"                                                                          \
+        "s_cbranch_vccz .Ls1_%=\n"                                                                          \
+        "s_mov_b64 exec, vcc\n"                                                                             \
         "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
         "v_rndne_f32 v61, v61\n"                                                                            \
         "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
@@ -1566,13 +1568,11 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_ldexp_f32 v62, v62, v61\n"                                                                       \
         "v_min_f32 v62, %[maxa], v62\n"                                                                     \
         "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
-        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
         "v_sub_f32 v63, 1.0, v62\n"                                                                         \
         "v_mul_f32 v63, %[T], v63\n"                                                                        \
-        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
-        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
-        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
-        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "s_mov_b64 exec, vcc\n"                                                                             \
+        "v_cmp_gt_f32 %[stp], %[minT], v63\n"                                                               \
+        "s_andn2_b64 exec, exec, %[stp]\n"                                                                  \
         "v_mul_f32 v61, %[T], v62\n"                                                                        \
         "v_fmac_f32 %[C0], v61, v56\n"                                                                      \
         "v_fmac_f32 %[C1], v61, v57\n"                                                                      \
@@ -1580,8 +1580,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         DEPTH_FMA("v59")                                                                                    \
         "v_mov_b32 %[T], v63\n"                                                                             \
         LAST_MOV("1")                                                                                       \
-        "s_mov_b64 exec, %[sav]\n"                                                                          \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_mov_b64 exec, %[act]\n"                                                                          \
         "s_cbranch_scc0 .Lend_%=\n"                                                                         \
         ".Ls1_%=:\n"                                                                                        \
         "s_waitcnt lgkmcnt(0)\n"                                                                            \
@@ -1594,8 +1594,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 v60, v41, %[vv]\n"                                                                      \
         "v_fmac_f32 v60, v40, %[uu]\n"                                                                      \
         "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
-        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
-        "s_cbranch_scc0 .Ls2_%=\n"                                                                          \
+        "s_cbranch_vccz .Ls2_%=\n"                                                                          \
+        "s_mov_b64 exec, vcc\n"                                                                             \
         "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
         "v_rndne_f32 v61, v61\n"                                                                            \
         "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
@@ -1610,13 +1610,11 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_ldexp_f32 v62, v62, v61\n"                                                                       \
         "v_min_f32 v62, %[maxa], v62\n"                                                                     \
         "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
-        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
         "v_sub_f32 v63, 1.0, v62\n"                                                                         \
         "v_mul_f32 v63, %[T], v63\n"                                                                        \
-        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
-        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
-        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
-        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "s_mov_b64 exec, vcc\n"                                                                             \
+        "v_cmp_gt_f32 %[stp], %[minT], v63\n"                                                               \
+        "s_andn2_b64 exec, exec, %[stp]\n"                                                                  \
         "v_mul_f32 v61, %[T], v62\n"                                                                        \
         "v_fmac_f32 %[C0], v61, v46\n"                                                                      \
         "v_fmac_f32 %[C1], v61, v47\n"                                                                      \
@@ -1624,8 +1622,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         DEPTH_FMA("v49")                                                                                    \
         "v_mov_b32 %[T], v63\n"                                                                             \
         LAST_MOV("2")                                                                                       \
-        "s_mov_b64 exec, %[sav]\n"                                                                          \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_mov_b64 exec, %[act]\n"                                                                          \
         "s_cbranch_scc0 .Lend_%=\n"                                                                         \
         ".Ls2_%=:\n"                                                                                        \
         "s_waitcnt lgkmcnt(0)\n"                                                                            \
@@ -1638,8 +1636,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_fmac_f32 v60, v51, %[vv]\n"                                                                      \
         "v_fmac_f32 v60, v50, %[uu]\n"                                                                      \
         "v_cmp_ngt_f32 vcc, %[cut], v60\n"                                                                  \
-        "s_and_b64 %[live], vcc, %[act]\n"                                                                  \
-        "s_cbranch_scc0 .Ls3_%=\n"                                                                          \
+        "s_cbranch_vccz .Ls3_%=\n"                                                                          \
+        "s_mov_b64 exec, vcc\n"                                                                             \
         "v_mul_f32 v61, 0x3fb8aa3b, v60\n"                                                                  \
         "v_rndne_f32 v61, v61\n"                                                                            \
         "v_fmac_f32 v60, 0xbf317200, v61\n"                                                                 \
@@ -1654,13 +1652,11 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "v_ldexp_f32 v62, v62, v61\n"                                                                       \
         "v_min_f32 v62, %[maxa], v62\n"                                                                     \
         "v_cmp_ngt_f32 vcc, %[mina], v62\n"                                                                 \
-        "s_and_b64 %[ctb], vcc, %[live]\n"                                                                  \
         "v_sub_f32 v63, 1.0, v62\n"                                                                         \
         "v_mul_f32 v63, %[T], v63\n"                                                                        \
-        "v_cmp_gt_f32 vcc, %[minT], v63\n"                                                                  \
-        "s_and_b64 %[stp], vcc, %[ctb]\n"                                                                   \
-        "s_andn2_b64 %[ctb], %[ctb], %[stp]\n"                                                              \
-        "s_and_saveexec_b64 %[sav], %[ctb]\n"                                                               \
+        "s_mov_b64 exec, vcc\n"                                                                             \
+        "v_cmp_gt_f32 %[stp], %[minT], v63\n"                                                               \
+        "s_andn2_b64 exec, exec, %[stp]\n"                                                                  \
         "v_mul_f32 v61, %[T], v62\n"                                                                        \
         "v_fmac_f32 %[C0], v61, v56\n"                                                                      \
         "v_fmac_f32 %[C1], v61, v57\n"                                                                      \
@@ -1668,8 +1664,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         DEPTH_FMA("v59")                                                                                    \
         "v_mov_b32 %[T], v63\n"                                                                             \
         LAST_MOV("3")                                                                                       \
-        "s_mov_b64 exec, %[sav]\n"                                                                          \
         "s_andn2_b64 %[act], %[act], %[stp]\n"                                                              \
+        "s_mov_b64 exec, %[act]\n"                                                                          \
         "s_cbranch_scc0 .Lend_%=\n"                                                                         \
         ".Ls3_%=:\n"                                                                                        \
         "v_add_u32 v39, 0xc0, v39\n"                                                                        \
@@ -1678,7 +1674,8 @@ __device__ __forceinline__ uint64_t blend_batch(uint32_t lds_addr, int32_t idx0,
         "s_cbranch_scc1 .Lstep_%=\n"                                                                        \
         ".Lend_%=:\n"                                                                                       \
         "s_waitcnt lgkmcnt(0)\n"                                                                            \
-        : [act] "=&s"(act), [live] "=&s"(live), [ctb] "=&s"(ctb), [stp] "=&s"(stp), [sav] "=&s"(sav), \
+        "s_mov_b64 exec, %[ent]\n"                                                                          \
+        : [act] "=&s"(act), [ent] "=&s"(ent), [stp] "=&s"(stp),                                       \
           [idx] "=&s"(idx), [T] "+v"(T), [C0] "+v"(C0), [C1] "+v"(C1), [C2] "+v"(C2), [D] "+v"(D),   \
           [last] "+v"(last)                                                                         \
         : [addr] "v"(lds_addr), [i0] "s"(idx0), [iend] "s"(idx_end), [uu] "v"(uu), [vv] "v"(vv),     \
