@@ -430,6 +430,18 @@ int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_g
                                const tdgs_render_options* opt, const tdgs_render_buffers* buf,
                                int32_t nb_fgaussians);
 
+/* tdgs_backward_project_adam with update_adc_stats_kernel! (training.jl:472-497) folded in:
+ * adc's accumulated 2D mean-gradient norms and contribution counts are updated from grads2d
+ * as tdgs_adc_stats / tdgs_adc_stats_frame (width and height from cam) would, bit for bit,
+ * in the same launch. No reference counterpart as one call: for trainers whose step between
+ * the backward pass and update! is only the statistics (training.jl:221-236, whose
+ * maybe_densify_and_prune! runs the statistics kernel at :313-318 and density control only
+ * every adc_interval iterations). adc->capacity must be at least g->n. */
+int tdgs_backward_project_adam_adc(void* stream, const tdgs_gradients* grads, tdgs_gaussians* g,
+                                   tdgs_adam_state* st, const tdgs_camera* cam,
+                                   const tdgs_render_options* opt, const tdgs_render_buffers* buf,
+                                   int32_t nb_fgaussians, tdgs_adc_buffers* adc);
+
 /* ---- optimiser: update! -------------------------------------------------------------- */
 
 /* update!(opt, fgradients, Val(sh_degree)) (optimizer.jl:964-1009): sparse Adam over the

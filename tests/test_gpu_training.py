@@ -268,7 +268,9 @@ def test_reference_adc_case_on_gpu(gpu):
 def test_backward_project_adam_equals_separate_steps(gpu, cfg, render_deg):
     """tdgs_backward_project_adam (the trainer's fused step) against tdgs_backward_project
     followed by tdgs_adam_step on the same 2D gradients: parameters and moments bit for bit
-    (SH3 float4 items, a render degree below the stored one, SH0)."""
+    (SH3 float4 items, a render degree below the stored one, SH0); and
+    tdgs_backward_project_adam_adc against tdgs_adc_stats before the separate steps: the same,
+    and the density-control accumulators (started from nonzero values) bit for bit."""
     from tdgs_amd import synthetic, training
     w = synthetic.config(cfg, n=20_000 if cfg else None, cameras=2)
     cam = w.cameras[-1]
@@ -276,9 +278,10 @@ def test_backward_project_adam_equals_separate_steps(gpu, cfg, render_deg):
     opts = host.RenderOptions.for_camera(cam, render_deg)
     deg = w.gaussians.sh_degree
     runs = []
+    stats = []
     gen = torch.Generator(device="cuda").manual_seed(5)
     grads2d = None
-    for fused in (False, True):
+    for fused in (False, True, "adc"):
         gd = gpu.TrainableGaussiansVector.from_host(w.gaussians, 0)
         out = gpu.RenderOutputs.for_camera(cam, 0)
         buf = gpu.RenderBuffers(len(gd), t, 0)
@@ -296,9 +299,15 @@ def test_backward_project_adam_equals_separate_steps(gpu, cfg, render_deg):
             gpu.backward_render_tiles_(fg, rgb_grad.contiguous(), out, cam, t, opts, buf)
             grads2d = fg.grads2d[:nbf].clone()
         fg.grads2d[:nbf].copy_(grads2d)
-        if fused:
+        adc = training.AdaptiveDensityControlBuffers(len(gd), 0)
+        adc.accum.copy_(torch.from_numpy(rng.uniform(0, 1e-3, len(gd)).astype(np.float32)))
+        adc.counts.copy_(torch.from_numpy(rng.integers(0, 5, len(gd)).astype(np.int32)))
+        if fused == "adc":
+            opt.backward_project_update_(fg, cam, opts, buf, adc=adc)
+        elif fused:
             opt.backward_project_update_(fg, cam, opts, buf)
         else:
+            training.adc_stats_(adc, fg, buf.fgidx_to_gidx, nbf, cam)
             gpu.check(gpu.lib().tdgs_backward_project(gpu.stream_ptr(0), C.byref(fg.struct()), C.byref(gd.struct()),
                                                       C.byref(cam.to_c()), C.byref(opts.to_c()),
                                                       C.byref(buf.struct()), C.c_int32(nbf)))
@@ -306,10 +315,15 @@ def test_backward_project_adam_equals_separate_steps(gpu, cfg, render_deg):
         torch.cuda.synchronize()
         assert opt.update_count == 8
         runs.append((gd.to_host(), [x.cpu().numpy() for x in (m.means, m.opacity, m.scaling, m.rotation, m.sh)]))
-    (ga, ma), (gb, mb) = runs
-    for x, y in ((ga.means_opacity, gb.means_opacity), (ga.scaling, gb.scaling), (ga.rotation, gb.rotation),
-                 (ga.sh, gb.sh)):
-        np.testing.assert_array_equal(x, y)
-    for x, y in zip(ma, mb):
-        np.testing.assert_array_equal(x, y)
+        stats.append((adc.accum.cpu().numpy(), adc.counts.cpu().numpy()))
+    (ga, ma) = runs[0]
+    for gb, mb in runs[1:]:
+        for x, y in ((ga.means_opacity, gb.means_opacity), (ga.scaling, gb.scaling), (ga.rotation, gb.rotation),
+                     (ga.sh, gb.sh)):
+            np.testing.assert_array_equal(x, y)
+        for x, y in zip(ma, mb):
+            np.testing.assert_array_equal(x, y)
     assert not np.array_equal(ga.means_opacity, w.gaussians.means_opacity)
+    np.testing.assert_array_equal(stats[2][0], stats[0][0])
+    np.testing.assert_array_equal(stats[2][1], stats[0][1])
+    assert (stats[0][1] != stats[1][1]).sum() > 100   # the separate statistics counted Gaussians

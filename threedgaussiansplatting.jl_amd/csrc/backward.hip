@@ -423,6 +423,11 @@ struct BackProjectArgs {
     tdgs_gradients gr;
     Grads2D g2;
     AdamInPlace adam;
+    // or null: update_adc_stats_kernel! folded in (acc[gi] += |dmu| scaled by the half image
+    // extent, cnt[gi] += 1, for each filtered Gaussian with a nonzero 2D mean gradient)
+    float* adc_acc;
+    int32_t* adc_cnt;
+    double adc_sw, adc_sh;
 };
 
 // The SH Adam moments (384 of the 472 bytes of moments per Gaussian at SH3) are read and
@@ -602,6 +607,14 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
     float dcol[3] = {0.0f, 0.0f, 0.0f};
     if (worker) {
         const int64_t gi = s_gi[jl];
+        // the density-control accumulators, read before the projection's work so that their
+        // loads are in flight during it
+        float acc0 = 0.0f;
+        int32_t cnt0 = 0;
+        if (ADAM && a.adc_acc) {
+            acc0 = a.adc_acc[gi];
+            cnt0 = a.adc_cnt[gi];
+        }
         BackwardProjectIn in;
         const float4 mo = reinterpret_cast<const float4*>(a.g.means_opacity)[gi];
         in.m[0] = mo.x; in.m[1] = mo.y; in.m[2] = mo.z;
@@ -619,6 +632,15 @@ __global__ __launch_bounds__(kBpThreads) void k_backward_project(BackProjectArgs
 #pragma unroll
         for (int k = 0; k < 9; ++k) in.g2[k] = *a.g2.at(k, f);
         const BackwardProjectOut o = backward_project(in, a.cam, a.opt);
+        if (ADAM && a.adc_acc) {
+            // (k_adc_stats's operations: the inactive Gaussians' 2D gradients are zero)
+            const float gx = in.g2[0], gy = in.g2[1];
+            if (gx != 0.0f || gy != 0.0f) {
+                const double nrm = sqrt((double)(gx * gx) * a.adc_sw + (double)(gy * gy) * a.adc_sh);
+                a.adc_acc[gi] = (float)((double)acc0 + nrm);
+                a.adc_cnt[gi] = cnt0 + 1;
+            }
+        }
         if (ADAM) {
             adam_geometry(a, gi, o.dm, o.dlogit, o.dlogs, o.dq);
         } else {
@@ -853,14 +875,16 @@ int tdgs_backward_project(void* stream, tdgs_gradients* grads, const tdgs_gaussi
     a.g = *g; a.cam = *cam; a.opt = *opt; a.nbf = nbf; a.frame = frame;
     a.fgidx_to_gidx = buf->fgidx_to_gidx; a.f2d = buf->f2d; a.counts = buf->counts; a.gr = *grads;
     TDGS_TRY(grads2d_view(grads, &a.g2));
+    a.adc_acc = nullptr;
+    a.adc_cnt = nullptr;
     k_backward_project<false><<<(unsigned)ceil_div(nbf, kBpThreads), kBpThreads, 0, s>>>(a);
     TDGS_LAUNCHED();
     return TDGS_OK;
 }
 
-int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_gaussians* g, tdgs_adam_state* st,
-                               const tdgs_camera* cam, const tdgs_render_options* opt,
-                               const tdgs_render_buffers* buf, int32_t nb_fgaussians) {
+static int backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_gaussians* g, tdgs_adam_state* st,
+                                 const tdgs_camera* cam, const tdgs_render_options* opt,
+                                 const tdgs_render_buffers* buf, int32_t nb_fgaussians, tdgs_adc_buffers* adc) {
     TDGS_TRY(check_gaussians(g, true));
     TDGS_TRY(check_options(opt, g->sh_degree));
     int64_t nbf;
@@ -891,11 +915,30 @@ int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_g
         d.bc1 = (float)(1.0 - pow((double)st->beta1, tt));
         d.bc2 = (float)(1.0 - pow((double)st->beta2, tt));
         d.eps = st->epsilon;
+        a.adc_acc = adc ? adc->accum_grad_norms : nullptr;
+        a.adc_cnt = adc ? adc->contribution_counts : nullptr;
+        a.adc_sw = (double)cam->width * cam->width / 4.0;
+        a.adc_sh = (double)cam->height * cam->height / 4.0;
         k_backward_project<true><<<(unsigned)ceil_div(nbf, kBpThreads), kBpThreads, 0, s>>>(a);
         TDGS_LAUNCHED();
     }
     st->update_count += 1;
     return TDGS_OK;
+}
+
+int tdgs_backward_project_adam(void* stream, const tdgs_gradients* grads, tdgs_gaussians* g, tdgs_adam_state* st,
+                               const tdgs_camera* cam, const tdgs_render_options* opt,
+                               const tdgs_render_buffers* buf, int32_t nb_fgaussians) {
+    return backward_project_adam(stream, grads, g, st, cam, opt, buf, nb_fgaussians, nullptr);
+}
+
+int tdgs_backward_project_adam_adc(void* stream, const tdgs_gradients* grads, tdgs_gaussians* g,
+                                   tdgs_adam_state* st, const tdgs_camera* cam, const tdgs_render_options* opt,
+                                   const tdgs_render_buffers* buf, int32_t nb_fgaussians, tdgs_adc_buffers* adc) {
+    TDGS_REQUIRE(adc && adc->accum_grad_norms && adc->contribution_counts, "null ADC arrays");
+    TDGS_REQUIRE(g && adc->capacity >= g->n, "ADC buffers hold %d Gaussians, need %d", adc ? adc->capacity : 0,
+                 g ? g->n : 0);
+    return backward_project_adam(stream, grads, g, st, cam, opt, buf, nb_fgaussians, adc);
 }
 
 int tdgs_backward(void* stream, tdgs_gradients* grads, const float* rgb_grad, const tdgs_render_outputs* out,

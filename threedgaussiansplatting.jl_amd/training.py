@@ -132,16 +132,22 @@ class AdamOptimizer:
         return s
 
     def backward_project_update_(self, fgradients: FilteredGaussiansGradientsVector, camera, options,
-                                 buffers):
+                                 buffers, adc=None):
         """The backward projection with update! applied in place of the 3D gradients
         (tdgs_backward_project_adam); the same parameters and moments as backward_project
-        followed by update_, bit for bit. fgradients.grads2d must hold the 2D gradients."""
+        followed by update_, bit for bit. fgradients.grads2d must hold the 2D gradients. With
+        adc (an AdaptiveDensityControlBuffers), the density-control statistics of the same
+        gradients are accumulated in the same launch, as adc_stats_ would
+        (tdgs_backward_project_adam_adc)."""
         g = self.gaussians
         st = self.struct()
-        check(lib().tdgs_backward_project_adam(stream_ptr(g.device.index), C.byref(fgradients.struct()),
-                                               C.byref(g.struct()), C.byref(st), C.byref(camera.to_c()),
-                                               C.byref(options.to_c()), C.byref(buffers.struct()),
-                                               C.c_int32(buffers.nb_fgaussians)))
+        args = (stream_ptr(g.device.index), C.byref(fgradients.struct()), C.byref(g.struct()), C.byref(st),
+                C.byref(camera.to_c()), C.byref(options.to_c()), C.byref(buffers.struct()),
+                C.c_int32(buffers.nb_fgaussians))
+        if adc is None:
+            check(lib().tdgs_backward_project_adam(*args))
+        else:
+            check(lib().tdgs_backward_project_adam_adc(*args, C.byref(adc.struct())))
         self.update_count = st.update_count
         return g
 
@@ -488,12 +494,16 @@ class Trainer:
         self.images.release(k)
         if self.fuse_optimizer and not self.adc_step_due():
             # no density control between the backward pass and update!: the backward
-            # projection applies the optimiser step itself (the 3D gradients are not stored)
+            # projection applies the optimiser step itself (the 3D gradients are not stored),
+            # and accumulates the density-control statistics (maybe_densify_and_prune!'s only
+            # work in such an iteration) in the same launch
             backward_render_tiles_(self.fgradients, self.rgb_image_grad, self.render_outputs, cam, self.tiling,
                                    self.render_options, self.render_buffers)
-            in_adc = self.maybe_densify_and_prune_()
+            stats = self.iteration_nb <= self.options.adc_final_iteration_nb
             self.update_learning_rates_()
-            self.optimizer.backward_project_update_(self.fgradients, cam, self.render_options, self.render_buffers)
+            self.optimizer.backward_project_update_(self.fgradients, cam, self.render_options, self.render_buffers,
+                                                    adc=self.adc if stats else None)
+            in_adc = False
         else:
             backward_(self.fgradients, self.rgb_image_grad, self.render_outputs, self.gaussians, cam, self.tiling,
                       self.render_options, self.render_buffers)
