@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import golden
+from conftest import golden, stacked_faint_gaussians
 from tdgs_amd import host, synthetic
 
 pytestmark = pytest.mark.gpu
@@ -98,6 +98,26 @@ def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact, extra):
     got, ref = _run(gpu, oracle, w.gaussians, cam, t, opts, rand_grad)
     for k in ["grads2d"] + ARRAYS:
         assert rel_l2(got[k], ref[k]) <= REL_L2, (k, rel_l2(got[k], ref[k]))
+
+
+@pytest.mark.parametrize("size,tile", [(8, (8, 8)), (16, (16, 16)), (16, (32, 32))])
+def test_backward_list_lengths_at_group_and_batch_ends(gpu, oracle, size, tile):
+    """One-tile images whose list holds 1 to 5 records, or 1 to 3 records past a full group of
+    four and past a full batch of 64, 256 or 1024 records; no pixel stops early, so the walk
+    back from each pixel's last contributor visits every record."""
+    from tdgs_amd.host import look_at_camera
+    cam = look_at_camera(size, size, 60.0, (0.0, 0.0, -4.0))
+    t = host.Tiling.for_camera(cam, *tile)
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.2, 0.1, 0.3))
+    gen = torch.Generator(device="cuda").manual_seed(5)
+
+    def rand_grad(rgb):
+        return (torch.rand(rgb.shape, generator=gen, device=rgb.device) - 0.5) * 1e-3
+
+    for k in (1, 2, 3, 5, 63, 65, 67, 255, 257, 259, 1023, 1025, 1027):
+        got, ref = _run(gpu, oracle, stacked_faint_gaussians(k), cam, t, opts, rand_grad)
+        for name in ["grads2d"] + ARRAYS:
+            assert rel_l2(got[name], ref[name]) <= REL_L2, (k, name, rel_l2(got[name], ref[name]))
 
 
 def test_backward_tiny_min_alpha_takes_range_checked_path(gpu, oracle):

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import golden
+from conftest import golden, stacked_faint_gaussians
 from tdgs_amd import host, synthetic
 
 pytestmark = pytest.mark.gpu
@@ -116,6 +116,26 @@ def test_render_odd_sizes_and_tiles(gpu, oracle, w, h, tile):
     r = oracle.render(wl.gaussians, cam, t, opts)
     out, buf = _gpu_render(gpu, wl.gaussians, cam, t, opts)
     _assert_forward_equal(r, out, buf)
+
+
+@pytest.mark.parametrize("size,tile", [(8, (8, 8)), (16, (16, 16)), (16, (32, 32))])
+def test_render_list_lengths_at_group_and_batch_ends(gpu, oracle, size, tile):
+    """One-tile images whose list holds 1 to 5 records, or 1 to 3 records past a full group of
+    four and past a full batch (64, 256 and 1024 records: one per thread of 8x8, 16x16 and 32x32
+    tiles; the 32x32 tile lies mostly outside its 16 x 16 image). No pixel stops early and the
+    list's last record contributes, so every record is stepped, including the padding after
+    the list's last group."""
+    from tdgs_amd.host import look_at_camera
+    cam = look_at_camera(size, size, 60.0, (0.0, 0.0, -4.0))
+    t = host.Tiling.for_camera(cam, *tile)
+    assert t.nb_tiles == 1
+    opts = host.RenderOptions.for_camera(cam, 0, background_color=(0.1, 0.2, 0.3))
+    for k in (1, 2, 3, 4, 5, 63, 64, 65, 66, 67, 255, 256, 257, 258, 259, 1023, 1024, 1025, 1026, 1027):
+        g = stacked_faint_gaussians(k)
+        r = oracle.render(g, cam, t, opts)
+        assert r["nb_keys"] == k and r["last"].max() == k and r["T"].min() > 1e-3, k
+        out, buf = _gpu_render(gpu, g, cam, t, opts)
+        _assert_forward_equal(r, out, buf)
 
 
 @pytest.mark.parametrize("width", [2040, 2048])
