@@ -104,6 +104,21 @@ def test_render_synthetic_bit_exact(gpu, oracle, cfg, n, tile):
     _assert_forward_equal(r, out, buf)
 
 
+@pytest.mark.parametrize("deg", [0, 1, 2])
+def test_render_sh3_storage_at_lower_degrees(gpu, oracle, deg):
+    """16-coefficient storage rendered at SH degrees 0-2 (training's degree schedule): the
+    colours use only the first (deg + 1)^2 coefficients of each channel."""
+    w = synthetic.config(1, n=20_000, cameras=2)
+    assert w.gaussians.sh_degree == 3
+    cam = w.cameras[-1]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, deg, background_color=(0.1, 0.2, 0.3))
+    r = oracle.render(w.gaussians, cam, t, opts)
+    out, buf = _gpu_render(gpu, w.gaussians, cam, t, opts)
+    assert r["nb_keys"] > 1000
+    _assert_forward_equal(r, out, buf)
+
+
 @pytest.mark.parametrize("w,h,tile", [(37, 23, (32, 32)), (301, 173, (8, 8)), (64, 64, (64, 16)), (1, 1, (16, 16))])
 def test_render_odd_sizes_and_tiles(gpu, oracle, w, h, tile):
     """Partial tiles at the right and bottom edges, 1024-thread (32x32) and 64-pixel tiles,
