@@ -99,10 +99,13 @@ def test_device_counts_key_overflow(gpu):
     opt.backward_project_update_(fg, cam, opts, buf)
     adc = training.AdaptiveDensityControlBuffers(len(g), 0)
     training.adc_stats_(adc, fg, buf.fgidx_to_gidx, -1, cam, buf)
+    adc_fused = training.AdaptiveDensityControlBuffers(len(g), 0)   # (tdgs_backward_project_adam_adc)
+    opt.backward_project_update_(fg, cam, opts, buf, adc=adc_fused)
     torch.cuda.synchronize()
     for a, b in zip(p0, (g.means_opacity, g.scaling, g.rotation, g.sh, opt.moments.sh)):
         assert torch.equal(a, b)
-    assert int(adc.counts.sum()) == 0 and float(adc.accum.abs().sum()) == 0.0
+    for st in (adc, adc_fused):
+        assert int(st.counts.sum()) == 0 and float(st.accum.abs().sum()) == 0.0
 
 
 def test_device_counts_nothing_visible(gpu):
@@ -209,6 +212,16 @@ def test_trainer_reruns_overflowing_step_and_grows_keys(gpu):
         a = getattr(tr.gaussians, name).double()
         b = getattr(ref.gaussians, name).double()
         assert float((a - b).norm()) <= 3e-4 * float(b.norm()), name
+    # the density-control statistics (accumulated inside the fused backward projection + Adam
+    # in these steps) count the replayed step once: the left-undone launch added nothing (a
+    # second count would change every Gaussian seen in that step; the two trainers' slightly
+    # different parameters may move a few across a visibility boundary)
+    assert tr.fuse_optimizer and tr.iteration_nb <= tr.options.adc_final_iteration_nb
+    seen = int((ref.adc.counts > 0).sum())
+    assert seen > 1000
+    assert int((tr.adc.counts != ref.adc.counts).sum()) <= max(2, seen // 1000)
+    a, b = tr.adc.accum.double(), ref.adc.accum.double()
+    assert float((a - b).norm()) <= 1e-3 * float(b.norm())
 
 
 @pytest.mark.parametrize("device_counts", [False, True])
