@@ -655,15 +655,22 @@ MEASURED_KERNELS = {
 }
 
 
-def cold_stages(core, out, g, cams, tiling, opts, buf, frames):
-    """Stage times with the caches flushed before every frame: 1 GiB written (more than the
-    256 MB infinity cache and the 8 x 4 MB L2) between frames, outside the profiled stages."""
+def cold_stages(core, out, g, cams, tiling, opts, buf, frames, write=False):
+    """Stage times with the caches flushed before every frame, outside the profiled stages:
+    1 GiB (more than the 256 MB Infinity Cache and the 8 x 4 MB L2) read between frames, so
+    the frame's data is not resident and the caches hold clean lines. write=True flushes by
+    writing the 1 GiB instead: the caches then hold the flush's dirty lines, whose write-back
+    the next kernels pay for as they evict them."""
     import torch
-    flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    flush = torch.zeros(1 << 28, dtype=torch.float32, device="cuda")
+    acc = torch.zeros((), dtype=torch.float32, device="cuda")
     L = core.lib()
     core.check(L.tdgs_profile_begin(C.c_int32(16 * frames + 64)))
     for k in range(frames):
-        flush.fill_(float(k))
+        if write:
+            flush.fill_(float(k))
+        else:
+            acc += flush.sum()
         core.render_(out, g, cams[k % len(cams)], tiling, opts, buf, device_counts=True)
     torch.cuda.synchronize()
     ms = (C.c_double * 13)()
@@ -854,6 +861,7 @@ def main():
     core.check(L.tdgs_profile_end(ms, cnt))
     assert int(mon[2]) == overflows0, "a frame's keys did not fit the key arrays"
     cold_stage_ms = cold_stages(core, out, g, cams, tiling, opts, buf, nextra)
+    cold_dirty_ms = cold_stages(core, out, g, cams, tiling, opts, buf, nextra, write=True)
 
     in_flight = None
     if not args.no_in_flight:
@@ -950,6 +958,7 @@ def main():
                                          tiling.nb_tiles, tiling.end_bit(), evals, evals_back, mc,
                                          cold_ms=cold_stage_ms),
         "stage_ms_cold_cache": {k: round(v, 4) for k, v in cold_stage_ms.items()},
+        "stage_ms_cold_cache_after_1GiB_write": {k: round(v, 4) for k, v in cold_dirty_ms.items()},
         "cpu_baseline": cpu,
         "extra_configs": extra,
     }
