@@ -100,6 +100,27 @@ def test_backward_synthetic(gpu, oracle, cfg, n, tile, exact, extra):
         assert rel_l2(got[k], ref[k]) <= REL_L2, (k, rel_l2(got[k], ref[k]))
 
 
+@pytest.mark.parametrize("deg", [0, 1, 2])
+def test_backward_sh3_storage_at_lower_degrees(gpu, oracle, deg):
+    """16-coefficient storage rendered at SH degrees 0-2 (training's degree schedule): the
+    gradients match the oracle's, and the coefficients above the render degree get exactly 0."""
+    w = synthetic.config(1, n=20_000, cameras=2)
+    cam = w.cameras[-1]
+    t = host.Tiling.for_camera(cam, 16, 16)
+    opts = host.RenderOptions.for_camera(cam, deg, background_color=(0.2, 0.1, 0.3))
+    gen = torch.Generator(device="cuda").manual_seed(13)
+
+    def rand_grad(rgb):
+        return (torch.rand(rgb.shape, generator=gen, device=rgb.device) - 0.5) * 1e-3
+
+    got, ref = _run(gpu, oracle, w.gaussians, cam, t, opts, rand_grad)
+    for k in ["grads2d"] + ARRAYS:
+        assert rel_l2(got[k], ref[k]) <= REL_L2, (k, rel_l2(got[k], ref[k]))
+    hr = (deg + 1) ** 2
+    assert got["sh"].shape[-1] == 16 and np.abs(got["sh"][..., :hr]).max() > 0
+    assert np.all(got["sh"][..., hr:] == 0)
+
+
 @pytest.mark.parametrize("size,tile", [(8, (8, 8)), (16, (16, 16)), (16, (32, 32))])
 def test_backward_list_lengths_at_group_and_batch_ends(gpu, oracle, size, tile):
     """One-tile images whose list holds 1 to 5 records, or 1 to 3 records past a full group of
